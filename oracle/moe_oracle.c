@@ -1,0 +1,581 @@
+/*
+ * moe_oracle.c -- CPU restatement of the MoE operator (TEST INFRASTRUCTURE).
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this
+ * file, always as the checker / the timed CPU baseline, never as a product path.
+ * Compiled with -O2 -ffp-contract=off so every multiply and add rounds on its
+ * own, like the reference's gemm_cpu built by g++ for x86-64 without FMA.
+ *
+ * Pinning (see tests/test_oracle.py):
+ *   codecs        -- exhaustive tables vs torch.float8_e4m3fn / float4_e2m1fn_x2 /
+ *                    float8_e8m0fnu, committed as tests/golden/codecs.npz;
+ *   bf16 RNE      -- vs torch's f32->bf16 cast and the reference bfloat16.cpp
+ *                    compiled into oracle/_ref;
+ *   router logits -- bit-exact vs the reference gemm_cpu<float> (oracle/_ref) and
+ *                    allclose vs torch matmul;
+ *   xo_expf       -- <= 2 ulp vs float64 exp over a dense sweep;
+ *   route/permute -- brute force (numpy argsort/lexsort) + invariants + ties;
+ *   FP8 GEMM path -- vs torch f32 matmul on dequantized operands;
+ *   full layer    -- reductions to the reference mlp(): identical experts give
+ *                    MoE(x) = 2 * mlp(x) with a shared expert of the same weights,
+ *                    and E = 1, k = 1 gives MoE(x) = mlp(x); the gate/up order
+ *                    known answer of tests/ops/test_cpp_mlp.py:129-153.
+ */
+#include "moe_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ---------------------------------------------------------------- codecs */
+
+/* bfloat16.cpp:5-25: add 0x7FFF + lsb to the f32 bits, keep the high half.
+ * No NaN/Inf special case, exactly like the reference. */
+uint16_t xo_bf16_from_f32(float f)
+{
+    uint32_t u = f2u(f);
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7FFFu + lsb;
+    return (uint16_t)(u >> 16);
+}
+
+float xo_f32_from_bf16(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+/* OCP 8-bit floating point spec (E4M3FN): bias 7, no infinities, S.1111.111
+ * is NaN, max normal 448, subnormal step 2^-9. */
+float xo_e4m3_decode(uint8_t b)
+{
+    int s = b >> 7, e = (b >> 3) & 15, m = b & 7;
+    float v;
+    if (e == 15 && m == 7) return NAN;
+    if (e == 0) v = ldexpf((float)m, -9);
+    else v = ldexpf((float)(8 + m), e - 10);
+    return s ? -v : v;
+}
+
+uint8_t xo_e4m3_encode(float f)
+{
+    uint32_t u = f2u(f);
+    uint8_t sign = (uint8_t)((u >> 31) << 7);
+    if (isnan(f)) return 0x7f;
+    float a = fabsf(f);
+    if (a >= 448.0f) return sign | 0x7e;        /* RNE of [448,464] is 448; above saturates */
+    if (a < 0x1p-6f) {                          /* subnormal range (and zero) */
+        float m = rintf(a * 512.0f);            /* exact scale, RNE; m == 8 -> 0x08 = 2^-6 */
+        return sign | (uint8_t)m;
+    }
+    uint32_t ua = f2u(a);
+    uint32_t r = (ua + 0x7FFFFu + ((ua >> 20) & 1u)) >> 20;   /* RNE to 3 mantissa bits */
+    uint32_t code = r - ((127u - 7u) << 3);
+    if (code > 0x7e) code = 0x7e;
+    return sign | (uint8_t)code;
+}
+
+/* OCP MX spec E2M1: bias 1, values 0, .5, 1, 1.5, 2, 3, 4, 6; no NaN/Inf. */
+float xo_e2m1_decode(uint8_t nib)
+{
+    static const float t[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+    float v = t[nib & 7];
+    return (nib & 8) ? -v : v;
+}
+
+uint8_t xo_e2m1_encode(float f)
+{
+    uint32_t u = f2u(f);
+    uint8_t sign = (uint8_t)((u >> 31) << 3);
+    float a = fabsf(f);
+    if (isnan(f)) return sign | 7;              /* no NaN in E2M1: saturate */
+    if (a >= 6.0f) return sign | 7;
+    if (a < 1.0f) return sign | (uint8_t)rintf(a * 2.0f);    /* 0, 0.5, (1.0 -> code 2) */
+    uint32_t ua = f2u(a);
+    uint32_t r = (ua + 0x1FFFFFu + ((ua >> 22) & 1u)) >> 22; /* RNE to 1 mantissa bit */
+    uint32_t code = r - ((127u - 1u) << 1);
+    if (code > 7) code = 7;
+    return sign | (uint8_t)code;
+}
+
+float xo_e8m0_decode(uint8_t b)
+{
+    if (b == 255) return NAN;
+    return ldexpf(1.0f, (int)b - 127);
+}
+
+/* ------------------------------------------------------------ scalar math */
+
+/* exp(x) = 2^n * p(r), n = rint(x / ln2), r = x - n*ln2 with ln2 split in two
+ * (Cody & Waite, "Software Manual for the Elementary Functions", 1980): LN2_HI
+ * is ln2 truncated to 12 significant bits so n*LN2_HI is exact for |n| < 2^12,
+ * LN2_LO = f32(ln2 - LN2_HI).  p is the degree-7 Taylor polynomial of e^r
+ * (coefficients 1/k! rounded to f32), |r| <= ln2/2, truncation error < 6e-9.
+ * Every step is a correctly rounded f32 operation (mul, fma, rint, ldexp), so
+ * the HIP kernels reproduce it bit for bit. */
+float xo_expf(float x)
+{
+    if (x != x) return x;
+    if (x > 88.75f) return INFINITY;
+    if (x < -104.0f) return 0.0f;
+    float n = rintf(x * 0x1.715476p+0f);
+    float r = fmaf(-n, 0x1.62ep-1f, x);
+    r = fmaf(-n, 0x1.0bfbe8p-15f, r);
+    float p = 0x1.a01a02p-13f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0x1.0p-1f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+/* mlp.cpp:10-21: never evaluates exp of a positive argument. */
+float xo_sigmoid(float x)
+{
+    if (x >= 0.0f) return 1.0f / (1.0f + xo_expf(-x));
+    float e = xo_expf(x);
+    return e / (1.0f + e);
+}
+
+float xo_silu(float x) { return x * xo_sigmoid(x); }   /* mlp.cpp:23-26 */
+
+/* -------------------------------------------------------------- quantizers */
+
+static void quant_group_fp8(const float *v, int64_t n, uint8_t *q, float *s)
+{
+    float amax = 0.0f;
+    for (int64_t i = 0; i < n; ++i) { float a = fabsf(v[i]); if (a > amax) amax = a; }
+    if (amax == 0.0f) { *s = 1.0f; memset(q, 0, (size_t)n); return; }
+    float inv = 448.0f / amax;
+    *s = amax / 448.0f;
+    for (int64_t i = 0; i < n; ++i) q[i] = xo_e4m3_encode(v[i] * inv);
+}
+
+void xo_quant_act_fp8(const float *x, int64_t rows, int64_t cols, uint8_t *q, float *s)
+{
+    int64_t G = cols / 128;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t g = 0; g < G; ++g)
+            quant_group_fp8(x + r * cols + g * 128, 128, q + r * cols + g * 128, s + r * G + g);
+}
+
+/* floor(log2(a)) for finite a > 0, exact (frexp: a = m * 2^e, m in [0.5, 1)). */
+static int ilog2f(float a) { int e; frexpf(a, &e); return e - 1; }
+
+static uint8_t mx_scale_byte(float amax, int emax_elem, int *se_out)
+{
+    if (amax == 0.0f) { *se_out = -127; return 0; }
+    int se = ilog2f(amax) - emax_elem;
+    if (se < -127) se = -127;
+    if (se > 127) se = 127;
+    *se_out = se;
+    return (uint8_t)(se + 127);
+}
+
+void xo_quant_act_mxfp8(const float *x, int64_t rows, int64_t cols, uint8_t *q, uint8_t *s)
+{
+    int64_t B = cols / 32;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t b = 0; b < B; ++b) {
+            const float *v = x + r * cols + b * 32;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; ++i) { float a = fabsf(v[i]); if (a > amax) amax = a; }
+            int se;
+            s[r * B + b] = mx_scale_byte(amax, 8, &se);
+            for (int i = 0; i < 32; ++i) q[r * cols + b * 32 + i] = xo_e4m3_encode(ldexpf(v[i], -se));
+        }
+}
+
+void xo_quant_weight_fp8_block(const float *w, int64_t n, int64_t k, uint8_t *q, float *s)
+{
+    int64_t NB = n / 128, KB = k / 128;
+    for (int64_t nb = 0; nb < NB; ++nb)
+        for (int64_t kb = 0; kb < KB; ++kb) {
+            float amax = 0.0f;
+            for (int64_t r = 0; r < 128; ++r)
+                for (int64_t c = 0; c < 128; ++c) {
+                    float a = fabsf(w[(nb * 128 + r) * k + kb * 128 + c]);
+                    if (a > amax) amax = a;
+                }
+            float inv = amax == 0.0f ? 0.0f : 448.0f / amax;
+            s[nb * KB + kb] = amax == 0.0f ? 1.0f : amax / 448.0f;
+            for (int64_t r = 0; r < 128; ++r)
+                for (int64_t c = 0; c < 128; ++c) {
+                    int64_t o = (nb * 128 + r) * k + kb * 128 + c;
+                    q[o] = xo_e4m3_encode(w[o] * inv);
+                }
+        }
+}
+
+void xo_quant_weight_mxfp4(const float *w, int64_t n, int64_t k, uint8_t *q, uint8_t *s)
+{
+    int64_t B = k / 32;
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t b = 0; b < B; ++b) {
+            const float *v = w + r * k + b * 32;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; ++i) { float a = fabsf(v[i]); if (a > amax) amax = a; }
+            int se;
+            s[r * B + b] = mx_scale_byte(amax, 2, &se);
+            for (int i = 0; i < 32; i += 2) {
+                uint8_t lo = xo_e2m1_encode(ldexpf(v[i], -se));
+                uint8_t hi = xo_e2m1_encode(ldexpf(v[i + 1], -se));
+                q[r * (k / 2) + (b * 32 + i) / 2] = (uint8_t)(lo | (hi << 4));
+            }
+        }
+}
+
+/* ------------------------------------------------------------------ router */
+
+static inline float ld(const void *p, int is_bf16, int64_t i)
+{
+    return is_bf16 ? xo_f32_from_bf16(((const uint16_t *)p)[i]) : ((const float *)p)[i];
+}
+
+/* gemm.h:57-83 (transB = true): for each row i, temp[j] += s * B[kk + j*ldb]
+ * over kk ascending -- per output a sequential k-sum of separately rounded
+ * products.  Evaluated here as a contiguous dot product per (i, j): same
+ * operations in the same order, so the same bits. */
+void xo_router_logits(const void *x, const void *wr, int is_bf16, int64_t T, int64_t E,
+                      int64_t H, float *logits)
+{
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t e = 0; e < E; ++e) {
+            float acc = 0.0f;
+            for (int64_t kk = 0; kk < H; ++kk) acc += ld(x, is_bf16, t * H + kk) * ld(wr, is_bf16, e * H + kk);
+            logits[t * E + e] = acc;
+        }
+}
+
+void xo_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,
+              int64_t n_group, int64_t topk_group, int renormalize, float scaling,
+              int32_t *idx, float *w)
+{
+    float *s = (float *)malloc(sizeof(float) * (size_t)E);
+    float *key = (float *)malloc(sizeof(float) * (size_t)E);
+    unsigned char *allowed = (unsigned char *)malloc((size_t)E);
+    unsigned char *taken = (unsigned char *)malloc((size_t)E);
+    for (int64_t t = 0; t < T; ++t) {
+        for (int64_t e = 0; e < E; ++e) {
+            s[e] = xo_sigmoid(logits[t * E + e]);
+            key[e] = bias ? s[e] + bias[e] : s[e];
+            allowed[e] = 1;
+            taken[e] = 0;
+        }
+        if (n_group > 1) {
+            int64_t gs = E / n_group;
+            float gscore[64];
+            unsigned char gkeep[64];
+            for (int64_t g = 0; g < n_group; ++g) {
+                float b1 = -INFINITY, b2 = -INFINITY;
+                for (int64_t e = g * gs; e < (g + 1) * gs; ++e) {
+                    if (key[e] > b1) { b2 = b1; b1 = key[e]; }
+                    else if (key[e] > b2) b2 = key[e];
+                }
+                gscore[g] = b1 + b2;
+                gkeep[g] = 0;
+            }
+            for (int64_t r = 0; r < topk_group; ++r) {
+                int64_t best = -1;
+                for (int64_t g = 0; g < n_group; ++g)
+                    if (!gkeep[g] && (best < 0 || gscore[g] > gscore[best])) best = g;
+                gkeep[best] = 1;
+            }
+            for (int64_t e = 0; e < E; ++e) allowed[e] = gkeep[e / gs];
+        }
+        float denom = 0.0f;
+        for (int64_t j = 0; j < k; ++j) {
+            int64_t best = -1;
+            for (int64_t e = 0; e < E; ++e)
+                if (allowed[e] && !taken[e] && (best < 0 || key[e] > key[best])) best = e;
+            taken[best] = 1;
+            idx[t * k + j] = (int32_t)best;
+            w[t * k + j] = s[best];
+            denom += s[best];
+        }
+        for (int64_t j = 0; j < k; ++j) {
+            float v = w[t * k + j];
+            w[t * k + j] = renormalize ? (v / denom) * scaling : v * scaling;
+        }
+    }
+    free(s); free(key); free(allowed); free(taken);
+}
+
+void xo_permute(const int32_t *idx, int64_t T, int64_t E, int64_t k, int32_t *counts,
+                int32_t *offsets, int32_t *perm, int32_t *inv)
+{
+    int64_t S = T * k;
+    int32_t *cursor = (int32_t *)calloc((size_t)E, sizeof(int32_t));
+    for (int64_t e = 0; e < E; ++e) counts[e] = 0;
+    for (int64_t i = 0; i < S; ++i) counts[idx[i]]++;
+    offsets[0] = 0;
+    for (int64_t e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + counts[e];
+    for (int64_t i = 0; i < S; ++i) {
+        int32_t e = idx[i];
+        int32_t pos = offsets[e] + cursor[e]++;
+        perm[pos] = (int32_t)i;
+        inv[i] = pos;
+    }
+    free(cursor);
+}
+
+/* --------------------------------------------------------------- the layer */
+
+typedef struct {
+    float lut8[256];
+    float lut4[16];
+} luts_t;
+
+static void make_luts(luts_t *L)
+{
+    for (int i = 0; i < 256; ++i) L->lut8[i] = xo_e4m3_decode((uint8_t)i);
+    for (int i = 0; i < 16; ++i) L->lut4[i] = xo_e2m1_decode((uint8_t)i);
+}
+
+/* y[n] = sum_k a[k] * dequant(W[n, k]) for an FP8 128x128 block-scaled W. */
+static void gemv_fp8(const luts_t *L, const float *a, const uint8_t *W, const float *S,
+                     int64_t N, int64_t K, float *y)
+{
+    int64_t KB = K / 128;
+    for (int64_t n = 0; n < N; ++n) {
+        const uint8_t *wr = W + n * K;
+        const float *sr = S + (n / 128) * KB;
+        float acc = 0.0f;
+        for (int64_t kk = 0; kk < K; ++kk) acc += a[kk] * (L->lut8[wr[kk]] * sr[kk / 128]);
+        y[n] = acc;
+    }
+}
+
+/* y[n] = sum_k a[k] * dequant(W[n, k]) for an MXFP4 W (e8m0 per 32 along k). */
+static void gemv_fp4(const luts_t *L, const float *a, const uint8_t *W, const uint8_t *S,
+                     int64_t N, int64_t K, float *y)
+{
+    for (int64_t n = 0; n < N; ++n) {
+        const uint8_t *wr = W + n * (K / 2);
+        const uint8_t *sr = S + n * (K / 32);
+        float acc = 0.0f;
+        for (int64_t kk = 0; kk < K; ++kk) {
+            uint8_t byte = wr[kk >> 1];
+            uint8_t nib = (kk & 1) ? (byte >> 4) : (byte & 15);
+            acc += a[kk] * (L->lut4[nib] * xo_e8m0_decode(sr[kk / 32]));
+        }
+        y[n] = acc;
+    }
+}
+
+/* One expert on one token.  mx = 1: MXFP8 activations + MXFP4 weights;
+ * mx = 0: FP8 1x128 activations + FP8 128x128 weights.  aq/as: the token's
+ * quantized activation row.  tmp: scratch of 2I + I + I floats + I bytes. */
+static void expert_row(const luts_t *L, int mx, const uint8_t *aq, const void *as, int64_t H,
+                       int64_t I, const uint8_t *w13, const void *s13, const uint8_t *w2,
+                       const void *s2, float *tmp, uint8_t *qtmp, float *y)
+{
+    float *a = tmp;              /* [H]  */
+    float *gu = a + H;           /* [2I] */
+    float *act = gu + 2 * I;     /* [I]  */
+    float *a2 = act + I;         /* [I]  */
+    if (mx) {
+        const uint8_t *se = (const uint8_t *)as;
+        for (int64_t kk = 0; kk < H; ++kk) a[kk] = L->lut8[aq[kk]] * xo_e8m0_decode(se[kk / 32]);
+        gemv_fp4(L, a, w13, (const uint8_t *)s13, 2 * I, H, gu);
+    } else {
+        const float *sf = (const float *)as;
+        for (int64_t kk = 0; kk < H; ++kk) a[kk] = L->lut8[aq[kk]] * sf[kk / 128];
+        gemv_fp8(L, a, w13, (const float *)s13, 2 * I, H, gu);
+    }
+    /* mlp.cpp:28-45: silu(gate) * up in f32, gate = first half, up = second */
+    for (int64_t i = 0; i < I; ++i) act[i] = xo_silu(gu[i]) * gu[I + i];
+    if (mx) {
+        uint8_t se[1024];
+        xo_quant_act_mxfp8(act, 1, I, qtmp, se);
+        for (int64_t i = 0; i < I; ++i) a2[i] = L->lut8[qtmp[i]] * xo_e8m0_decode(se[i / 32]);
+        gemv_fp4(L, a2, w2, (const uint8_t *)s2, H, I, y);
+    } else {
+        float sf[1024];
+        xo_quant_act_fp8(act, 1, I, qtmp, sf);
+        for (int64_t i = 0; i < I; ++i) a2[i] = L->lut8[qtmp[i]] * sf[i / 128];
+        gemv_fp8(L, a2, w2, (const float *)s2, H, I, y);
+    }
+}
+
+int xo_moe_forward(const xo_moe_cfg *c, const xo_moe_inputs *in, xo_moe_outputs *o)
+{
+    const int64_t T = c->T, H = c->H, I = c->I, E = c->E, k = c->k, S = T * k;
+    if (H % 128 || I % 128 || I > 131072 / 4 || k < 1 || k > E) return -1;
+    luts_t L;
+    make_luts(&L);
+
+    float *logits = o->logits ? o->logits : (float *)malloc(sizeof(float) * (size_t)(T * E));
+    int32_t *idx = o->idx ? o->idx : (int32_t *)malloc(sizeof(int32_t) * (size_t)S);
+    float *w = o->w ? o->w : (float *)malloc(sizeof(float) * (size_t)S);
+    int32_t *counts = o->counts ? o->counts : (int32_t *)malloc(sizeof(int32_t) * (size_t)E);
+    int32_t *offsets = o->offsets ? o->offsets : (int32_t *)malloc(sizeof(int32_t) * (size_t)(E + 1));
+    int32_t *perm = o->perm ? o->perm : (int32_t *)malloc(sizeof(int32_t) * (size_t)S);
+    int32_t *inv = o->inv ? o->inv : (int32_t *)malloc(sizeof(int32_t) * (size_t)S);
+    float *acc = o->out_f32 ? o->out_f32 : (float *)malloc(sizeof(float) * (size_t)(T * H));
+
+    if (in->logits_in) memcpy(logits, in->logits_in, sizeof(float) * (size_t)(T * E));
+    else xo_router_logits(in->x, in->router_w, c->x_is_bf16, T, E, H, logits);
+    xo_route(logits, in->router_bias, T, E, k, c->n_group, c->topk_group, c->renormalize,
+             c->scaling, idx, w);
+    xo_permute(idx, T, E, k, counts, offsets, perm, inv);
+
+    /* activations: FP8 1x128 for FP8 experts (routed and shared), MXFP8 for FP4 experts */
+    float *xf = (float *)malloc(sizeof(float) * (size_t)(T * H));
+    for (int64_t i = 0; i < T * H; ++i) xf[i] = ld(in->x, c->x_is_bf16, i);
+    uint8_t *xq = (uint8_t *)malloc((size_t)(T * H));
+    float *xs = (float *)malloc(sizeof(float) * (size_t)(T * (H / 128)));
+    xo_quant_act_fp8(xf, T, H, xq, xs);
+    uint8_t *mq = NULL, *ms = NULL;
+    if (c->routed_fp4) {
+        mq = (uint8_t *)malloc((size_t)(T * H));
+        ms = (uint8_t *)malloc((size_t)(T * (H / 32)));
+        xo_quant_act_mxfp8(xf, T, H, mq, ms);
+    }
+
+    /* per-slot expert outputs, computed independently (parallel-safe) */
+    int64_t R = S + (c->has_shared ? T : 0);
+    float *ys = (float *)malloc(sizeof(float) * (size_t)(R * H));
+    int nth = c->nthreads > 0 ? c->nthreads : 1;
+    (void)nth;
+#pragma omp parallel num_threads(nth)
+    {
+        float *tmp = (float *)malloc(sizeof(float) * (size_t)(H + 4 * I));
+        uint8_t *qtmp = (uint8_t *)malloc((size_t)I);
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t r = 0; r < R; ++r) {
+            if (r < S) {
+                int64_t t = r / k;
+                int64_t e = idx[r];
+                if (c->routed_fp4) {
+                    expert_row(&L, 1, mq + t * H, ms + t * (H / 32), H, I,
+                               in->w13 + e * (2 * I) * (H / 2),
+                               (const uint8_t *)in->s13 + e * (2 * I) * (H / 32),
+                               in->w2 + e * H * (I / 2),
+                               (const uint8_t *)in->s2 + e * H * (I / 32), tmp, qtmp, ys + r * H);
+                } else {
+                    expert_row(&L, 0, xq + t * H, xs + t * (H / 128), H, I,
+                               in->w13 + e * (2 * I) * H,
+                               (const float *)in->s13 + e * (2 * I / 128) * (H / 128),
+                               in->w2 + e * H * I,
+                               (const float *)in->s2 + e * (H / 128) * (I / 128), tmp, qtmp,
+                               ys + r * H);
+                }
+            } else {
+                int64_t t = r - S;
+                expert_row(&L, 0, xq + t * H, xs + t * (H / 128), H, I, in->sw13, in->ss13,
+                           in->sw2, in->ss2, tmp, qtmp, ys + r * H);
+            }
+        }
+        free(tmp);
+        free(qtmp);
+    }
+
+    /* combine: shared first, then the k routed slots in order; f32; one cast */
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t h = 0; h < H; ++h) {
+            float a = c->has_shared ? ys[(S + t) * H + h] : 0.0f;
+            for (int64_t j = 0; j < k; ++j) a = a + w[t * k + j] * ys[(t * k + j) * H + h];
+            acc[t * H + h] = a;
+        }
+    if (c->x_is_bf16) {
+        uint16_t *ob = (uint16_t *)o->out;
+        for (int64_t i = 0; i < T * H; ++i) ob[i] = xo_bf16_from_f32(acc[i]);
+    } else {
+        memcpy(o->out, acc, sizeof(float) * (size_t)(T * H));
+    }
+
+    free(xf); free(xq); free(xs); free(mq); free(ms); free(ys);
+    if (!o->logits) free(logits);
+    if (!o->idx) free(idx);
+    if (!o->w) free(w);
+    if (!o->counts) free(counts);
+    if (!o->offsets) free(offsets);
+    if (!o->perm) free(perm);
+    if (!o->inv) free(inv);
+    if (!o->out_f32) free(acc);
+    return 0;
+}
+
+/* ------------------------------------------------- reference-path f32 layer */
+
+/* gemm.h:57-83 with transB = true, verbatim loop order: i -> kk -> j with an f32
+ * row accumulator and strided B reads B[kk + j*ldb]. */
+static void gemm_cpu_tb(const float *A, const float *B, float *C, int64_t m, int64_t K,
+                        int64_t n, float *temp)
+{
+    for (int64_t i = 0; i < m; ++i) {
+        for (int64_t j = 0; j < n; ++j) temp[j] = 0.0f;
+        for (int64_t kk = 0; kk < K; ++kk) {
+            float s = A[i * K + kk];
+            for (int64_t j = 0; j < n; ++j) temp[j] += s * B[kk + j * K];
+        }
+        for (int64_t j = 0; j < n; ++j) C[i * n + j] = temp[j];
+    }
+}
+
+/* mlp.cpp:10-26 exactly as the reference evaluates it (libm expf), used by the
+ * reference-path layer so that E = 1, k = 1 reproduces mlp() bit for bit. */
+static float sigmoid_libm(float x)
+{
+    if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
+    return expf(x) / (1.0f + expf(x));
+}
+
+/* mlp() CPU branch (mlp.cpp:71-83): linear(x, gate_up) -> helper (silu*up) ->
+ * linear(act, down), f32 throughout. */
+static void mlp_f32(const float *x, int64_t m, const float *w13, const float *w2, int64_t H,
+                    int64_t I, float *y, float *gu, float *act, float *temp)
+{
+    gemm_cpu_tb(x, w13, gu, m, H, 2 * I, temp);
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < I; ++j)
+            { float g = gu[i * 2 * I + j]; act[i * I + j] = (g * sigmoid_libm(g)) * gu[i * 2 * I + j + I]; }
+    gemm_cpu_tb(act, w2, y, m, I, H, temp);
+}
+
+void xo_moe_ref_f32(const float *x, const float *router_w, const float *router_bias,
+                    const float *w13, const float *w2, const float *sw13, const float *sw2,
+                    int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int renormalize,
+                    float scaling, int64_t t0, int64_t t1, float *out)
+{
+    (void)T;
+    int64_t m = t1 - t0;
+    const float *xs = x + t0 * H;
+    int64_t maxn = 2 * I > H ? 2 * I : H;
+    if (E > maxn) maxn = E;
+    float *temp = (float *)malloc(sizeof(float) * (size_t)maxn);
+    float *logits = (float *)malloc(sizeof(float) * (size_t)(m * E));
+    int32_t *idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)(m * k));
+    float *w = (float *)malloc(sizeof(float) * (size_t)(m * k));
+    gemm_cpu_tb(xs, router_w, logits, m, H, E, temp);
+    xo_route(logits, router_bias, m, E, k, 1, 1, renormalize, scaling, idx, w);
+
+    float *gu = (float *)malloc(sizeof(float) * (size_t)(m * 2 * I));
+    float *act = (float *)malloc(sizeof(float) * (size_t)(m * I));
+    float *y = (float *)malloc(sizeof(float) * (size_t)(m * H));
+    float *xe = (float *)malloc(sizeof(float) * (size_t)(m * H));
+    int64_t *rows = (int64_t *)malloc(sizeof(int64_t) * (size_t)m);
+    float *rw = (float *)malloc(sizeof(float) * (size_t)m);
+
+    if (sw13) mlp_f32(xs, m, sw13, sw2, H, I, out, gu, act, temp);
+    else memset(out, 0, sizeof(float) * (size_t)(m * H));
+    for (int64_t e = 0; e < E; ++e) {
+        int64_t me = 0;
+        for (int64_t i = 0; i < m; ++i)
+            for (int64_t j = 0; j < k; ++j)
+                if (idx[i * k + j] == e) { rows[me] = i; rw[me] = w[i * k + j]; ++me; }
+        if (!me) continue;
+        for (int64_t r = 0; r < me; ++r) memcpy(xe + r * H, xs + rows[r] * H, sizeof(float) * (size_t)H);
+        mlp_f32(xe, me, w13 + e * 2 * I * H, w2 + e * H * I, H, I, y, gu, act, temp);
+        for (int64_t r = 0; r < me; ++r)
+            for (int64_t h = 0; h < H; ++h) out[rows[r] * H + h] += rw[r] * y[r * H + h];
+    }
+    free(temp); free(logits); free(idx); free(w); free(gu); free(act); free(y); free(xe);
+    free(rows); free(rw);
+}
