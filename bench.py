@@ -1,0 +1,229 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X MoE operator (one GPU).
+
+Workload (the configuration the headline metric is
+quoted on): one V4-Flash MoE layer forward at prefill, 8192 bf16 tokens,
+hidden 4096, 256 routed experts top-6 + 1 shared, intermediate 2048, FP8 e4m3
+weights with 128x128 block scales, sigmoid router with bias ~ N(0, 0.1) and
+Zipf(1.1)-skewed popularity.  A step = one full layer forward (router, top-k,
+permute, gate_up GEMM + SwiGLU, down GEMM, combine) with inputs resident in
+HBM.  The same JSON line also carries the decode configuration (configs[3]:
+T in {1, 16, 64, 256}, uniform routing, HBM GB/s), the single FP8 GEMM
+(configs[1]) and the MXFP4 layer.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "xstar-infer_amd")
+sys.path.insert(0, PKG)
+sys.path.insert(0, ROOT)
+
+H, I, E, K_TOP = 4096, 2048, 256, 6
+PEAK_FP8_TFLOPS = 5000.0      # MI355X dense FP8 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+METRIC = "MoE-layer tokens/s + TFLOP/s (% FP8 MFMA peak) and decode HBM GB/s, hid4096"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_forward(layer, x, steps, warmup, profile=False):
+    import torch
+    import xs_moe_capi as X
+    out = torch.empty_like(x)
+    for _ in range(warmup):
+        layer.forward(x, out=out)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        layer.forward(x, out=out)
+    e1.record(st)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    stages = None
+    if profile:
+        # second pass with per-stage HIP events recorded by the library on its stream
+        X.profile_enable(True)
+        for _ in range(steps):
+            layer.forward(x, out=out)
+        torch.cuda.synchronize()
+        tot, n = X.profile_read()
+        X.profile_enable(False)
+        stages = {kk: v / max(n, 1) for kk, v in tot.items()}
+    return ms, stages
+
+
+def routed_expert_count(layer, x):
+    import torch
+    T = x.shape[0]
+    dbg = dict(counts=torch.empty(layer.E, dtype=torch.int32, device="cuda"))
+    layer.forward(x, debug=dbg)
+    torch.cuda.synchronize()
+    return int((dbg["counts"] > 0).sum().item())
+
+
+def cpu_baseline(g, sample_tokens):
+    """The reference's CPU path restated (oracle.moe_ref_f32: gemm_cpu loop order,
+    f32 mlp per expert, single thread) on the first `sample_tokens` tokens of the
+    workload, with the FP8 weights dequantized to f32 (as a reference user would
+    load them)."""
+    import numpy as np
+    import torch
+    import oracle
+
+    x = g["x"][:sample_tokens].float().cpu().numpy()
+    wr = g["router_w"].float().cpu().numpy()
+    bias = g["bias"].cpu().numpy() if g["bias"] is not None else None
+    logits = oracle.router_logits(x, wr, False)
+    idx, _ = oracle.route(logits, bias, g["k"])
+    touched = sorted(set(idx.ravel().tolist()))
+
+    def deq(q, s):
+        v = q.view(torch.float8_e4m3fn).float()
+        rep = s.repeat_interleave(128, -2).repeat_interleave(128, -1)
+        return (v * rep).cpu().numpy()
+
+    w13 = {e: deq(g["w13"][e], g["s13"][e]) for e in touched}
+    w2 = {e: deq(g["w2"][e], g["s2"][e]) for e in touched}
+    sh = g["shared"]
+    shared = (deq(sh[0], sh[1]), deq(sh[2], sh[3])) if sh is not None else None
+    t0 = time.perf_counter()
+    oracle.moe_ref_f32(x, wr, bias, w13, w2, g["k"], shared=shared)
+    dt = time.perf_counter() - t0
+    return dict(value=sample_tokens / dt, unit="tokens/s", cores=1, kind="port",
+                sample=(f"first {sample_tokens} tokens of the prefill workload, reference-path f32 "
+                        f"(gemm_cpu i->kk->j order, mlp per expert, 1 thread; {len(touched)} experts "
+                        f"+ shared touched); {dt:.2f} s on {os.cpu_count()} visible cores"),
+                seconds=dt)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="prefill only, no extra configs")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=8)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (the MoE operator is built and measured for a "
+              f"single MI355X holding all experts of a layer); --gpus {a.gpus} is not supported.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    import xs_moe_capi as X
+    from moe_synth import synth_layer, layer_from, expert_bytes, layer_flops
+
+    dev_name = torch.cuda.get_device_name(0)
+    log(f"device: {dev_name}")
+    # ---------------- prefill (headline) ----------------
+    T = 8192
+    g = synth_layer(T, H, I, E, K_TOP, seed=0, zipf=1.1)
+    layer = layer_from(g)
+    ms, stages = time_forward(layer, g["x"], a.steps, a.warmup, profile=True)
+    flops = layer_flops(T, H, I, E, K_TOP)
+    ne = routed_expert_count(layer, g["x"])
+    wbytes = (ne + 1) * expert_bytes(H, I, False) + E * H * 2
+    act_bytes = T * H * 2 * 2 + T * H + (T * K_TOP + T) * (I + 2 * H)
+    gu_ms = stages["gemm_gate_up"]
+    gu_flops = (K_TOP + 1) * T * 2 * H * 2 * I
+    achieved = gu_flops / (gu_ms * 1e-3) / 1e12
+    res = {
+        "metric": METRIC,
+        "value": T / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 (bf16 in/out, f32 accumulate)",
+        "data": "synthetic (seeded N(0,1) tokens, N(0,0.02) weights quantized on the GPU)",
+        "config": {"workload": "V4-Flash MoE layer prefill, configs[2]", "tokens": T, "hidden": H,
+                   "moe_intermediate": I, "experts": E, "top_k": K_TOP, "shared_experts": 1,
+                   "weights": "e4m3 128x128 block scales", "routing": "sigmoid+bias, Zipf(1.1)",
+                   "parallelism": "single GPU"},
+        "layer_tflops": flops / (ms * 1e-3) / 1e12,
+        "layer_frac_fp8_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
+        "layer_hbm_gbs": (wbytes + act_bytes) / (ms * 1e-3) / 1e9,
+        "stage_ms": stages,
+        "roofline": {"kernel": "moe_gemm_kernel<gate_up> (grouped FP8 gate_up GEMM + SwiGLU)",
+                     "bound": "mfma", "achieved": achieved, "peak": PEAK_FP8_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP8_TFLOPS, "traffic": None},
+    }
+    del layer
+    if not a.no_cpu:
+        log("cpu baseline ...")
+        cb = cpu_baseline(g, a.cpu_tokens)
+        res["cpu_baseline"] = {kk: cb[kk] for kk in ("value", "unit", "cores", "kind", "sample")}
+    del g
+    torch.cuda.empty_cache()
+
+    if not a.quick:
+        # ---------------- decode (HBM-bound) ----------------
+        dec = {}
+        gd = synth_layer(256, H, I, E, K_TOP, seed=1, bias_std=0.0)
+        for Td in (1, 16, 64, 256):
+            L = layer_from(gd)
+            xd = gd["x"][:Td].contiguous()
+            msd, st = time_forward(L, xd, max(a.steps, 50), a.warmup, profile=True)
+            ned = routed_expert_count(L, xd)
+            by = (ned + 1) * expert_bytes(H, I, False) + E * H * 2 + Td * H * 4
+            dec[str(Td)] = {"ms": msd, "experts_touched": ned + 1, "hbm_gbs": by / (msd * 1e-3) / 1e9,
+                            "frac_hbm_peak": by / (msd * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                            "tokens_per_s": Td / (msd * 1e-3), "stage_ms": st}
+        res["decode"] = dec
+        del gd
+        torch.cuda.empty_cache()
+        # ---------------- single FP8 GEMM ----------------
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(2)
+        A = torch.randn((512, 4096), generator=gen, device="cuda").to(torch.bfloat16)
+        Wt = torch.randn((4096, 4096), generator=gen, device="cuda", dtype=torch.bfloat16) * 0.02
+        bq, bs = X.quant_weight_fp8_block(Wt)
+        C_ = torch.empty((512, 4096), dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(X.lib().xs_gemm_fp8_blockscale_workspace_size(512, 4096), dtype=torch.uint8, device="cuda")
+        for _ in range(a.warmup):
+            X.gemm_fp8_blockscale(A, bq, bs, out=C_, workspace=ws)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        n = 50
+        for _ in range(n):
+            X.gemm_fp8_blockscale(A, bq, bs, out=C_, workspace=ws)
+        e1.record()
+        torch.cuda.synchronize()
+        gms = e0.elapsed_time(e1) / n
+        gfl = 2 * 512 * 4096 * 4096
+        res["gemm_fp8_512x4096x4096"] = {"ms": gms, "tflops": gfl / (gms * 1e-3) / 1e12,
+                                         "frac_fp8_peak": gfl / (gms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS}
+        # ---------------- MXFP4 routed experts ----------------
+        g4 = synth_layer(2048, H, I, E, K_TOP, seed=3, fp4=True)
+        L4 = layer_from(g4)
+        ms4, st4 = time_forward(L4, g4["x"], a.steps, a.warmup, profile=True)
+        ne4 = routed_expert_count(L4, g4["x"])
+        by4 = ne4 * expert_bytes(H, I, True) + expert_bytes(H, I, False) + E * H * 2
+        fl4 = layer_flops(2048, H, I, E, K_TOP)
+        res["fp4_2048"] = {"ms": ms4, "tokens_per_s": 2048 / (ms4 * 1e-3), "tflops": fl4 / (ms4 * 1e-3) / 1e12,
+                           "hbm_gbs_weights": by4 / (ms4 * 1e-3) / 1e9, "stage_ms": st4}
+    print(json.dumps(res))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

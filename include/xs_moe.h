@@ -1,0 +1,203 @@
+/*
+ * xs_moe.h -- C ABI of the MI355X (gfx950) MoE operator library libxs_moe.so.
+ *
+ * Plain C: pointers, sizes, enums.  No torch or HIP types appear in any
+ * signature; a stream is passed as `void *` (a hipStream_t, NULL = the null
+ * stream).  Every entry point returns 0 on success or a non-zero xs_status;
+ * xs_last_error() then holds a message for the calling thread.  The C++ Tensor
+ * layer converts non-zero codes into std::runtime_error, as CHECK_CUDA does in
+ * the reference (xstar_cpp/include/cuda/cuda_check.h:23-31).
+ *
+ * All device pointers must be device-resident (hipMalloc'd or torch CUDA
+ * tensors).  Compute entry points enqueue work on `stream` and return without
+ * synchronising; callers that need results on the host synchronise the stream
+ * (the C++ Tensor ops do, matching the reference's synchronous launchers,
+ * xstar_cpp/src/ops/gemm.cu:238-239).
+ *
+ * Reference interfaces each group replaces are cited per declaration
+ * (paths relative to the reference repository root).
+ */
+#ifndef XS_MOE_H
+#define XS_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    XS_OK = 0,
+    XS_ERR_INVALID = 1,      /* bad argument (shape, dtype, null pointer, alignment) */
+    XS_ERR_HIP = 2,          /* a HIP runtime call or kernel launch failed */
+    XS_ERR_UNSUPPORTED = 3,  /* valid request this build does not implement */
+    XS_ERR_WORKSPACE = 4     /* workspace too small */
+} xs_status;
+
+/* Element types.  The first two values match the reference's DType
+ * (xstar_cpp/include/dtype.h:8-12). */
+typedef enum {
+    XS_F32 = 0,
+    XS_BF16 = 1,
+    XS_FP8_E4M3 = 2,   /* OCP E4M3FN, 1 byte */
+    XS_FP4_E2M1X2 = 3, /* OCP E2M1, two per byte, element 2i in the low nibble */
+    XS_E8M0 = 4,       /* OCP E8M0 scale byte: 2^(b-127) */
+    XS_I32 = 5
+} xs_dtype;
+
+/* Thread-local message of the last failing call on this thread. */
+const char *xs_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * Runtime shim.  Replaces cuda_alloc / cuda_free / cuda_memcpy_h2d / _d2h /
+ * _d2d / cuda_free_bytes (xstar_cpp/include/cuda/cuda_allocator.h:32-69,
+ * xstar_cpp/src/cuda/cuda_allocator.cu:7-45).
+ * ------------------------------------------------------------------------- */
+int xs_device_count(int *count);
+int xs_malloc(void **ptr, size_t bytes);
+int xs_free(void *ptr);
+int xs_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int xs_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int xs_memcpy_d2d(void *dst, const void *src, size_t bytes);
+int xs_free_bytes(size_t *free_bytes);
+int xs_stream_synchronize(void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Stage entry points.  The reference has no MoE code (README.md:28,45); each
+ * stage replaces the op it would otherwise be composed from, noted per entry.
+ * ------------------------------------------------------------------------- */
+
+/* Router logits = x . router_w^T in f32 (replaces linear(x, router_w, nullptr),
+ * xstar_cpp/src/ops/linear.cpp:9-66 over gemm_launch, xstar_cpp/include/ops/gemm.h:165-176).
+ * x [T, H], router_w [E, H], dtype XS_F32 or XS_BF16 (both the same);
+ * logits [T, E] f32.  exact = 1: sequential-k f32 accumulation with separately
+ * rounded products, bit-identical to gemm_cpu (gemm.h:57-83).  exact = 0 (bf16
+ * only): bf16 MFMA with f32 accumulation.  H % 128 == 0. */
+int xs_moe_router_logits(const void *x, const void *router_w, int dtype, int64_t T, int64_t E,
+                         int64_t H, int exact, float *logits, void *stream);
+
+/* Top-k routing (no reference counterpart; contract: sigmoid scores
+ * s = sigmoid(logit) with the branched form of xstar_cpp/src/ops/mlp.cpp:10-21,
+ * selection key s + bias (bias may be NULL), optional group-limited selection
+ * (n_group > 1 keeps the topk_group groups with the largest top-2 key sum),
+ * top-k with ties to the lower expert index, weights s_j / sum(s) * scaling
+ * when renormalize, else s_j * scaling).  logits [T, E] f32, idx [T, k] i32,
+ * w [T, k] f32.  E <= 1024, k <= 16, n_group <= 64. */
+int xs_moe_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,
+                 int64_t n_group, int64_t topk_group, int renormalize, float scaling,
+                 int32_t *idx, float *w, void *stream);
+
+/* Stable counting sort of the T*k slots (slot = t*k + j) by expert.
+ * counts [E], offsets [E+1] (exclusive scan), perm [T*k] (position -> slot),
+ * inv [T*k] (slot -> position).  workspace: xs_moe_permute_workspace_size()
+ * bytes of device memory. */
+size_t xs_moe_permute_workspace_size(int64_t T, int64_t E);
+int xs_moe_permute(const int32_t *idx, int64_t T, int64_t E, int64_t k, int32_t *counts,
+                   int32_t *offsets, int32_t *perm, int32_t *inv, void *workspace,
+                   size_t workspace_bytes, void *stream);
+
+/* Activation quantization (no reference counterpart).
+ * FP8: per (row, 128-column group) scale = amax/448 (amax == 0 -> 1),
+ *      q = e4m3_rne(v * (448/amax)); q [rows, cols] bytes, s [rows, cols/128] f32.
+ * MXFP8 (OCP MX v1.0): per (row, 32-column block) exponent se = floor(log2 amax) - 8,
+ *      q = e4m3_rne_sat(v * 2^-se); s [rows, cols/32] e8m0 bytes.
+ * x dtype XS_F32 or XS_BF16. */
+int xs_quant_act_fp8(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, float *s,
+                     void *stream);
+int xs_quant_act_mxfp8(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q,
+                       uint8_t *s, void *stream);
+
+/* Weight quantization for loading dense checkpoints (no reference counterpart;
+ * the reference loads F32/BF16 only, xstar_cpp/src/weight_io.cpp:122-127).
+ * FP8 128x128 blocks: w [batch, n, k] -> q [batch, n, k], s [batch, n/128, k/128] f32,
+ *   scale = amax/448 over the block (amax == 0 -> 1), q = e4m3_rne(v * 448/amax).
+ * MXFP4: w [batch, n, k] -> q [batch, n, k/2] packed, s [batch, n, k/32] e8m0,
+ *   se = floor(log2 amax) - 2, q = e2m1_rne_sat(v * 2^-se). */
+int xs_quant_weight_fp8_block(const void *w, int dtype, int64_t batch, int64_t n, int64_t k,
+                              uint8_t *q, float *s, void *stream);
+int xs_quant_weight_mxfp4(const void *w, int dtype, int64_t batch, int64_t n, int64_t k,
+                          uint8_t *q, uint8_t *s, void *stream);
+
+/* Single FP8 block-scaled GEMM: C = dequant(A) . dequant(B)^T, bf16 out.
+ * Replaces gemm_launch(C, A, B, nullptr, m, k, n, transB=true, ...)
+ * (xstar_cpp/include/ops/gemm.h:165-176) for FP8 operands.
+ * A [M, K] bf16 activations (quantized per 1x128 inside, workspace holds them),
+ * B [N, K] e4m3 with Bs [N/128, K/128] f32 block scales, C [M, N] bf16.
+ * K % 128 == 0, N % 128 == 0. */
+size_t xs_gemm_fp8_blockscale_workspace_size(int64_t M, int64_t K);
+int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int64_t M,
+                           int64_t N, int64_t K, void *C, void *workspace,
+                           size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * The whole MoE layer.  Replaces mlp(x, gate_up_weight, down_weight)
+ * (xstar_cpp/include/ops/mlp.h:51) at its call sites in transformer_block
+ * (xstar_cpp/src/ops/transformer_block.cpp:75,142,204,353).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    int64_t T;            /* tokens */
+    int64_t H;            /* hidden (multiple of 256) */
+    int64_t I;            /* expert intermediate (multiple of 128) */
+    int64_t E;            /* routed experts (<= 1024) */
+    int64_t top_k;        /* <= 16 */
+    int64_t n_group;      /* 1 = no group-limited routing */
+    int64_t topk_group;
+    int renormalize;      /* 1: w = s / sum(s) */
+    float routed_scaling; /* multiplies the routed weights */
+    int x_dtype;          /* XS_BF16 or XS_F32: x, router_w and out */
+    int routed_format;    /* XS_FP8_E4M3 (128x128 f32 scales) or XS_FP4_E2M1X2 (MXFP4) */
+    int has_shared;       /* 1: shared expert weights present (FP8 128x128) */
+    int router_exact;     /* 1: bit-exact sequential f32 router logits */
+} xs_moe_params;
+
+typedef struct {
+    const void *x;             /* [T, H] x_dtype */
+    const void *router_w;      /* [E, H] x_dtype */
+    const float *router_bias;  /* [E] f32 or NULL */
+    /* routed experts.  FP8: w13 [E, 2I, H] e4m3, w13_scale [E, 2I/128, H/128] f32,
+     *                       w2 [E, H, I] e4m3,   w2_scale [E, H/128, I/128] f32.
+     *                  FP4: w13 [E, 2I, H/2], w13_scale [E, 2I, H/32] e8m0,
+     *                       w2 [E, H, I/2],   w2_scale [E, H, I/32] e8m0.
+     * w13 rows are [gate ; up] (xstar_cpp/include/ops/mlp.h:4-14). */
+    const void *w13; const void *w13_scale;
+    const void *w2;  const void *w2_scale;
+    /* shared expert, FP8 128x128 (E = 1 shapes), or NULL when !has_shared */
+    const void *shared_w13; const float *shared_w13_scale;
+    const void *shared_w2;  const float *shared_w2_scale;
+    void *out;                 /* [T, H] x_dtype */
+    /* optional device outputs for inspection (NULL = not written) */
+    float *logits;             /* [T, E] */
+    int32_t *topk_idx;         /* [T, k] */
+    float *topk_w;             /* [T, k] */
+    int32_t *counts;           /* [E] */
+    int32_t *offsets;          /* [E+1] */
+    int32_t *perm;             /* [T*k] */
+    int32_t *inv;              /* [T*k] */
+} xs_moe_tensors;
+
+/* Device workspace the forward needs for these params (bytes, 256-aligned). */
+size_t xs_moe_workspace_size(const xs_moe_params *p);
+
+/* Router -> top-k -> permute (+ activation quant) -> grouped gate_up GEMM with
+ * SwiGLU and FP8 re-quant -> grouped down GEMM -> weighted combine (+ shared).
+ * Stream-ordered, no host synchronisation inside. */
+int xs_moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *workspace,
+                   size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Per-stage timing hook (no reference counterpart; the reference times ops with
+ * torch.cuda.Event around whole calls, bench/bench_splitkv.py:86-105).  While
+ * enabled, xs_moe_forward records a HIP event at each stage boundary on its
+ * stream (router logits, route, activation quant, permute, gate_up GEMM, down
+ * GEMM, combine).  xs_moe_profile_read waits for the recorded forwards, writes
+ * the summed milliseconds of up to 7 stages and the number of forwards, and
+ * clears the record.  Process-wide state: not for concurrent callers.
+ * ------------------------------------------------------------------------- */
+int xs_moe_profile_enable(int enable);
+int xs_moe_profile_read(float *stage_ms, int n_stages, int *n_calls);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -267,11 +267,12 @@ def moe_forward(x, router_w, router_bias, w13, s13, w2, s2, k, shared=None, rout
 
 def moe_ref_f32(x, router_w, router_bias, w13, w2, k, shared=None, renormalize=True,
                 scaling=1.0, t0=0, t1=None):
-    """Reference-path f32 MoE (the reference's CPU ops composed; single-threaded)."""
+    """Reference-path f32 MoE (the reference's CPU ops composed; single-threaded).
+    w13 / w2: arrays [E, ...] or dicts {expert: array} holding only the experts
+    the tokens route to."""
     x = np.ascontiguousarray(x, np.float32)
     T, H = x.shape
     E = router_w.shape[0]
-    I = w2.shape[-1]
     t1 = T if t1 is None else t1
     out = np.empty((t1 - t0, H), np.float32)
     keep = []
@@ -283,8 +284,18 @@ def moe_ref_f32(x, router_w, router_bias, w13, w2, k, shared=None, renormalize=T
         keep.append(a)
         return a.ctypes.data
 
+    def table(w):
+        tab = (C.c_void_p * E)()
+        for e in range(E):
+            a = w.get(e) if isinstance(w, dict) else w[e]
+            tab[e] = ptr(a)
+        return tab
+
+    any_w2 = next(iter(w2.values())) if isinstance(w2, dict) else w2[0]
+    I = any_w2.shape[-1]
+    t13, t2 = table(w13), table(w2)
     sw13, sw2 = shared if shared is not None else (None, None)
-    lib().xo_moe_ref_f32(ptr(x), ptr(router_w), ptr(router_bias), ptr(w13), ptr(w2), ptr(sw13),
+    lib().xo_moe_ref_f32(ptr(x), ptr(router_w), ptr(router_bias), t13, t2, ptr(sw13),
                          ptr(sw2), T, H, I, E, k, int(renormalize), float(scaling), t0, t1,
                          out.ctypes.data)
     return out

@@ -540,7 +540,7 @@ static void mlp_f32(const float *x, int64_t m, const float *w13, const float *w2
 }
 
 void xo_moe_ref_f32(const float *x, const float *router_w, const float *router_bias,
-                    const float *w13, const float *w2, const float *sw13, const float *sw2,
+                    const float *const *w13_tab, const float *const *w2_tab, const float *sw13, const float *sw2,
                     int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int renormalize,
                     float scaling, int64_t t0, int64_t t1, float *out)
 {
@@ -572,7 +572,8 @@ void xo_moe_ref_f32(const float *x, const float *router_w, const float *router_b
                 if (idx[i * k + j] == e) { rows[me] = i; rw[me] = w[i * k + j]; ++me; }
         if (!me) continue;
         for (int64_t r = 0; r < me; ++r) memcpy(xe + r * H, xs + rows[r] * H, sizeof(float) * (size_t)H);
-        mlp_f32(xe, me, w13 + e * 2 * I * H, w2 + e * H * I, H, I, y, gu, act, temp);
+        if (!w13_tab[e] || !w2_tab[e]) continue;   /* caller guarantees e is not routed to */
+        mlp_f32(xe, me, w13_tab[e], w2_tab[e], H, I, y, gu, act, temp);
         for (int64_t r = 0; r < me; ++r)
             for (int64_t h = 0; h < H; ++h) out[rows[r] * H + h] += rw[r] * y[r * H + h];
     }

@@ -137,14 +137,16 @@ typedef struct {
 int xo_moe_forward(const xo_moe_cfg *cfg, const xo_moe_inputs *in, xo_moe_outputs *out);
 
 /* Reference-path fp32 MoE: the reference's CPU ops composed as a MoE layer.
- * Weights are dense f32 (w13 [E,2I,H], w2 [E,H,I], shared likewise, or NULL);
+ * Weights are dense f32, one pointer per expert (w13_tab[e] -> [2I,H],
+ * w2_tab[e] -> [H,I]; NULL allowed for experts the tokens do not route to;
+ * shared sw13 [2I,H] / sw2 [H,I] or NULL);
  * x f32 [T,H].  Router = linear (gemm_cpu order), route as xo_route, each
  * routed/shared expert = mlp() numerics (gemm_cpu i->kk->j loop with strided
  * transB reads, f32 silu*up), combine in f32.  This is the timed CPU baseline;
  * it runs single-threaded like the reference.  Only tokens [t0, t1) are
  * computed (bounded samples); routing still covers those tokens only. */
 void xo_moe_ref_f32(const float *x, const float *router_w, const float *router_bias,
-                    const float *w13, const float *w2, const float *sw13, const float *sw2,
+                    const float *const *w13_tab, const float *const *w2_tab, const float *sw13, const float *sw2,
                     int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int renormalize,
                     float scaling, int64_t t0, int64_t t1, float *out);
 

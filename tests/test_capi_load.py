@@ -1,0 +1,46 @@
+"""The C-ABI library loads on a machine without a GPU and exports every entry
+point include/xs_moe.h declares (no compute calls here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    src = open(os.path.join(ROOT, "include", "xs_moe.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(xs_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_declares_the_stage_entry_points():
+    names = declared_functions()
+    for n in ("xs_moe_forward", "xs_moe_route", "xs_moe_permute", "xs_moe_router_logits",
+              "xs_quant_act_fp8", "xs_gemm_fp8_blockscale", "xs_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    import xs_moe_capi
+    if not os.path.exists(xs_moe_capi.LIB_PATH):
+        pytest.fail("libxs_moe.so not built (run python xstar-infer_amd/build.py)")
+    lib = ctypes.CDLL(xs_moe_capi.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # the ctypes binding covers the same set
+    assert set(xs_moe_capi.EXPORTS) == set(declared_functions())
+
+
+def test_argument_validation_without_gpu():
+    import xs_moe_capi as X
+    L = X.lib()
+    p = X.MoeParams(16, 100, 128, 8, 2, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 0, 0)
+    assert L.xs_moe_workspace_size(ctypes.byref(p)) == 0          # H % 256 != 0
+    p.H = 256
+    assert L.xs_moe_workspace_size(ctypes.byref(p)) > 0
+    rc = L.xs_moe_route(None, None, 4, 8, 2, 1, 1, 1, 1.0, None, None, None)
+    assert rc == 1 and b"null" in L.xs_last_error()
+    rc = L.xs_quant_act_fp8(ctypes.c_void_p(16), X.XS_BF16, 4, 100, ctypes.c_void_p(16), ctypes.c_void_p(16), None)
+    assert rc == 1 and b"128" in L.xs_last_error()

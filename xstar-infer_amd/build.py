@@ -1,0 +1,74 @@
+"""Builds the MoE operator in-tree.
+
+  xstar_cpp_py/libxs_moe.so   HIP kernels + C ABI (include/xs_moe.h), hipcc for gfx950
+  xstar_cpp_py/xstar_cpp*.so  pybind11 module: Tensor + ops (g++, links libxs_moe.so)
+
+Usage: python xstar-infer_amd/build.py [--only hip|py]
+"""
+from __future__ import annotations
+
+import argparse
+import glob
+import os
+import subprocess
+import sys
+import sysconfig
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+OUT = os.path.join(HERE, "xstar_cpp_py")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    # packed FP32 instructions are kept out of every kernel
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-result",
+]
+
+
+def _run(cmd):
+    print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build_hip() -> str:
+    os.makedirs(OUT, exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(HERE, "csrc", "hip", "*.hip")))
+    out = os.path.join(OUT, "libxs_moe.so")
+    tmp = out + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc", "hip"),
+          *srcs, "-o", tmp, "-Wl,-soname,libxs_moe.so"])
+    os.replace(tmp, out)
+    return out
+
+
+def build_py() -> str:
+    import pybind11
+
+    srcs = sorted(glob.glob(os.path.join(HERE, "csrc", "src", "**", "*.cpp"), recursive=True))
+    srcs.append(os.path.join(HERE, "csrc", "bindings", "python_bindings.cpp"))
+    ext = sysconfig.get_config_var("EXT_SUFFIX")
+    out = os.path.join(OUT, "xstar_cpp" + ext)
+    tmp = out + ".tmp"
+    inc = [pybind11.get_include(), sysconfig.get_paths()["include"], os.path.join(ROOT, "include"),
+           os.path.join(HERE, "csrc", "include")]
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+          *[f"-I{i}" for i in inc], *srcs, "-o", tmp, f"-L{OUT}", "-lxs_moe",
+          "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, out)
+    return out
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--only", choices=["hip", "py"], default=None)
+    a = ap.parse_args(argv)
+    if a.only in (None, "hip"):
+        build_hip()
+    if a.only in (None, "py") and os.path.exists(os.path.join(HERE, "csrc", "bindings", "python_bindings.cpp")):
+        build_py()
+
+
+if __name__ == "__main__":
+    sys.exit(main())

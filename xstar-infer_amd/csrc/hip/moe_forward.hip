@@ -1,0 +1,381 @@
+// moe_forward.hip -- the whole MoE layer behind xs_moe_forward, and the single
+// FP8 block-scaled GEMM behind xs_gemm_fp8_blockscale.
+//
+// Replaces mlp(x, gate_up_weight, down_weight) (xstar_cpp/src/ops/mlp.cpp:47-86)
+// at the transformer_block call sites.  Every stage is enqueued on one stream
+// with no host synchronisation.  Device memory comes only from the caller's
+// workspace, laid out by WsLayout below.
+#include "moe_gemm.hpp"
+
+namespace xs {
+
+static size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// ---- optional per-stage timing (xs_moe_profile_*) ----
+// Stage boundaries: 0 logits | 1 route | 2 act quant | 3 permute | 4 gate_up |
+// 5 down | 6 combine | 7 end.  One set of 8 events per forward, up to kProfMax
+// forwards between two reads.
+static constexpr int kStages = 7, kProfMax = 512;
+static bool g_prof = false;
+static int g_prof_n = 0;
+static hipEvent_t g_prof_ev[kProfMax][kStages + 1];
+static bool g_prof_made[kProfMax] = {};
+
+static int prof_mark(int stage, hipStream_t st)
+{
+    if (!g_prof || g_prof_n >= kProfMax) return XS_OK;
+    int s = g_prof_n;
+    if (!g_prof_made[s]) {
+        for (int i = 0; i <= kStages; ++i) XS_HIP(hipEventCreate(&g_prof_ev[s][i]));
+        g_prof_made[s] = true;
+    }
+    XS_HIP(hipEventRecord(g_prof_ev[s][stage], st));
+    if (stage == kStages) ++g_prof_n;
+    return XS_OK;
+}
+
+struct WsLayout {
+    size_t logits, idx, w, mask, wordprefix, counts, offsets, perm, inv, row_token, tiles;
+    size_t xq, xs, xmq, xms, actq, acts, actms, y;
+    size_t total;
+};
+
+static int pick_bm(double rows_per_tile_group)
+{
+    if (rows_per_tile_group >= 96) return 128;
+    if (rows_per_tile_group >= 48) return 64;
+    if (rows_per_tile_group >= 24) return 32;
+    return 16;
+}
+
+static WsLayout layout(const xs_moe_params *p)
+{
+    const size_t T = (size_t)p->T, H = (size_t)p->H, I = (size_t)p->I, E = (size_t)p->E, k = (size_t)p->top_k;
+    const size_t S = T * k, R = S + (p->has_shared ? T : 0);
+    const size_t W = (size_t)mask_words_for(p->T);
+    const bool fp4 = p->routed_format == XS_FP4_E2M1X2;
+    WsLayout L = {};
+    size_t o = 0;
+    auto take = [&](size_t &field, size_t bytes) { field = o; o += al(bytes); };
+    take(L.logits, 4 * T * E);
+    take(L.idx, 4 * S);
+    take(L.w, 4 * S);
+    take(L.mask, 4 * W * E);
+    take(L.wordprefix, 4 * W * E);
+    take(L.counts, 4 * E);
+    take(L.offsets, 4 * (E + 2));
+    take(L.perm, 4 * S);
+    take(L.inv, 4 * S);
+    take(L.row_token, 4 * R);
+    take(L.tiles, 4 * (E + 2));
+    take(L.xq, T * H);
+    take(L.xs, 4 * T * (H / 128));
+    take(L.xmq, fp4 ? T * H : 0);
+    take(L.xms, fp4 ? T * (H / 32) : 0);
+    take(L.actq, R * I);
+    take(L.acts, 4 * R * (I / 128));
+    take(L.actms, fp4 ? S * (I / 32) : 0);
+    take(L.y, 2 * R * H);
+    L.total = o;
+    return L;
+}
+
+static int check_params(const xs_moe_params *p)
+{
+    XS_REQUIRE(p != nullptr, "params is null");
+    XS_REQUIRE(p->T >= 0 && p->T < (1 << 24), "T out of range");
+    XS_REQUIRE(p->H >= 256 && p->H % 256 == 0, "shape mismatch: H must be a multiple of 256");
+    XS_REQUIRE(p->I >= 128 && p->I % 128 == 0, "shape mismatch: I must be a multiple of 128");
+    XS_REQUIRE(p->E >= 1 && p->E <= 1024, "E must be in [1, 1024]");
+    XS_REQUIRE(p->top_k >= 1 && p->top_k <= 16 && p->top_k <= p->E, "top_k must be in [1, min(16, E)]");
+    XS_REQUIRE(p->x_dtype == XS_BF16 || p->x_dtype == XS_F32, "unsupported dtype");
+    XS_REQUIRE(p->routed_format == XS_FP8_E4M3 || p->routed_format == XS_FP4_E2M1X2,
+               "unsupported routed expert format");
+    XS_REQUIRE(p->T * p->top_k + p->T < ((int64_t)1 << 31), "too many rows");
+    if (p->n_group > 1) {
+        XS_REQUIRE(p->n_group <= 64 && p->E % p->n_group == 0 && p->E / p->n_group >= 2,
+                   "n_group must divide E into groups of >= 2 (n_group <= 64)");
+        XS_REQUIRE(p->topk_group >= 1 && p->topk_group <= p->n_group &&
+                       p->topk_group * (p->E / p->n_group) >= p->top_k,
+                   "topk_group must keep at least top_k experts");
+    }
+    return XS_OK;
+}
+
+int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_t ws_bytes,
+                hipStream_t st)
+{
+    int rc = check_params(p);
+    if (rc) return rc;
+    XS_REQUIRE(t && t->x && t->router_w && t->w13 && t->w13_scale && t->w2 && t->w2_scale && t->out,
+               "null pointer");
+    XS_REQUIRE(!p->has_shared || (t->shared_w13 && t->shared_w13_scale && t->shared_w2 && t->shared_w2_scale),
+               "null shared expert pointer");
+    const WsLayout L = layout(p);
+    XS_REQUIRE(ws != nullptr || L.total == 0, "workspace is null");
+    if (ws_bytes < L.total) return set_error(XS_ERR_WORKSPACE, "workspace too small: %zu < %zu", ws_bytes, L.total);
+    XS_REQUIRE(((uintptr_t)ws & 255) == 0, "workspace must be 256-byte aligned");
+    const int64_t T = p->T, H = p->H, I = p->I, E = p->E, k = p->top_k;
+    if (T == 0) return XS_OK;
+    const int64_t S = T * k;
+    const bool fp4 = p->routed_format == XS_FP4_E2M1X2;
+    const int shared_rows = p->has_shared ? (int)T : 0;
+    char *base = (char *)ws;
+#define WS(type, field) reinterpret_cast<type *>(base + L.field)
+    float *logits = WS(float, logits);
+    int32_t *idx = WS(int32_t, idx);
+    float *w = WS(float, w);
+    uint32_t *mask = WS(uint32_t, mask);
+    int32_t *offsets = WS(int32_t, offsets);
+    int32_t *inv = WS(int32_t, inv);
+    int32_t *tiles = WS(int32_t, tiles);
+    const int Wd = mask_words_for(T);
+
+    // 1. router: logits -> top-k + per-expert token masks
+    if ((rc = prof_mark(0, st))) return rc;
+    rc = launch_mask_clear(mask, (int64_t)Wd * E, st);
+    if (rc) return rc;
+    rc = launch_router_logits(t->x, t->router_w, p->x_dtype, T, E, H, p->router_exact, logits, st);
+    if (rc) return rc;
+    if ((rc = prof_mark(1, st))) return rc;
+    rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
+                      p->routed_scaling, idx, w, mask, Wd, st);
+    if (rc) return rc;
+    // 2. activation quantization (once per token, gathered by the GEMMs)
+    if ((rc = prof_mark(2, st))) return rc;
+    if (!fp4 || p->has_shared) {
+        rc = launch_quant_act(t->x, p->x_dtype, T, H, WS(uint8_t, xq), WS(float, xs), 0, st);
+        if (rc) return rc;
+    }
+    if (fp4) {
+        rc = launch_quant_act(t->x, p->x_dtype, T, H, WS(uint8_t, xmq), WS(uint8_t, xms), 1, st);
+        if (rc) return rc;
+    }
+    // 3. permute: (expert, token)-sorted positions, tile offsets
+    if ((rc = prof_mark(3, st))) return rc;
+    const int bm = pick_bm((double)S / (double)E);
+    PermuteOut po = {};
+    po.counts = WS(int32_t, counts);
+    po.offsets = offsets;
+    po.perm = WS(int32_t, perm);
+    po.inv = inv;
+    po.row_token = WS(int32_t, row_token);
+    po.tile_off[0] = tiles;
+    po.tile_bm[0] = bm;
+    po.n_tile_sizes = 1;
+    po.offsets_ext = 1;
+    rc = launch_permute(idx, mask, T, E, k, shared_rows, WS(int32_t, wordprefix), po, st);
+    if (rc) return rc;
+
+    const int routed_tiles = (int)(S / bm + (E < S ? E : S));
+    const int shared_tiles = (int)((shared_rows + bm - 1) / bm);
+
+    // 4. gate_up GEMM + SwiGLU + activation re-quant
+    GemmArgs g1 = {};
+    g1.row_token = po.row_token;
+    g1.B = (const uint8_t *)t->w13;
+    g1.Bs = t->w13_scale;
+    g1.Bsh = (const uint8_t *)t->shared_w13;
+    g1.Bssh = t->shared_w13_scale;
+    g1.offsets = offsets;
+    g1.tile_off = tiles;
+    g1.E = (int)E;
+    g1.K = (int)H;
+    g1.N = (int)I;
+    g1.bm = bm;
+    g1.Cq = WS(uint8_t, actq);
+    GemmArgs g2 = {};
+    g2.row_token = nullptr;
+    g2.A = WS(uint8_t, actq);
+    g2.B = (const uint8_t *)t->w2;
+    g2.Bs = t->w2_scale;
+    g2.Bsh = (const uint8_t *)t->shared_w2;
+    g2.Bssh = t->shared_w2_scale;
+    g2.offsets = offsets;
+    g2.tile_off = tiles;
+    g2.E = (int)E;
+    g2.K = (int)I;
+    g2.N = (int)H;
+    g2.bm = bm;
+    g2.Cy = WS(uint16_t, y);
+    g2.ldc = H;
+
+    if ((rc = prof_mark(4, st))) return rc;
+    if (!fp4) {
+        g1.A = WS(uint8_t, xq);
+        g1.As = WS(float, xs);
+        g1.Cs = WS(float, acts);
+        g1.e_lo = 0;
+        g1.e_hi = (int)E + (shared_rows ? 1 : 0);
+        rc = launch_gemm(g1, true, false, routed_tiles + shared_tiles, st);
+        if (rc) return rc;
+        if ((rc = prof_mark(5, st))) return rc;
+        g2.As = WS(float, acts);
+        g2.e_lo = 0;
+        g2.e_hi = g1.e_hi;
+        rc = launch_gemm(g2, false, false, routed_tiles + shared_tiles, st);
+        if (rc) return rc;
+    } else {
+        GemmArgs r1 = g1;
+        r1.A = WS(uint8_t, xmq);
+        r1.As = WS(uint8_t, xms);
+        r1.Cs = WS(uint8_t, actms);
+        r1.e_lo = 0;
+        r1.e_hi = (int)E;
+        rc = launch_gemm(r1, true, true, routed_tiles, st);
+        if (rc) return rc;
+        if (shared_rows) {
+            GemmArgs s1 = g1;
+            s1.A = WS(uint8_t, xq);
+            s1.As = WS(float, xs);
+            s1.Cs = WS(float, acts);
+            s1.e_lo = (int)E;
+            s1.e_hi = (int)E + 1;
+            rc = launch_gemm(s1, true, false, shared_tiles, st);
+            if (rc) return rc;
+        }
+        if ((rc = prof_mark(5, st))) return rc;
+        GemmArgs r2 = g2;
+        r2.As = WS(uint8_t, actms);
+        r2.e_lo = 0;
+        r2.e_hi = (int)E;
+        rc = launch_gemm(r2, false, true, routed_tiles, st);
+        if (rc) return rc;
+        if (shared_rows) {
+            GemmArgs s2 = g2;
+            s2.As = WS(float, acts);
+            s2.e_lo = (int)E;
+            s2.e_hi = (int)E + 1;
+            rc = launch_gemm(s2, false, false, shared_tiles, st);
+            if (rc) return rc;
+        }
+    }
+    // 5. weighted combine (+ shared), one cast to the output dtype
+    if ((rc = prof_mark(6, st))) return rc;
+    rc = launch_combine(WS(uint16_t, y), inv, w, T, k, H, S, shared_rows ? 1 : 0, t->out, p->x_dtype, st);
+    if (rc) return rc;
+    if ((rc = prof_mark(7, st))) return rc;
+
+    // optional inspection outputs
+    auto cp = [&](void *dst, const void *src, size_t bytes) -> int {
+        if (dst && bytes) XS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, st));
+        return XS_OK;
+    };
+    if ((rc = cp(t->logits, logits, 4 * (size_t)(T * E)))) return rc;
+    if ((rc = cp(t->topk_idx, idx, 4 * (size_t)S))) return rc;
+    if ((rc = cp(t->topk_w, w, 4 * (size_t)S))) return rc;
+    if ((rc = cp(t->counts, po.counts, 4 * (size_t)E))) return rc;
+    if ((rc = cp(t->offsets, offsets, 4 * (size_t)(E + 1)))) return rc;
+    if ((rc = cp(t->perm, po.perm, 4 * (size_t)S))) return rc;
+    if ((rc = cp(t->inv, inv, 4 * (size_t)S))) return rc;
+#undef WS
+    return XS_OK;
+}
+
+// --------------------------------------------------- single FP8 GEMM (C = A.B^T)
+__global__ void single_segment_kernel(int32_t *offsets, int32_t *tiles, int M, int bm)
+{
+    offsets[0] = 0;
+    offsets[1] = M;
+    offsets[2] = M;
+    tiles[0] = 0;
+    tiles[1] = (M + bm - 1) / bm;
+    tiles[2] = tiles[1];
+}
+
+static size_t gemm_ws(int64_t M, int64_t K, size_t *o_s, size_t *o_meta)
+{
+    size_t q = al((size_t)M * K);
+    size_t s = al(4 * (size_t)M * (K / 128));
+    *o_s = q;
+    *o_meta = q + s;
+    return q + s + 256;
+}
+
+}  // namespace xs
+
+using namespace xs;
+
+extern "C" {
+
+size_t xs_moe_workspace_size(const xs_moe_params *p)
+{
+    if (check_params(p)) return 0;
+    return layout(p).total;
+}
+
+int xs_moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *workspace,
+                   size_t workspace_bytes, void *stream)
+{
+    return moe_forward(p, t, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int xs_moe_profile_enable(int enable)
+{
+    g_prof = enable != 0;
+    g_prof_n = 0;
+    return XS_OK;
+}
+
+int xs_moe_profile_read(float *stage_ms, int n_stages, int *n_calls)
+{
+    XS_REQUIRE(stage_ms && n_stages >= 1, "null pointer");
+    for (int i = 0; i < n_stages; ++i) stage_ms[i] = 0.f;
+    for (int s = 0; s < g_prof_n; ++s) {
+        XS_HIP(hipEventSynchronize(g_prof_ev[s][kStages]));
+        for (int i = 0; i < kStages && i < n_stages; ++i) {
+            float ms = 0.f;
+            XS_HIP(hipEventElapsedTime(&ms, g_prof_ev[s][i], g_prof_ev[s][i + 1]));
+            stage_ms[i] += ms;
+        }
+    }
+    if (n_calls) *n_calls = g_prof_n;
+    g_prof_n = 0;
+    return XS_OK;
+}
+
+size_t xs_gemm_fp8_blockscale_workspace_size(int64_t M, int64_t K)
+{
+    size_t a, b;
+    return gemm_ws(M, K, &a, &b);
+}
+
+int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int64_t M, int64_t N,
+                           int64_t K, void *C, void *workspace, size_t workspace_bytes, void *stream)
+{
+    XS_REQUIRE(A && B && Bs && C, "null pointer");
+    XS_REQUIRE(M >= 0 && M < (1 << 24) && N >= 128 && N % 128 == 0 && K >= 128 && K % 128 == 0,
+               "shape mismatch: N and K must be multiples of 128");
+    size_t o_s, o_meta;
+    size_t need = gemm_ws(M, K, &o_s, &o_meta);
+    if (!workspace || workspace_bytes < need)
+        return set_error(XS_ERR_WORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, need);
+    if (M == 0) return XS_OK;
+    hipStream_t st = (hipStream_t)stream;
+    char *ws = (char *)workspace;
+    int rc = launch_quant_act(A, XS_BF16, M, K, (uint8_t *)ws, ws + o_s, 0, st);
+    if (rc) return rc;
+    int32_t *offsets = (int32_t *)(ws + o_meta);
+    int32_t *tiles = offsets + 4;
+    const int bm = M >= 2048 ? 128 : (M >= 1024 ? 64 : (M >= 256 ? 32 : 16));
+    single_segment_kernel<<<1, 1, 0, st>>>(offsets, tiles, (int)M, bm);
+    XS_LAUNCH_CHECK();
+    GemmArgs g = {};
+    g.A = (const uint8_t *)ws;
+    g.As = ws + o_s;
+    g.B = B;
+    g.Bs = Bs;
+    g.offsets = offsets;
+    g.tile_off = tiles;
+    g.e_lo = 0;
+    g.e_hi = 1;
+    g.E = 1;
+    g.K = (int)K;
+    g.N = (int)N;
+    g.bm = bm;
+    g.Cy = (uint16_t *)C;
+    g.ldc = N;
+    return launch_gemm(g, false, false, (int)((M + bm - 1) / bm), st);
+}
+
+}  // extern "C"

@@ -1,0 +1,466 @@
+// moe_gemm.hip -- grouped block-scaled GEMMs for the MoE experts on gfx950.
+//
+// Nearest reference code: gemm_silu_and_mul_kernel (xstar_cpp/src/ops/mlp.cu:52-200;
+// paired gate/up tiles sharing one A tile, SwiGLU in f32 with one downcast)
+// and gemm_kernel (xstar_cpp/src/ops/gemm.cu:41-210).  Those are SIMT f32
+// kernels on 32x32 tiles; here every expert is an FP8 (or MXFP4) MFMA GEMM:
+//
+//   * rows of one expert are contiguous positions of the permutation; a block
+//     owns BM of them and a 256-wide slab of output columns;
+//   * K advances 128 at a time (one FP8 scale block) through a two-stage LDS
+//     ring (16-byte chunks, XOR-swizzled so the MFMA operand reads are
+//     bank-conflict free);
+//   * FP8: each 16x16x128 MFMA (v_mfma_f32_16x16x128_f8f6f4) yields the
+//     partial sum of one 128-K block, which is folded into the f32 accumulator
+//     with the product of the activation row scale and the weight block scale;
+//   * MXFP4: v_mfma_scale_f32_16x16x128_f8f6f4 applies the per-32 e8m0 scales
+//     of both operands in hardware and accumulates across all of K;
+//   * gate_up: the 256 columns are 128 gate rows + the matching 128 up rows of
+//     W13 (interleaved per 16-column subtile so one wave holds matching pairs);
+//     the epilogue computes silu(g)*u in f32 and re-quantizes the activation
+//     for the down GEMM (FP8 1x128, or MXFP8 1x32 for FP4 experts);
+//   * down: the epilogue writes bf16 rows (weighted combine runs after).
+#include "moe_gemm.hpp"
+
+namespace xs {
+
+template <int BM>
+struct Shape {
+    static constexpr int WM = BM >= 128 ? 2 : 1;
+    static constexpr int WN = 4 / WM;
+    static constexpr int TM = BM / WM;          // wave rows
+    static constexpr int TN = 256 / WN;         // wave columns
+    static constexpr int MI = TM / 16;
+    static constexpr int NJ = TN / 16;
+};
+
+// LDS row swizzles: 16-byte chunk c of row r lives at physical chunk c ^ f(r).
+__device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }   // 128-byte rows
+__device__ __forceinline__ int swz4(int r, int c) { return c ^ ((r >> 2) & 3); }   // 64-byte rows
+
+__device__ __forceinline__ v8i cat(v4i a, v4i b) { return v8i{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}; }
+
+// Locate the tile of blockIdx.y: expert e and first row m0 within the expert.
+__device__ __forceinline__ bool find_tile(const GemmArgs &a, int &e, int &m0, int &rows)
+{
+    const int base = a.tile_off[a.e_lo];
+    const int i = base + (int)blockIdx.y;
+    if (i >= a.tile_off[a.e_hi]) return false;
+    int lo = a.e_lo, hi = a.e_hi - 1;   // largest e with tile_off[e] <= i
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (a.tile_off[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    e = lo;
+    m0 = (i - a.tile_off[e]) * a.bm;
+    rows = a.offsets[e + 1] - a.offsets[e] - m0;
+    return rows > 0;
+}
+
+template <int BM, bool GATEUP, bool FP4>
+__global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
+{
+    using S = Shape<BM>;
+    constexpr int BROW = FP4 ? 64 : 128;          // bytes per B row per K step
+    constexpr int A_BYTES = BM * 128, B_BYTES = 256 * BROW;
+    constexpr int STAGE = A_BYTES + B_BYTES;
+    constexpr int NA = (BM * 8 + 255) / 256;      // A chunks per thread
+    constexpr int NB = B_BYTES / 16 / 256;        // B chunks per thread
+
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int KB = a.K / 128;
+    uint8_t *stage0 = smem;
+    float *sA = reinterpret_cast<float *>(smem + 2 * STAGE);          // [KB][BM] (FP4: u32 words)
+    float *sB = sA + KB * BM;                                          // FP8: [2][KB]; FP4: [KB][256] u32
+    float *red = sB + (FP4 ? KB * 256 : 2 * KB);                       // [WN][BM]
+
+    int e, m0, rows;
+    if (!find_tile(a, e, m0, rows)) return;
+    if (rows > BM) rows = BM;
+    const bool shared = e == a.E;
+    const int pos0 = a.offsets[e] + m0;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / S::WN, wn = wave % S::WN;
+    const int l16 = lane & 15, g = lane >> 4;
+
+    const int n0 = blockIdx.x * (GATEUP ? 128 : 256);
+    const int Nrows = GATEUP ? 2 * a.N : a.N;                  // rows of B for this expert
+    const uint8_t *Bexp = shared ? a.Bsh : a.B + (size_t)e * Nrows * (FP4 ? a.K / 2 : a.K);
+
+    // B row of virtual column vr (0..255)
+    auto brow_of = [&](int vr) -> int {
+        if (GATEUP) {
+            int sub = vr >> 4, w = vr & 15;
+            int n = n0 + (sub >> 1) * 16 + w;
+            return (sub & 1) ? a.N + n : n;
+        }
+        return min(n0 + vr, a.N - 1);
+    };
+    auto arow_of = [&](int r) -> int {
+        int p = pos0 + min(r, rows - 1);
+        return a.row_token ? a.row_token[p] : p;
+    };
+
+    // ---- per-thread global source pointers (fixed across K) ----
+    const uint8_t *ga[NA];
+    int la[NA];
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+        int q = tid + 256 * u;
+        int r = q >> 3, c = q & 7;
+        ga[u] = a.A + (size_t)arow_of(r < BM ? r : 0) * a.K + c * 16;
+        la[u] = (q < BM * 8) ? r * 128 + swz8(r, c) * 16 : -1;
+    }
+    const uint8_t *gb[NB];
+    int lb[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        int q = tid + 256 * u;
+        if (FP4) {
+            int r = q >> 2, c = q & 3;
+            gb[u] = Bexp + (size_t)brow_of(r) * (a.K / 2) + c * 16;
+            lb[u] = r * 64 + swz4(r, c) * 16;
+        } else {
+            int r = q >> 3, c = q & 7;
+            gb[u] = Bexp + (size_t)brow_of(r) * a.K + c * 16;
+            lb[u] = r * 128 + swz8(r, c) * 16;
+        }
+    }
+
+    // ---- scales for the whole tile ----
+    if (FP4) {
+        const uint8_t *As8 = reinterpret_cast<const uint8_t *>(a.As);
+        uint32_t *sAw = reinterpret_cast<uint32_t *>(sA);
+        for (int q = tid; q < KB * BM; q += 256) {
+            int r = q % BM, kb = q / BM;
+            sAw[q] = *reinterpret_cast<const uint32_t *>(As8 + (size_t)arow_of(r) * (a.K / 32) + kb * 4);
+        }
+        const uint8_t *Bs8 = reinterpret_cast<const uint8_t *>(a.Bs) + (size_t)e * Nrows * (a.K / 32);
+        uint32_t *sBw = reinterpret_cast<uint32_t *>(sB);
+        for (int q = tid; q < KB * 256; q += 256) {
+            int vr = q & 255, kb = q >> 8;
+            sBw[q] = *reinterpret_cast<const uint32_t *>(Bs8 + (size_t)brow_of(vr) * (a.K / 32) + kb * 4);
+        }
+    } else {
+        const float *Asf = reinterpret_cast<const float *>(a.As);
+        for (int q = tid; q < KB * BM; q += 256) {
+            int r = q % BM, kb = q / BM;
+            sA[q] = Asf[(size_t)arow_of(r) * KB + kb];
+        }
+        const float *Bsf = shared ? a.Bssh : reinterpret_cast<const float *>(a.Bs) + (size_t)e * (Nrows / 128) * KB;
+        for (int q = tid; q < 2 * KB; q += 256) {
+            int b = q / KB, kb = q % KB;
+            int nb;
+            if (GATEUP) nb = (b ? a.N + n0 : n0) / 128;
+            else nb = min(n0 / 128 + b, a.N / 128 - 1);
+            sB[q] = Bsf[(size_t)nb * KB + kb];
+        }
+    }
+
+    v4f acc[S::MI][S::NJ];
+#pragma unroll
+    for (int i = 0; i < S::MI; ++i)
+#pragma unroll
+        for (int j = 0; j < S::NJ; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    v4i ra[NA], rb[NB];
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int u = 0; u < NA; ++u)
+            if (la[u] >= 0) ra[u] = *reinterpret_cast<const v4i *>(ga[u] + (size_t)kb * 128);
+#pragma unroll
+        for (int u = 0; u < NB; ++u) rb[u] = *reinterpret_cast<const v4i *>(gb[u] + (size_t)kb * BROW);
+    };
+    auto sstore = [&](int buf) {
+        uint8_t *st = stage0 + buf * STAGE;
+#pragma unroll
+        for (int u = 0; u < NA; ++u)
+            if (la[u] >= 0) *reinterpret_cast<v4i *>(st + la[u]) = ra[u];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) *reinterpret_cast<v4i *>(st + A_BYTES + lb[u]) = rb[u];
+    };
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+
+    for (int kb = 0; kb < KB; ++kb) {
+        const int buf = kb & 1;
+        if (kb + 1 < KB) gload(kb + 1);
+        const uint8_t *sa_ = stage0 + buf * STAGE;
+        const uint8_t *sb_ = sa_ + A_BYTES;
+
+        // Operand layout of v_mfma_*_16x16x128_f8f6f4 (gfx950): for an FP8
+        // operand, lane 16g + r holds row r with K = [16g, 16g+16) in bytes 0..15
+        // and K = [64+16g, 64+16g+16) in bytes 16..31, i.e. LDS chunks g and g+4
+        // of the row; for an FP4 operand, lane 16g + r holds K = [32g, 32g+32)
+        // (element 2i in the low nibble), i.e. 16-byte chunk g of a 64-byte row.
+        // The e8m0 scale of (row r, 32-wide K block b) is taken from lane 16b + r.
+        // Pinned by the FP8 x FP4 parity tests.
+        v8i afr[S::MI];
+#pragma unroll
+        for (int i = 0; i < S::MI; ++i) {
+            int r = wm * S::TM + 16 * i + l16;
+            v4i lo = *reinterpret_cast<const v4i *>(sa_ + r * 128 + swz8(r, g) * 16);
+            v4i hi = *reinterpret_cast<const v4i *>(sa_ + r * 128 + swz8(r, g + 4) * 16);
+            afr[i] = cat(lo, hi);
+        }
+        if (FP4) {
+            const uint32_t *sAw = reinterpret_cast<const uint32_t *>(sA) + kb * BM;
+            const uint32_t *sBw = reinterpret_cast<const uint32_t *>(sB) + kb * 256;
+            int sa_s[S::MI];
+#pragma unroll
+            for (int i = 0; i < S::MI; ++i) sa_s[i] = (int)((sAw[wm * S::TM + 16 * i + l16] >> (8 * g)) & 0xffu);
+#pragma unroll
+            for (int j = 0; j < S::NJ; ++j) {
+                int vr = wn * S::TN + 16 * j + l16;
+                v4i b4 = *reinterpret_cast<const v4i *>(sb_ + vr * 64 + swz4(vr, g) * 16);
+                v8i bfr = v8i{b4[0], b4[1], b4[2], b4[3], 0, 0, 0, 0};
+                int sb_s = (int)((sBw[vr] >> (8 * g)) & 0xffu);
+#pragma unroll
+                for (int i = 0; i < S::MI; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(afr[i], bfr, acc[i][j], 0, 4, 0,
+                                                                                sa_s[i], 0, sb_s);
+            }
+        } else {
+            float csc[S::MI][4][2];
+            const float sb0 = sB[kb], sb1 = sB[KB + kb];
+#pragma unroll
+            for (int i = 0; i < S::MI; ++i) {
+                v4f sa4 = *reinterpret_cast<const v4f *>(sA + kb * BM + wm * S::TM + 16 * i + 4 * g);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    csc[i][v][0] = sa4[v] * sb0;
+                    csc[i][v][1] = sa4[v] * sb1;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < S::NJ; ++j) {
+                int vr = wn * S::TN + 16 * j + l16;
+                v4i lo = *reinterpret_cast<const v4i *>(sb_ + vr * 128 + swz8(vr, g) * 16);
+                v4i hi = *reinterpret_cast<const v4i *>(sb_ + vr * 128 + swz8(vr, g + 4) * 16);
+                v8i bfr = cat(lo, hi);
+                const int blk = GATEUP ? (j & 1) : ((wn * S::TN + 16 * j) >> 7);
+#pragma unroll
+                for (int i = 0; i < S::MI; ++i) {
+                    v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(afr[i], bfr, v4f{0.f, 0.f, 0.f, 0.f},
+                                                                             0, 0, 0, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], csc[i][v][blk], acc[i][j][v]);
+                }
+            }
+        }
+        if (kb + 1 < KB) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ------------------------------------------------------------ epilogue
+    if (GATEUP) {
+        constexpr int NP = S::NJ / 2;     // gate/up pairs per wave
+        float act[S::MI][NP][4];
+#pragma unroll
+        for (int i = 0; i < S::MI; ++i)
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float gt = acc[i][2 * p][v], up = acc[i][2 * p + 1][v];
+                    act[i][p][v] = gt * fast_sigmoid(gt) * up;
+                }
+        uint8_t *stg = smem;   // [BM][128] fp8 staging (stage buffers are free now)
+        if (!FP4) {
+            // FP8 1x128: row amax over the block's 128 act columns (all waves of a row)
+#pragma unroll
+            for (int i = 0; i < S::MI; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float m = 0.f;
+#pragma unroll
+                    for (int p = 0; p < NP; ++p) m = fmaxf(m, __builtin_fabsf(act[i][p][v]));
+#pragma unroll
+                    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, WAVE));
+                    if (l16 == 0) red[wn * BM + wm * S::TM + 16 * i + 4 * g + v] = m;
+                }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < S::MI; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    int r = wm * S::TM + 16 * i + 4 * g + v;
+                    float amax = 0.f;
+#pragma unroll
+                    for (int w = 0; w < S::WN; ++w) amax = fmaxf(amax, red[w * BM + r]);
+                    float inv = amax == 0.f ? 0.f : __fdiv_rn(448.0f, amax);
+#pragma unroll
+                    for (int p = 0; p < NP; p += 2) {
+                        float x0 = fminf(fmaxf(act[i][p][v] * inv, -448.f), 448.f);
+                        float x1 = fminf(fmaxf(act[i][p + 1][v] * inv, -448.f), 448.f);
+                        uint32_t pk = e4m3_pack2_hw(x0, x1);
+                        int c0 = (wn * NP + p) * 16 + l16;
+                        stg[r * 128 + c0] = (uint8_t)(pk & 0xff);
+                        stg[r * 128 + c0 + 16] = (uint8_t)(pk >> 8);
+                    }
+                }
+            __syncthreads();
+            float *Cs = reinterpret_cast<float *>(a.Cs);
+            for (int r = tid; r < rows; r += 256) {
+                float amax = 0.f;
+#pragma unroll
+                for (int w = 0; w < S::WN; ++w) amax = fmaxf(amax, red[w * BM + r]);
+                Cs[(size_t)(pos0 + r) * (a.N / 128) + n0 / 128] = amax == 0.f ? 1.0f : __fdiv_rn(amax, 448.0f);
+            }
+        } else {
+            // MXFP8 1x32: a 32-column block is pairs (2q, 2q+1) of one wave
+            uint8_t *Cs8 = reinterpret_cast<uint8_t *>(a.Cs);
+#pragma unroll
+            for (int i = 0; i < S::MI; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    int r = wm * S::TM + 16 * i + 4 * g + v;
+#pragma unroll
+                    for (int p = 0; p < NP; p += 2) {
+                        float m = fmaxf(__builtin_fabsf(act[i][p][v]), __builtin_fabsf(act[i][p + 1][v]));
+#pragma unroll
+                        for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, WAVE));
+                        int se = mx_exponent(m, 8);
+                        float x0 = fminf(fmaxf(__builtin_ldexpf(act[i][p][v], -se), -448.f), 448.f);
+                        float x1 = fminf(fmaxf(__builtin_ldexpf(act[i][p + 1][v], -se), -448.f), 448.f);
+                        uint32_t pk = e4m3_pack2_hw(x0, x1);
+                        int c0 = (wn * NP + p) * 16 + l16;
+                        stg[r * 128 + c0] = (uint8_t)(pk & 0xff);
+                        stg[r * 128 + c0 + 16] = (uint8_t)(pk >> 8);
+                        if (l16 == 0 && r < rows)
+                            Cs8[(size_t)(pos0 + r) * (a.N / 32) + (n0 + (wn * NP + p) * 16) / 32] = (uint8_t)(se + 127);
+                    }
+                }
+            __syncthreads();
+        }
+        for (int q = tid; q < rows * 8; q += 256) {
+            int r = q >> 3, c = q & 7;
+            *reinterpret_cast<v4i *>(a.Cq + (size_t)(pos0 + r) * a.N + n0 + c * 16) =
+                *reinterpret_cast<const v4i *>(stg + r * 128 + c * 16);
+        }
+    } else {
+        uint16_t *stg = reinterpret_cast<uint16_t *>(smem);   // [BM][256] bf16
+#pragma unroll
+        for (int i = 0; i < S::MI; ++i)
+#pragma unroll
+            for (int j = 0; j < S::NJ; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    int r = wm * S::TM + 16 * i + 4 * g + v;
+                    int c = wn * S::TN + 16 * j + l16;
+                    stg[r * 256 + c] = bf16_from_f32(acc[i][j][v]);
+                }
+        __syncthreads();
+        const int ncols = min(256, a.N - n0);
+        for (int q = tid; q < rows * 32; q += 256) {
+            int r = q >> 5, c = q & 31;
+            if (c * 8 < ncols)
+                *reinterpret_cast<v4i *>(a.Cy + (size_t)(pos0 + r) * a.ldc + n0 + c * 8) =
+                    *reinterpret_cast<const v4i *>(stg + r * 256 + c * 8);
+        }
+    }
+}
+
+template <int BM, bool GATEUP, bool FP4>
+static size_t gemm_smem_bytes(int K)
+{
+    using S = Shape<BM>;
+    const int KB = K / 128;
+    size_t stage = (size_t)BM * 128 + 256 * (FP4 ? 64 : 128);
+    size_t b = 2 * stage + 4 * (size_t)KB * BM + 4 * (FP4 ? (size_t)KB * 256 : 2 * (size_t)KB) + 4 * (size_t)S::WN * BM;
+    size_t epi = GATEUP ? (size_t)BM * 128 : (size_t)BM * 512;
+    return b > epi ? b : epi;   // staging reuses the stage buffers, which precede the scales
+}
+
+template <int BM, bool GATEUP, bool FP4>
+static int launch_one(const GemmArgs &a, int grid_y, hipStream_t st)
+{
+    size_t smem = gemm_smem_bytes<BM, GATEUP, FP4>(a.K);
+    if (smem > 160 * 1024) return set_error(XS_ERR_UNSUPPORTED, "K=%d needs %zu bytes of LDS", a.K, smem);
+    auto fn = moe_gemm_kernel<BM, GATEUP, FP4>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        XS_HIP(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        attr_set = true;
+    }
+    int grid_x = GATEUP ? a.N / 128 : (a.N + 255) / 256;
+    if (grid_y <= 0) return XS_OK;
+    fn<<<dim3((unsigned)grid_x, (unsigned)grid_y), dim3(256), smem, st>>>(a);
+    XS_LAUNCH_CHECK();
+    return XS_OK;
+}
+
+int launch_gemm(const GemmArgs &a, bool gateup, bool fp4, int grid_y, hipStream_t st)
+{
+#define XS_G(BMV)                                                                           \
+    case BMV:                                                                               \
+        if (gateup) return fp4 ? launch_one<BMV, true, true>(a, grid_y, st)                 \
+                               : launch_one<BMV, true, false>(a, grid_y, st);               \
+        return fp4 ? launch_one<BMV, false, true>(a, grid_y, st)                            \
+                   : launch_one<BMV, false, false>(a, grid_y, st);
+    switch (a.bm) {
+        XS_G(16)
+        XS_G(32)
+        XS_G(64)
+        XS_G(128)
+    default:
+        return set_error(XS_ERR_INVALID, "unsupported tile rows %d", a.bm);
+    }
+#undef XS_G
+}
+
+// --------------------------------------------------------------- combine
+// out[t] = y_shared[t] + sum_j w[t,j] * y[inv[t*k+j]]  (f32, slot order, one cast)
+template <typename OutT>
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict__ y,
+                                                      const int32_t *__restrict__ inv,
+                                                      const float *__restrict__ w, int k, int H,
+                                                      int64_t shared_base, int has_shared,
+                                                      OutT *__restrict__ out)
+{
+    const int t = blockIdx.x;
+    int pos[16];
+    float wt[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        if (j < k) {
+            pos[j] = inv[(size_t)t * k + j];
+            wt[j] = w[(size_t)t * k + j];
+        }
+    for (int c = threadIdx.x * 8; c < H; c += 256 * 8) {
+        float acc[8];
+        if (has_shared) load8(y + (size_t)(shared_base + t) * H + c, acc);
+        else
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            if (j < k) {
+                float v[8];
+                load8(y + (size_t)pos[j] * H + c, v);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(wt[j], v[i]));
+            }
+        }
+        store8(out + (size_t)t * H + c, acc);
+    }
+}
+
+int launch_combine(const uint16_t *y, const int32_t *inv, const float *w, int64_t T, int64_t k,
+                   int64_t H, int64_t shared_base, int has_shared, void *out, int out_dtype,
+                   hipStream_t st)
+{
+    if (T == 0) return XS_OK;
+    if (out_dtype == XS_BF16)
+        combine_kernel<uint16_t><<<dim3((unsigned)T), dim3(256), 0, st>>>(y, inv, w, (int)k, (int)H, shared_base,
+                                                                          has_shared, (uint16_t *)out);
+    else
+        combine_kernel<float><<<dim3((unsigned)T), dim3(256), 0, st>>>(y, inv, w, (int)k, (int)H, shared_base,
+                                                                       has_shared, (float *)out);
+    XS_LAUNCH_CHECK();
+    return XS_OK;
+}
+
+}  // namespace xs

@@ -1,0 +1,34 @@
+// moe_gemm.hpp -- argument block and launchers of the grouped expert GEMMs.
+#pragma once
+
+#include "moe_internal.hpp"
+
+namespace xs {
+
+struct GemmArgs {
+    const uint8_t *A;          // FP8 activation rows [*, K]
+    const void *As;            // f32 [*, K/128] (FP8) or e8m0 [*, K/32] (MXFP8)
+    const int32_t *row_token;  // position -> A row (NULL: A row = position)
+    const uint8_t *B;          // routed weights [E, Nrows, K] (FP4: [E, Nrows, K/2])
+    const void *Bs;            // routed scales
+    const uint8_t *Bsh;        // shared expert weights (FP8), used for e == E
+    const float *Bssh;         // shared expert scales
+    const int32_t *offsets;    // [E+2] row offsets per expert (E = shared segment)
+    const int32_t *tile_off;   // [E+2] tile offsets for tile height bm
+    int e_lo, e_hi;            // experts covered by this launch: [e_lo, e_hi)
+    int E;
+    int K;                     // reduction length
+    int N;                     // gate_up: I (output act columns); down: H
+    int bm;                    // tile rows: 16, 32, 64 or 128
+    uint8_t *Cq;               // gate_up: act rows [*, I] FP8
+    void *Cs;                  // gate_up: f32 [*, I/128] or e8m0 [*, I/32]
+    uint16_t *Cy;              // down: bf16 rows [*, ldc]
+    int64_t ldc;
+};
+
+int launch_gemm(const GemmArgs &a, bool gateup, bool fp4, int grid_y, hipStream_t st);
+int launch_combine(const uint16_t *y, const int32_t *inv, const float *w, int64_t T, int64_t k,
+                   int64_t H, int64_t shared_base, int has_shared, void *out, int out_dtype,
+                   hipStream_t st);
+
+}  // namespace xs

@@ -1,0 +1,76 @@
+// moe_internal.hpp -- declarations shared by the MoE translation units.
+#pragma once
+
+#include "xs_device.hpp"
+
+namespace xs {
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(uint16_t v) { return f32_from_bf16(v); }
+
+// 8 consecutive elements -> f32 (16-byte aligned for bf16, 32-byte for f32).
+__device__ __forceinline__ void load8(const uint16_t *p, float *v)
+{
+    v4i r = *reinterpret_cast<const v4i *>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float((uint32_t)r[i] << 16);
+        v[2 * i + 1] = __uint_as_float((uint32_t)r[i] & 0xFFFF0000u);
+    }
+}
+__device__ __forceinline__ void load8(const float *p, float *v)
+{
+    v4f a = *reinterpret_cast<const v4f *>(p);
+    v4f b = *reinterpret_cast<const v4f *>(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[i] = a[i];
+        v[4 + i] = b[i];
+    }
+}
+
+// 8 f32 values -> 8 consecutive outputs (bf16 RNE or f32).
+__device__ __forceinline__ void store8(uint16_t *p, const float *v)
+{
+    v4i r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        r[i] = (int)((uint32_t)bf16_from_f32(v[2 * i]) | ((uint32_t)bf16_from_f32(v[2 * i + 1]) << 16));
+    *reinterpret_cast<v4i *>(p) = r;
+}
+__device__ __forceinline__ void store8(float *p, const float *v)
+{
+    *reinterpret_cast<v4f *>(p) = v4f{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<v4f *>(p + 4) = v4f{v[4], v[5], v[6], v[7]};
+}
+
+// ---- launchers (stream-ordered, no synchronisation) ----
+int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
+                         int exact, float *logits, hipStream_t st);
+int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,
+                 int64_t n_group, int64_t topk_group, int renorm, float scaling, int32_t *idx,
+                 float *w, uint32_t *mask, int mask_words, hipStream_t st);
+int launch_quant_act(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, void *s,
+                     int mx, hipStream_t st);
+
+// Permute.  Inputs: idx [T, k] and the per-expert token bitmasks built by the
+// route kernel (mask [E+?][mask_words]).  Outputs positions sorted by
+// (expert, token); a trailing shared-expert segment of T rows (identity) when
+// shared_rows != 0.
+struct PermuteOut {
+    int32_t *counts;      // [E]
+    int32_t *offsets;     // [E+2]: routed offsets, offsets[E+1] = end of the shared segment
+    int32_t *perm;        // [T*k] position -> slot
+    int32_t *inv;         // [T*k] slot -> position
+    int32_t *row_token;   // [T*k + T] position -> token
+    int32_t *tile_off[3]; // per tile size: [E+2] exclusive scan of ceil(count/BM) (incl. shared)
+    int tile_bm[3];
+    int n_tile_sizes;
+    int offsets_ext;      // offsets has E+2 entries
+};
+int mask_words_for(int64_t T);
+int launch_mask_clear(uint32_t *mask, int64_t words, hipStream_t st);
+int launch_permute(const int32_t *idx, const uint32_t *mask, int64_t T, int64_t E, int64_t k,
+                   int shared_rows, int32_t *wordprefix, const PermuteOut &o, hipStream_t st);
+
+}  // namespace xs

@@ -1,0 +1,498 @@
+// moe_router.hip -- router logits, top-k routing, activation and weight
+// quantizers for gfx950.
+//
+// Router logits replace linear(x, router_w, nullptr) (xstar_cpp/src/ops/linear.cpp:9-66).
+// Two variants: an exact kernel that reproduces gemm_cpu's sequential f32
+// accumulation (xstar_cpp/include/ops/gemm.h:57-83) bit for bit, and a bf16
+// MFMA kernel (v_mfma_f32_16x16x32_bf16, f32 accumulate).
+// Routing uses the branched sigmoid of xstar_cpp/src/ops/mlp.cpp:10-21 over a
+// reproducible exp, so indices and weights are bit-identical to the CPU
+// restatement given the same logits.
+#include "moe_internal.hpp"
+
+namespace xs {
+
+// ------------------------------------------------------------ exact logits
+// 256 threads = 16 tokens x 16 experts; k-chunks of 64 staged in LDS; each
+// thread owns one (t, e) and accumulates sequentially in k with separately
+// rounded products (no contraction), as gemm_cpu does.
+template <typename T>
+__global__ __launch_bounds__(256) void router_logits_exact_kernel(const T *__restrict__ x,
+                                                                  const T *__restrict__ wr,
+                                                                  int Tn, int E, int H,
+                                                                  float *__restrict__ logits)
+{
+#pragma clang fp contract(off)
+    __shared__ float xs_[16][65];
+    __shared__ float ws_[16][65];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
+    float acc = 0.0f;
+    for (int k0 = 0; k0 < H; k0 += 64) {
+        for (int i = threadIdx.x; i < 16 * 64; i += 256) {
+            int r = i >> 6, c = i & 63;
+            int tt = min(t0 + r, Tn - 1), ee = min(e0 + r, E - 1);
+            xs_[r][c] = to_f32(x[(size_t)tt * H + k0 + c]);
+            ws_[r][c] = to_f32(wr[(size_t)ee * H + k0 + c]);
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int c = 0; c < 64; ++c) acc = acc + xs_[ty][c] * ws_[tx][c];   // no contraction (pragma above)
+        __syncthreads();
+    }
+    int t = t0 + ty, e = e0 + tx;
+    if (t < Tn && e < E) logits[(size_t)t * E + e] = acc;
+}
+
+// ------------------------------------------------------------- MFMA logits
+// Block = 4 waves, tile 64 tokens x 64 experts.  Wave w owns tokens
+// [16w, 16w+16) against all 64 experts (four 16x16 output subtiles).  Operands
+// come straight from global memory (16 B per lane per MFMA; the router weight
+// is 2 MB and stays L2-resident).  MFMA 16x16x32 bf16: lane l supplies row
+// (l % 16) and k-slice (l / 16) of 8 elements for both A and B, so the
+// k-pairing is consistent whatever the hardware's internal k order.
+__global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t *__restrict__ x,
+                                                                 const uint16_t *__restrict__ wr,
+                                                                 int Tn, int E, int H,
+                                                                 float *__restrict__ logits)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int t0 = blockIdx.y * 64 + wave * 16, e0 = blockIdx.x * 64;
+    const int trow = min(t0 + r, Tn - 1);
+    const v8bf *xa = reinterpret_cast<const v8bf *>(x + (size_t)trow * H + g * 8);
+    const v8bf *wb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        wb[j] = reinterpret_cast<const v8bf *>(wr + (size_t)min(e0 + 16 * j + r, E - 1) * H + g * 8);
+    v4f acc[4] = {};
+    for (int k = 0; k < H; k += 128) {
+        v8bf a[4], b[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a[u] = xa[(k + 32 * u) / 8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) b[j][u] = wb[j][(k + 32 * u) / 8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], b[j][u], acc[j], 0, 0, 0);
+    }
+    // output layout: lane holds column (l % 16), rows 4*(l/16) + v
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        int e = e0 + 16 * j + r;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            int t = t0 + 4 * g + v;
+            if (t < Tn && e < E) logits[(size_t)t * E + e] = acc[j][v];
+        }
+    }
+}
+
+// ----------------------------------------------------------------- routing
+struct Cand {
+    float key;
+    float s;
+    int e;
+};
+
+// a is better than b: larger key, ties to the lower expert index; e < 0 = empty.
+__device__ __forceinline__ bool better(const Cand &a, const Cand &b)
+{
+    if (a.e < 0) return false;
+    if (b.e < 0) return true;
+    return a.key > b.key || (a.key == b.key && a.e < b.e);
+}
+
+__device__ __forceinline__ Cand wave_best(Cand c)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        Cand d;
+        d.key = __shfl_xor(c.key, o, WAVE);
+        d.s = __shfl_xor(c.s, o, WAVE);
+        d.e = __shfl_xor(c.e, o, WAVE);
+        if (better(d, c)) c = d;
+    }
+    return c;
+}
+
+// One wave per token.  Lane l holds experts l + 64*i, i < NV.
+template <int NV>
+__global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ logits,
+                                                    const float *__restrict__ bias, int Tn, int E,
+                                                    int k, int n_group, int topk_group, int renorm,
+                                                    float scaling, int32_t *__restrict__ idx,
+                                                    float *__restrict__ wout,
+                                                    uint32_t *__restrict__ mask, int mask_words)
+{
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= Tn) return;
+    float s[NV], key[NV];
+    bool ok[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        int e = lane + 64 * i;
+        ok[i] = e < E;
+        float lg = ok[i] ? logits[(size_t)t * E + e] : 0.0f;
+        s[i] = xs_sigmoid(lg);
+        key[i] = (ok[i] && bias) ? __fadd_rn(s[i], bias[e]) : s[i];
+    }
+    if (n_group > 1) {
+        const int gs = E / n_group;
+        float my_score = -__builtin_inff();
+        for (int gidx = 0; gidx < n_group; ++gidx) {
+            // top-2 keys of the group: lane-local, then a wave merge of pairs
+            float b1 = -__builtin_inff(), b2 = -__builtin_inff();
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                int e = lane + 64 * i;
+                if (ok[i] && e / gs == gidx) {
+                    if (key[i] > b1) { b2 = b1; b1 = key[i]; }
+                    else if (key[i] > b2) b2 = key[i];
+                }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                float c1 = __shfl_xor(b1, o, WAVE), c2 = __shfl_xor(b2, o, WAVE);
+                float n1 = fmaxf(b1, c1);
+                float n2 = fmaxf(fminf(b1, c1), fmaxf(b2, c2));
+                b1 = n1;
+                b2 = n2;
+            }
+            if (lane == gidx) my_score = __fadd_rn(b1, b2);
+        }
+        // keep the topk_group best groups (ties -> lower group index)
+        uint64_t keep = 0;
+        for (int rnd = 0; rnd < topk_group; ++rnd) {
+            Cand c;
+            c.key = my_score;
+            c.s = 0.0f;
+            c.e = (lane < n_group && !((keep >> lane) & 1ull)) ? lane : -1;
+            c = wave_best(c);
+            keep |= 1ull << c.e;
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            int e = lane + 64 * i;
+            if (ok[i]) ok[i] = (keep >> (e / gs)) & 1ull;
+        }
+    }
+    int sel_e[16];
+    float sel_s[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        if (j < k) {
+        Cand c;
+        c.e = -1;
+        c.key = 0.0f;
+        c.s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            Cand d;
+            d.e = ok[i] ? lane + 64 * i : -1;
+            d.key = key[i];
+            d.s = s[i];
+            if (better(d, c)) c = d;
+        }
+        c = wave_best(c);
+        sel_e[j] = c.e;
+        sel_s[j] = c.s;
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            if (lane + 64 * i == c.e) ok[i] = false;
+        }
+    }
+    float denom = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        if (j < k) denom = __fadd_rn(denom, sel_s[j]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        if (j < k && lane == j) {
+            float wv = renorm ? __fmul_rn(__fdiv_rn(sel_s[j], denom), scaling) : __fmul_rn(sel_s[j], scaling);
+            idx[(size_t)t * k + j] = sel_e[j];
+            wout[(size_t)t * k + j] = wv;
+            if (mask) atomicOr(&mask[(size_t)sel_e[j] * mask_words + (t >> 5)], 1u << (t & 31));
+        }
+    }
+}
+
+int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,
+                 int64_t n_group, int64_t topk_group, int renorm, float scaling, int32_t *idx,
+                 float *w, uint32_t *mask, int mask_words, hipStream_t st)
+{
+    if (T == 0) return XS_OK;
+    dim3 grid((unsigned)((T + 3) / 4)), block(256);
+    int nv = (int)((E + 63) / 64);
+#define XS_ROUTE(NVV)                                                                       \
+    route_kernel<NVV><<<grid, block, 0, st>>>(logits, bias, (int)T, (int)E, (int)k,         \
+                                              (int)n_group, (int)topk_group, renorm, scaling, \
+                                              idx, w, mask, mask_words)
+    if (nv <= 1) XS_ROUTE(1);
+    else if (nv <= 2) XS_ROUTE(2);
+    else if (nv <= 4) XS_ROUTE(4);
+    else if (nv <= 8) XS_ROUTE(8);
+    else XS_ROUTE(16);
+#undef XS_ROUTE
+    XS_LAUNCH_CHECK();
+    return XS_OK;
+}
+
+int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
+                         int exact, float *logits, hipStream_t st)
+{
+    if (T == 0) return XS_OK;
+    if (exact || dtype == XS_F32) {
+        dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16)), block(256);
+        if (dtype == XS_F32)
+            router_logits_exact_kernel<float><<<grid, block, 0, st>>>((const float *)x, (const float *)wr,
+                                                                      (int)T, (int)E, (int)H, logits);
+        else
+            router_logits_exact_kernel<uint16_t><<<grid, block, 0, st>>>(
+                (const uint16_t *)x, (const uint16_t *)wr, (int)T, (int)E, (int)H, logits);
+    } else {
+        dim3 grid((unsigned)((E + 63) / 64), (unsigned)((T + 63) / 64)), block(256);
+        router_logits_mfma_kernel<<<grid, block, 0, st>>>((const uint16_t *)x, (const uint16_t *)wr,
+                                                          (int)T, (int)E, (int)H, logits);
+    }
+    XS_LAUNCH_CHECK();
+    return XS_OK;
+}
+
+// ---------------------------------------------------- activation quantizers
+// FP8 1x128: each thread owns 8 consecutive columns, 16 lanes share a group.
+template <typename T>
+__global__ __launch_bounds__(256) void quant_act_fp8_kernel(const T *__restrict__ x, int64_t rows,
+                                                            int cols, uint8_t *__restrict__ q,
+                                                            float *__restrict__ s)
+{
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int per_row = cols / 8;
+    const int64_t row = gid / per_row;
+    if (row >= rows) return;   // rows are whole multiples of 16 threads: groups stay aligned
+    const int c8 = (int)(gid - row * per_row);
+    float v[8];
+    load8(x + row * cols + c8 * 8, v);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, WAVE));
+    float inv = amax == 0.0f ? 0.0f : __fdiv_rn(448.0f, amax);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo |= e4m3_encode_sw(__fmul_rn(v[i], inv)) << (8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hi |= e4m3_encode_sw(__fmul_rn(v[4 + i], inv)) << (8 * i);
+    *reinterpret_cast<v2i *>(q + row * cols + c8 * 8) = v2i{(int)lo, (int)hi};
+    if ((c8 & 15) == 0) s[row * (cols / 128) + c8 / 16] = amax == 0.0f ? 1.0f : __fdiv_rn(amax, 448.0f);
+}
+
+// MXFP8 1x32: 4 lanes per block of 32.
+template <typename T>
+__global__ __launch_bounds__(256) void quant_act_mxfp8_kernel(const T *__restrict__ x, int64_t rows,
+                                                              int cols, uint8_t *__restrict__ q,
+                                                              uint8_t *__restrict__ s)
+{
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int per_row = cols / 8;
+    const int64_t row = gid / per_row;
+    if (row >= rows) return;
+    const int c8 = (int)(gid - row * per_row);
+    float v[8];
+    load8(x + row * cols + c8 * 8, v);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, WAVE));
+    int se = mx_exponent(amax, 8);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo |= e4m3_encode_sw(__builtin_ldexpf(v[i], -se)) << (8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hi |= e4m3_encode_sw(__builtin_ldexpf(v[4 + i], -se)) << (8 * i);
+    *reinterpret_cast<v2i *>(q + row * cols + c8 * 8) = v2i{(int)lo, (int)hi};
+    if ((c8 & 3) == 0) s[row * (cols / 32) + c8 / 4] = (uint8_t)(se + 127);
+}
+
+int launch_quant_act(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, void *s,
+                     int mx, hipStream_t st)
+{
+    if (rows == 0) return XS_OK;
+    int64_t threads = rows * (cols / 8);
+    dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+    if (mx) {
+        if (dtype == XS_F32)
+            quant_act_mxfp8_kernel<float><<<grid, block, 0, st>>>((const float *)x, rows, (int)cols, q, (uint8_t *)s);
+        else
+            quant_act_mxfp8_kernel<uint16_t><<<grid, block, 0, st>>>((const uint16_t *)x, rows, (int)cols, q, (uint8_t *)s);
+    } else {
+        if (dtype == XS_F32)
+            quant_act_fp8_kernel<float><<<grid, block, 0, st>>>((const float *)x, rows, (int)cols, q, (float *)s);
+        else
+            quant_act_fp8_kernel<uint16_t><<<grid, block, 0, st>>>((const uint16_t *)x, rows, (int)cols, q, (float *)s);
+    }
+    XS_LAUNCH_CHECK();
+    return XS_OK;
+}
+
+// ------------------------------------------------------- weight quantizers
+// FP8 128x128 block: one 256-thread block per (batch, nb, kb) block.
+template <typename T>
+__global__ __launch_bounds__(256) void quant_weight_fp8_block_kernel(const T *__restrict__ w, int n,
+                                                                     int k, uint8_t *__restrict__ q,
+                                                                     float *__restrict__ s)
+{
+    __shared__ float red[4];
+    const int KB = k / 128, NB = n / 128;
+    const int64_t b = blockIdx.z;
+    const int nb = blockIdx.y, kb = blockIdx.x;
+    const T *wb = w + b * (int64_t)n * k;
+    uint8_t *qb = q + b * (int64_t)n * k;
+    // thread: row = tid / 2 (0..127), 64 columns = 8 chunks of 8
+    const int r = threadIdx.x >> 1, half = threadIdx.x & 1;
+    const int64_t base = (int64_t)(nb * 128 + r) * k + kb * 128 + half * 64;
+    float amax = 0.0f;
+    for (int c = 0; c < 64; c += 8) {
+        float v[8];
+        load8(wb + base + c, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
+    }
+    amax = wave_max(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float inv = amax == 0.0f ? 0.0f : __fdiv_rn(448.0f, amax);
+    for (int c = 0; c < 64; c += 8) {
+        float v[8];
+        load8(wb + base + c, v);
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lo |= e4m3_encode_sw(__fmul_rn(v[i], inv)) << (8 * i);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hi |= e4m3_encode_sw(__fmul_rn(v[4 + i], inv)) << (8 * i);
+        *reinterpret_cast<v2i *>(qb + base + c) = v2i{(int)lo, (int)hi};
+    }
+    if (threadIdx.x == 0) s[(b * NB + nb) * KB + kb] = amax == 0.0f ? 1.0f : __fdiv_rn(amax, 448.0f);
+}
+
+// MXFP4: 4 lanes per 32-element block, each lane packs 8 values into 4 bytes.
+template <typename T>
+__global__ __launch_bounds__(256) void quant_weight_mxfp4_kernel(const T *__restrict__ w, int64_t rows,
+                                                                 int k, uint8_t *__restrict__ q,
+                                                                 uint8_t *__restrict__ s)
+{
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int per_row = k / 8;
+    const int64_t row = gid / per_row;
+    if (row >= rows) return;
+    const int c8 = (int)(gid - row * per_row);
+    float v[8];
+    load8(w + row * k + c8 * 8, v);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, WAVE));
+    int se = mx_exponent(amax, 2);
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) packed |= e2m1_encode_sw(__builtin_ldexpf(v[i], -se)) << (4 * i);
+    *reinterpret_cast<uint32_t *>(q + row * (k / 2) + c8 * 4) = packed;
+    if ((c8 & 3) == 0) s[row * (k / 32) + c8 / 4] = (uint8_t)(se + 127);
+}
+
+}  // namespace xs
+
+using namespace xs;
+
+extern "C" {
+
+int xs_moe_router_logits(const void *x, const void *router_w, int dtype, int64_t T, int64_t E,
+                         int64_t H, int exact, float *logits, void *stream)
+{
+    XS_REQUIRE(x && router_w && logits, "null pointer");
+    XS_REQUIRE(dtype == XS_F32 || dtype == XS_BF16, "unsupported dtype");
+    XS_REQUIRE(T >= 0 && E >= 1 && H >= 128 && H % 128 == 0, "shape mismatch: H %% 128 != 0");
+    return launch_router_logits(x, router_w, dtype, T, E, H, exact, logits, (hipStream_t)stream);
+}
+
+int xs_moe_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,
+                 int64_t n_group, int64_t topk_group, int renormalize, float scaling,
+                 int32_t *idx, float *w, void *stream)
+{
+    XS_REQUIRE(logits && idx && w, "null pointer");
+    XS_REQUIRE(E >= 1 && E <= 1024, "E must be in [1, 1024]");
+    XS_REQUIRE(k >= 1 && k <= 16 && k <= E, "top_k must be in [1, min(16, E)]");
+    if (n_group > 1) {
+        XS_REQUIRE(n_group <= 64 && E % n_group == 0 && E / n_group >= 2,
+                   "n_group must divide E into groups of >= 2 (n_group <= 64)");
+        XS_REQUIRE(topk_group >= 1 && topk_group <= n_group && topk_group * (E / n_group) >= k,
+                   "topk_group must keep at least top_k experts");
+    }
+    return launch_route(logits, bias, T, E, k, n_group, topk_group, renormalize, scaling, idx, w,
+                        nullptr, 0, (hipStream_t)stream);
+}
+
+int xs_quant_act_fp8(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, float *s,
+                     void *stream)
+{
+    XS_REQUIRE(x && q && s, "null pointer");
+    XS_REQUIRE(dtype == XS_F32 || dtype == XS_BF16, "unsupported dtype");
+    XS_REQUIRE(rows >= 0 && cols > 0 && cols % 128 == 0, "cols must be a multiple of 128");
+    return launch_quant_act(x, dtype, rows, cols, q, s, 0, (hipStream_t)stream);
+}
+
+int xs_quant_act_mxfp8(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q,
+                       uint8_t *s, void *stream)
+{
+    XS_REQUIRE(x && q && s, "null pointer");
+    XS_REQUIRE(dtype == XS_F32 || dtype == XS_BF16, "unsupported dtype");
+    XS_REQUIRE(rows >= 0 && cols > 0 && cols % 32 == 0, "cols must be a multiple of 32");
+    return launch_quant_act(x, dtype, rows, cols, q, s, 1, (hipStream_t)stream);
+}
+
+int xs_quant_weight_fp8_block(const void *w, int dtype, int64_t batch, int64_t n, int64_t k,
+                              uint8_t *q, float *s, void *stream)
+{
+    XS_REQUIRE(w && q && s, "null pointer");
+    XS_REQUIRE(dtype == XS_F32 || dtype == XS_BF16, "unsupported dtype");
+    XS_REQUIRE(batch >= 1 && n > 0 && k > 0 && n % 128 == 0 && k % 128 == 0,
+               "n and k must be multiples of 128");
+    XS_REQUIRE(batch <= 65535, "batch too large");
+    dim3 grid((unsigned)(k / 128), (unsigned)(n / 128), (unsigned)batch), block(256);
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == XS_F32)
+        quant_weight_fp8_block_kernel<float><<<grid, block, 0, st>>>((const float *)w, (int)n, (int)k, q, s);
+    else
+        quant_weight_fp8_block_kernel<uint16_t><<<grid, block, 0, st>>>((const uint16_t *)w, (int)n, (int)k, q, s);
+    XS_LAUNCH_CHECK();
+    return XS_OK;
+}
+
+int xs_quant_weight_mxfp4(const void *w, int dtype, int64_t batch, int64_t n, int64_t k,
+                          uint8_t *q, uint8_t *s, void *stream)
+{
+    XS_REQUIRE(w && q && s, "null pointer");
+    XS_REQUIRE(dtype == XS_F32 || dtype == XS_BF16, "unsupported dtype");
+    XS_REQUIRE(batch >= 1 && n > 0 && k > 0 && k % 32 == 0, "k must be a multiple of 32");
+    int64_t rows = batch * n;
+    int64_t threads = rows * (k / 8);
+    dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == XS_F32)
+        quant_weight_mxfp4_kernel<float><<<grid, block, 0, st>>>((const float *)w, rows, (int)k, q, s);
+    else
+        quant_weight_mxfp4_kernel<uint16_t><<<grid, block, 0, st>>>((const uint16_t *)w, rows, (int)k, q, s);
+    XS_LAUNCH_CHECK();
+    return XS_OK;
+}
+
+}  // extern "C"

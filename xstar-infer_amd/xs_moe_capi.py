@@ -1,0 +1,269 @@
+"""ctypes binding of the C ABI in include/xs_moe.h (libxs_moe.so).
+
+This is the binding a Python caller adds to use the library without the
+pybind11 module; the tests and bench.py call the kernels through it.  Device
+buffers are torch CUDA tensors (device memory and streams only); every compute
+call goes to the HIP library.  Importing fails loudly when libxs_moe.so has not
+been built: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "xstar_cpp_py", "libxs_moe.so")
+
+XS_F32, XS_BF16, XS_FP8_E4M3, XS_FP4_E2M1X2, XS_E8M0, XS_I32 = range(6)
+
+P = C.c_void_p
+I64 = C.c_int64
+
+
+class MoeParams(C.Structure):
+    _fields_ = [("T", I64), ("H", I64), ("I", I64), ("E", I64), ("top_k", I64),
+                ("n_group", I64), ("topk_group", I64), ("renormalize", C.c_int),
+                ("routed_scaling", C.c_float), ("x_dtype", C.c_int), ("routed_format", C.c_int),
+                ("has_shared", C.c_int), ("router_exact", C.c_int)]
+
+
+class MoeTensors(C.Structure):
+    _fields_ = [(n, P) for n in (
+        "x", "router_w", "router_bias", "w13", "w13_scale", "w2", "w2_scale",
+        "shared_w13", "shared_w13_scale", "shared_w2", "shared_w2_scale", "out",
+        "logits", "topk_idx", "topk_w", "counts", "offsets", "perm", "inv")]
+
+
+EXPORTS = {
+    "xs_last_error": (C.c_char_p, []),
+    "xs_device_count": (C.c_int, [P]),
+    "xs_malloc": (C.c_int, [P, C.c_size_t]),
+    "xs_free": (C.c_int, [P]),
+    "xs_memcpy_h2d": (C.c_int, [P, P, C.c_size_t]),
+    "xs_memcpy_d2h": (C.c_int, [P, P, C.c_size_t]),
+    "xs_memcpy_d2d": (C.c_int, [P, P, C.c_size_t]),
+    "xs_free_bytes": (C.c_int, [P]),
+    "xs_stream_synchronize": (C.c_int, [P]),
+    "xs_moe_router_logits": (C.c_int, [P, P, C.c_int, I64, I64, I64, C.c_int, P, P]),
+    "xs_moe_route": (C.c_int, [P, P, I64, I64, I64, I64, I64, C.c_int, C.c_float, P, P, P]),
+    "xs_moe_permute_workspace_size": (C.c_size_t, [I64, I64]),
+    "xs_moe_permute": (C.c_int, [P, I64, I64, I64, P, P, P, P, P, C.c_size_t, P]),
+    "xs_quant_act_fp8": (C.c_int, [P, C.c_int, I64, I64, P, P, P]),
+    "xs_quant_act_mxfp8": (C.c_int, [P, C.c_int, I64, I64, P, P, P]),
+    "xs_quant_weight_fp8_block": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P]),
+    "xs_quant_weight_mxfp4": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P]),
+    "xs_gemm_fp8_blockscale_workspace_size": (C.c_size_t, [I64, I64]),
+    "xs_gemm_fp8_blockscale": (C.c_int, [P, P, P, I64, I64, I64, P, P, C.c_size_t, P]),
+    "xs_moe_workspace_size": (C.c_size_t, [P]),
+    "xs_moe_forward": (C.c_int, [P, P, P, C.c_size_t, P]),
+    "xs_moe_profile_enable": (C.c_int, [C.c_int]),
+    "xs_moe_profile_read": (C.c_int, [P, C.c_int, P]),
+}
+
+STAGES = ("router_logits", "route", "act_quant", "permute", "gemm_gate_up", "gemm_down", "combine")
+
+
+def profile_enable(on=True):
+    check(lib().xs_moe_profile_enable(int(on)))
+
+
+def profile_read():
+    """-> (dict stage -> summed ms, number of forwards) since the last read."""
+    ms = (C.c_float * len(STAGES))()
+    n = C.c_int(0)
+    check(lib().xs_moe_profile_read(ms, len(STAGES), C.byref(n)))
+    return {s: float(ms[i]) for i, s in enumerate(STAGES)}, n.value
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python xstar-infer_amd/build.py`")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in EXPORTS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+class XsError(RuntimeError):
+    pass
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise XsError(f"xs_moe error {rc}: {lib().xs_last_error().decode()}")
+
+
+# ---------------------------------------------------------------- torch glue
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream():
+    import torch
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dtype_code(t):
+    import torch
+    if t.dtype == torch.bfloat16:
+        return XS_BF16
+    if t.dtype == torch.float32:
+        return XS_F32
+    raise XsError("unsupported dtype")
+
+
+def _u8(t):
+    """Raw-byte view of a quantized tensor (uint8 or torch float8 / float4 dtypes)."""
+    import torch
+    return t if t.dtype == torch.uint8 else t.view(torch.uint8)
+
+
+def router_logits(x, router_w, exact=False):
+    import torch
+    T, H = x.shape
+    E = router_w.shape[0]
+    out = torch.empty((T, E), dtype=torch.float32, device=x.device)
+    check(lib().xs_moe_router_logits(_ptr(x), _ptr(router_w), _dtype_code(x), T, E, H, int(exact),
+                                     _ptr(out), _stream()))
+    return out
+
+
+def route(logits, bias, k, n_group=1, topk_group=1, renormalize=True, scaling=1.0):
+    import torch
+    T, E = logits.shape
+    idx = torch.empty((T, k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((T, k), dtype=torch.float32, device=logits.device)
+    check(lib().xs_moe_route(_ptr(logits), _ptr(bias), T, E, k, n_group, topk_group,
+                             int(renormalize), float(scaling), _ptr(idx), _ptr(w), _stream()))
+    return idx, w
+
+
+def permute(idx, E):
+    import torch
+    T, k = idx.shape
+    dev = idx.device
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(T * k, dtype=torch.int32, device=dev)
+    inv = torch.empty(T * k, dtype=torch.int32, device=dev)
+    nb = lib().xs_moe_permute_workspace_size(T, E)
+    ws = torch.empty(max(nb, 256), dtype=torch.uint8, device=dev)
+    check(lib().xs_moe_permute(_ptr(idx), T, E, k, _ptr(counts), _ptr(offsets), _ptr(perm), _ptr(inv),
+                               _ptr(ws), ws.numel(), _stream()))
+    return counts, offsets, perm, inv
+
+
+def quant_act_fp8(x):
+    import torch
+    rows, cols = x.shape
+    q = torch.empty((rows, cols), dtype=torch.uint8, device=x.device)
+    s = torch.empty((rows, cols // 128), dtype=torch.float32, device=x.device)
+    check(lib().xs_quant_act_fp8(_ptr(x), _dtype_code(x), rows, cols, _ptr(q), _ptr(s), _stream()))
+    return q, s
+
+
+def quant_act_mxfp8(x):
+    import torch
+    rows, cols = x.shape
+    q = torch.empty((rows, cols), dtype=torch.uint8, device=x.device)
+    s = torch.empty((rows, cols // 32), dtype=torch.uint8, device=x.device)
+    check(lib().xs_quant_act_mxfp8(_ptr(x), _dtype_code(x), rows, cols, _ptr(q), _ptr(s), _stream()))
+    return q, s
+
+
+def quant_weight_fp8_block(w):
+    """w [..., n, k] (bf16/f32, CUDA) -> (q uint8 [..., n, k], s f32 [..., n/128, k/128])."""
+    import torch
+    *lead, n, k = w.shape
+    b = 1
+    for d in lead:
+        b *= d
+    q = torch.empty(w.shape, dtype=torch.uint8, device=w.device)
+    s = torch.empty((*lead, n // 128, k // 128), dtype=torch.float32, device=w.device)
+    check(lib().xs_quant_weight_fp8_block(_ptr(w), _dtype_code(w), b, n, k, _ptr(q), _ptr(s), _stream()))
+    return q, s
+
+
+def quant_weight_mxfp4(w):
+    import torch
+    *lead, n, k = w.shape
+    b = 1
+    for d in lead:
+        b *= d
+    q = torch.empty((*lead, n, k // 2), dtype=torch.uint8, device=w.device)
+    s = torch.empty((*lead, n, k // 32), dtype=torch.uint8, device=w.device)
+    check(lib().xs_quant_weight_mxfp4(_ptr(w), _dtype_code(w), b, n, k, _ptr(q), _ptr(s), _stream()))
+    return q, s
+
+
+def gemm_fp8_blockscale(a, bq, bs, out=None, workspace=None):
+    import torch
+    M, K = a.shape
+    N = bq.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    nb = lib().xs_gemm_fp8_blockscale_workspace_size(M, K)
+    if workspace is None:
+        workspace = torch.empty(nb, dtype=torch.uint8, device=a.device)
+    check(lib().xs_gemm_fp8_blockscale(_ptr(a), _ptr(_u8(bq)), _ptr(bs), M, N, K, _ptr(out),
+                                       _ptr(workspace), workspace.numel(), _stream()))
+    return out
+
+
+class MoeLayer:
+    """Holds weights (device tensors) and calls xs_moe_forward."""
+
+    def __init__(self, router_w, w13, w13_scale, w2, w2_scale, top_k, router_bias=None,
+                 shared=None, routed_format=XS_FP8_E4M3, n_group=1, topk_group=1,
+                 renormalize=True, routed_scaling=1.0, router_exact=False):
+        self.router_w, self.router_bias = router_w, router_bias
+        self.w13, self.w13_scale, self.w2, self.w2_scale = _u8(w13), w13_scale, _u8(w2), w2_scale
+        self.shared = None if shared is None else (_u8(shared[0]), shared[1], _u8(shared[2]), shared[3])
+        self.top_k, self.routed_format = top_k, routed_format
+        self.n_group, self.topk_group = n_group, topk_group
+        self.renormalize, self.routed_scaling, self.router_exact = renormalize, routed_scaling, router_exact
+        self.E, self.H = router_w.shape
+        self.I = w2.shape[-1] * (2 if routed_format == XS_FP4_E2M1X2 else 1)
+        self._ws = None
+
+    def params(self, T, x_dtype):
+        return MoeParams(T, self.H, self.I, self.E, self.top_k, self.n_group, self.topk_group,
+                         int(self.renormalize), float(self.routed_scaling), x_dtype,
+                         self.routed_format, int(self.shared is not None), int(self.router_exact))
+
+    def workspace(self, T, x_dtype, device):
+        import torch
+        p = self.params(T, x_dtype)
+        nb = lib().xs_moe_workspace_size(C.byref(p))
+        if nb == 0:
+            check(1)
+        if self._ws is None or self._ws.numel() < nb:
+            self._ws = torch.empty(nb, dtype=torch.uint8, device=device)
+        return self._ws
+
+    def forward(self, x, out=None, debug=None):
+        """debug: optional dict of preallocated device tensors with keys among
+        logits, topk_idx, topk_w, counts, offsets, perm, inv."""
+        import torch
+        T = x.shape[0]
+        xd = _dtype_code(x)
+        if out is None:
+            out = torch.empty((T, self.H), dtype=x.dtype, device=x.device)
+        ws = self.workspace(T, xd, x.device)
+        p = self.params(T, xd)
+        sh = self.shared or (None, None, None, None)
+        d = debug or {}
+        t = MoeTensors(_ptr(x), _ptr(self.router_w), _ptr(self.router_bias), _ptr(self.w13),
+                       _ptr(self.w13_scale), _ptr(self.w2), _ptr(self.w2_scale), _ptr(sh[0]),
+                       _ptr(sh[1]), _ptr(sh[2]), _ptr(sh[3]), _ptr(out),
+                       *[_ptr(d.get(n)) for n in ("logits", "topk_idx", "topk_w", "counts",
+                                                 "offsets", "perm", "inv")])
+        check(lib().xs_moe_forward(C.byref(p), C.byref(t), _ptr(ws), ws.numel(), _stream()))
+        return out
