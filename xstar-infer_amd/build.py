@@ -24,6 +24,8 @@ HIP_FLAGS = [
     # packed FP32 instructions are kept out of every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
+    # MFMA results in VGPRs: the FP8 kernels fold every partial product with VALU FMAs
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

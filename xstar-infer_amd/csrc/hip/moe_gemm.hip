@@ -7,12 +7,13 @@
 //
 //   * rows of one expert are contiguous positions of the permutation; a block
 //     owns BM of them and a 256-wide slab of output columns;
-//   * K advances 128 at a time (one FP8 scale block) through a two-stage LDS
-//     ring (16-byte chunks, XOR-swizzled so the MFMA operand reads are
-//     bank-conflict free);
+//   * K advances 128 at a time (one FP8 scale block).  Operand tiles move
+//     global -> LDS with global_load_lds_dwordx4 (no VGPR staging) into a ring
+//     of NST stages, issued NST-1 steps ahead of use; 16-byte chunks are
+//     XOR-swizzled per row so the MFMA operand reads are bank-conflict free;
 //   * FP8: each 16x16x128 MFMA (v_mfma_f32_16x16x128_f8f6f4) yields the
-//     partial sum of one 128-K block, which is folded into the f32 accumulator
-//     with the product of the activation row scale and the weight block scale;
+//     partial sum of one 128-K block, folded into the f32 accumulator with the
+//     product of the activation row scale and the weight block scale;
 //   * MXFP4: v_mfma_scale_f32_16x16x128_f8f6f4 applies the per-32 e8m0 scales
 //     of both operands in hardware and accumulates across all of K;
 //   * gate_up: the 256 columns are 128 gate rows + the matching 128 up rows of
@@ -24,14 +25,27 @@
 
 namespace xs {
 
-template <int BM>
-struct Shape {
+template <int BM, bool FP4>
+struct Cfg {
     static constexpr int WM = BM >= 128 ? 2 : 1;
     static constexpr int WN = 4 / WM;
     static constexpr int TM = BM / WM;          // wave rows
     static constexpr int TN = 256 / WN;         // wave columns
     static constexpr int MI = TM / 16;
     static constexpr int NJ = TN / 16;
+    static constexpr int NST = BM <= 32 ? 4 : 3;                 // LDS ring stages
+    static constexpr int BROW = FP4 ? 64 : 128;                  // B bytes per row per K step
+    static constexpr int A_BYTES = BM * 128;
+    static constexpr int B_BYTES = 256 * BROW;
+    static constexpr int SA_BYTES = 512;                         // 128 row scales (f32 or 4 x e8m0)
+    static constexpr int SB_BYTES = FP4 ? 1024 : 0;              // 256 column scale words (MXFP4)
+    static constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES + SB_BYTES;
+    static constexpr int A_INSTR = A_BYTES / 1024;               // 1 KB per wave-wide DMA
+    static constexpr int NA_W = A_INSTR >= 4 ? A_INSTR / 4 : 1;  // per wave (dummies pad)
+    static constexpr int NB_W = B_BYTES / 1024 / 4;
+    static constexpr int NS_W = FP4 ? 2 : 1;                     // row-scale (+ column-scale) dwords
+    static constexpr int PER_STAGE = NA_W + NB_W + NS_W;         // DMA instructions per wave per stage
+    static constexpr int TRASH = 1024;                           // target of padding DMAs
 };
 
 // LDS row swizzles: 16-byte chunk c of row r lives at physical chunk c ^ f(r).
@@ -39,6 +53,31 @@ __device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }
 __device__ __forceinline__ int swz4(int r, int c) { return c ^ ((r >> 2) & 3); }   // 64-byte rows
 
 __device__ __forceinline__ v8i cat(v4i a, v4i b) { return v8i{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}; }
+
+__device__ __forceinline__ uint32_t lds_off(const void *p)
+{
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// Wave-wide DMA global -> LDS: lane i's 16 (or 4) bytes land at lds + 16*i (4*i).
+// The LDS base goes through M0 and must be wave-uniform.
+// M0 is written only inside these statements; compiled kernels here use M0 for
+// nothing else.
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds)
+{
+    const uint32_t s = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(s) : "memory");
+}
+__device__ __forceinline__ void dma4(const void *g, uint32_t lds)
+{
+    const uint32_t s = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(s) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // Locate the tile of blockIdx.y: expert e and first row m0 within the expert.
 __device__ __forceinline__ bool find_tile(const GemmArgs &a, int &e, int &m0, int &rows)
@@ -60,19 +99,12 @@ __device__ __forceinline__ bool find_tile(const GemmArgs &a, int &e, int &m0, in
 template <int BM, bool GATEUP, bool FP4>
 __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
 {
-    using S = Shape<BM>;
-    constexpr int BROW = FP4 ? 64 : 128;          // bytes per B row per K step
-    constexpr int A_BYTES = BM * 128, B_BYTES = 256 * BROW;
-    constexpr int STAGE = A_BYTES + B_BYTES;
-    constexpr int NA = (BM * 8 + 255) / 256;      // A chunks per thread
-    constexpr int NB = B_BYTES / 16 / 256;        // B chunks per thread
-
+    using S = Cfg<BM, FP4>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int KB = a.K / 128;
-    uint8_t *stage0 = smem;
-    float *sA = reinterpret_cast<float *>(smem + 2 * STAGE);          // [KB][BM] (FP4: u32 words)
-    float *sB = sA + KB * BM;                                          // FP8: [2][KB]; FP4: [KB][256] u32
-    float *red = sB + (FP4 ? KB * 256 : 2 * KB);                       // [WN][BM]
+    uint8_t *trash = smem + S::NST * S::STAGE;
+    float *sB = reinterpret_cast<float *>(trash + S::TRASH);          // FP8: [2][KB]
+    float *red = sB + 2 * KB;                                         // [WN][BM]
 
     int e, m0, rows;
     if (!find_tile(a, e, m0, rows)) return;
@@ -101,52 +133,45 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
         return a.row_token ? a.row_token[p] : p;
     };
 
-    // ---- per-thread global source pointers (fixed across K) ----
-    const uint8_t *ga[NA];
-    int la[NA];
+    // ---- per-lane DMA sources (fixed across K; the K offset is added per step) ----
+    const uint8_t *gA[S::NA_W];
+    uint32_t lA[S::NA_W];
 #pragma unroll
-    for (int u = 0; u < NA; ++u) {
-        int q = tid + 256 * u;
-        int r = q >> 3, c = q & 7;
-        ga[u] = a.A + (size_t)arow_of(r < BM ? r : 0) * a.K + c * 16;
-        la[u] = (q < BM * 8) ? r * 128 + swz8(r, c) * 16 : -1;
+    for (int u = 0; u < S::NA_W; ++u) {
+        const int q = wave + 4 * u;                    // wave-wide instruction index
+        const int p = 64 * q + lane;                   // LDS chunk written by this lane
+        const int r = p >> 3, c = swz8(r, p & 7);
+        const bool real = q < S::A_INSTR;
+        gA[u] = a.A + (size_t)arow_of(real ? r : 0) * a.K + c * 16;
+        lA[u] = real ? (uint32_t)(64 * q * 16) : 0xFFFFFFFFu;
     }
-    const uint8_t *gb[NB];
-    int lb[NB];
+    const uint8_t *gB[S::NB_W];
 #pragma unroll
-    for (int u = 0; u < NB; ++u) {
-        int q = tid + 256 * u;
+    for (int u = 0; u < S::NB_W; ++u) {
+        const int q = wave + 4 * u;
+        const int p = 64 * q + lane;
         if (FP4) {
-            int r = q >> 2, c = q & 3;
-            gb[u] = Bexp + (size_t)brow_of(r) * (a.K / 2) + c * 16;
-            lb[u] = r * 64 + swz4(r, c) * 16;
+            const int vr = p >> 2, c = swz4(vr, p & 3);
+            gB[u] = Bexp + (size_t)brow_of(vr) * (a.K / 2) + c * 16;
         } else {
-            int r = q >> 3, c = q & 7;
-            gb[u] = Bexp + (size_t)brow_of(r) * a.K + c * 16;
-            lb[u] = r * 128 + swz8(r, c) * 16;
+            const int vr = p >> 3, c = swz8(vr, p & 7);
+            gB[u] = Bexp + (size_t)brow_of(vr) * a.K + c * 16;
         }
     }
+    // row scales: waves 0/1 load rows 64w + lane (waves beyond BM target trash)
+    const bool sa_real = wave * 64 < BM;
+    const uint8_t *gSA;
+    if (FP4)
+        gSA = reinterpret_cast<const uint8_t *>(a.As) + (size_t)arow_of(sa_real ? wave * 64 + lane : 0) * (a.K / 32);
+    else
+        gSA = reinterpret_cast<const uint8_t *>(a.As) + (size_t)arow_of(sa_real ? wave * 64 + lane : 0) * KB * 4;
+    const uint8_t *gSB = nullptr;
+    if (FP4)
+        gSB = reinterpret_cast<const uint8_t *>(a.Bs) + (size_t)e * Nrows * (a.K / 32) +
+              (size_t)brow_of(wave * 64 + lane) * (a.K / 32);
 
-    // ---- scales for the whole tile ----
-    if (FP4) {
-        const uint8_t *As8 = reinterpret_cast<const uint8_t *>(a.As);
-        uint32_t *sAw = reinterpret_cast<uint32_t *>(sA);
-        for (int q = tid; q < KB * BM; q += 256) {
-            int r = q % BM, kb = q / BM;
-            sAw[q] = *reinterpret_cast<const uint32_t *>(As8 + (size_t)arow_of(r) * (a.K / 32) + kb * 4);
-        }
-        const uint8_t *Bs8 = reinterpret_cast<const uint8_t *>(a.Bs) + (size_t)e * Nrows * (a.K / 32);
-        uint32_t *sBw = reinterpret_cast<uint32_t *>(sB);
-        for (int q = tid; q < KB * 256; q += 256) {
-            int vr = q & 255, kb = q >> 8;
-            sBw[q] = *reinterpret_cast<const uint32_t *>(Bs8 + (size_t)brow_of(vr) * (a.K / 32) + kb * 4);
-        }
-    } else {
-        const float *Asf = reinterpret_cast<const float *>(a.As);
-        for (int q = tid; q < KB * BM; q += 256) {
-            int r = q % BM, kb = q / BM;
-            sA[q] = Asf[(size_t)arow_of(r) * KB + kb];
-        }
+    // ---- FP8 weight block scales for the whole tile ----
+    if (!FP4) {
         const float *Bsf = shared ? a.Bssh : reinterpret_cast<const float *>(a.Bs) + (size_t)e * (Nrows / 128) * KB;
         for (int q = tid; q < 2 * KB; q += 256) {
             int b = q / KB, kb = q % KB;
@@ -157,38 +182,46 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
         }
     }
 
+    const uint32_t smem_base = lds_off(smem);
+    const uint32_t trash_lds = __builtin_amdgcn_readfirstlane(lds_off(trash));
+    // Issue the DMAs of K step kb into ring stage kb % NST.  Steps past the end
+    // reload the last step (the stage is never read again): counts stay uniform.
+    auto issue = [&](int kb) {
+        const int kk = kb < KB ? kb : KB - 1;
+        const uint32_t st = __builtin_amdgcn_readfirstlane(smem_base + (uint32_t)((kb % S::NST) * S::STAGE));
+#pragma unroll
+        for (int u = 0; u < S::NA_W; ++u) {
+            const uint32_t dst = lA[u] == 0xFFFFFFFFu ? trash_lds : st + __builtin_amdgcn_readfirstlane(lA[u]);
+            dma16(gA[u] + (size_t)kk * 128, dst);
+        }
+#pragma unroll
+        for (int u = 0; u < S::NB_W; ++u)
+            dma16(gB[u] + (size_t)kk * S::BROW, st + S::A_BYTES + (uint32_t)((wave + 4 * u) * 1024));
+        if (FP4) {
+            dma4(gSA + (size_t)kk * 4, sa_real ? st + S::A_BYTES + S::B_BYTES + wave * 256 : trash_lds);
+            dma4(gSB + (size_t)kk * 4, st + S::A_BYTES + S::B_BYTES + S::SA_BYTES + wave * 256);
+        } else {
+            dma4(gSA + (size_t)kk * 4, sa_real ? st + S::A_BYTES + S::B_BYTES + wave * 256 : trash_lds);
+        }
+    };
+
     v4f acc[S::MI][S::NJ];
 #pragma unroll
     for (int i = 0; i < S::MI; ++i)
 #pragma unroll
         for (int j = 0; j < S::NJ; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    v4i ra[NA], rb[NB];
-    auto gload = [&](int kb) {
+    __syncthreads();   // sB visible; all address loads done before the DMA stream starts
 #pragma unroll
-        for (int u = 0; u < NA; ++u)
-            if (la[u] >= 0) ra[u] = *reinterpret_cast<const v4i *>(ga[u] + (size_t)kb * 128);
-#pragma unroll
-        for (int u = 0; u < NB; ++u) rb[u] = *reinterpret_cast<const v4i *>(gb[u] + (size_t)kb * BROW);
-    };
-    auto sstore = [&](int buf) {
-        uint8_t *st = stage0 + buf * STAGE;
-#pragma unroll
-        for (int u = 0; u < NA; ++u)
-            if (la[u] >= 0) *reinterpret_cast<v4i *>(st + la[u]) = ra[u];
-#pragma unroll
-        for (int u = 0; u < NB; ++u) *reinterpret_cast<v4i *>(st + A_BYTES + lb[u]) = rb[u];
-    };
-
-    gload(0);
-    sstore(0);
-    __syncthreads();
+    for (int s = 0; s < S::NST - 1; ++s) issue(s);
 
     for (int kb = 0; kb < KB; ++kb) {
-        const int buf = kb & 1;
-        if (kb + 1 < KB) gload(kb + 1);
-        const uint8_t *sa_ = stage0 + buf * STAGE;
-        const uint8_t *sb_ = sa_ + A_BYTES;
+        wait_vmcnt<(S::NST - 2) * S::PER_STAGE>();   // this wave's DMAs for step kb have landed
+        __syncthreads();                             // ... and every other wave's
+        issue(kb + S::NST - 1);                      // refills the stage consumed at kb - 1
+        const uint8_t *sa_ = smem + (kb % S::NST) * S::STAGE;
+        const uint8_t *sb_ = sa_ + S::A_BYTES;
+        const uint8_t *ssc = sb_ + S::B_BYTES;
 
         // Operand layout of v_mfma_*_16x16x128_f8f6f4 (gfx950): for an FP8
         // operand, lane 16g + r holds row r with K = [16g, 16g+16) in bytes 0..15
@@ -206,8 +239,8 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
             afr[i] = cat(lo, hi);
         }
         if (FP4) {
-            const uint32_t *sAw = reinterpret_cast<const uint32_t *>(sA) + kb * BM;
-            const uint32_t *sBw = reinterpret_cast<const uint32_t *>(sB) + kb * 256;
+            const uint32_t *sAw = reinterpret_cast<const uint32_t *>(ssc);
+            const uint32_t *sBw = reinterpret_cast<const uint32_t *>(ssc + S::SA_BYTES);
             int sa_s[S::MI];
 #pragma unroll
             for (int i = 0; i < S::MI; ++i) sa_s[i] = (int)((sAw[wm * S::TM + 16 * i + l16] >> (8 * g)) & 0xffu);
@@ -223,36 +256,52 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
                                                                                 sa_s[i], 0, sb_s);
             }
         } else {
-            float csc[S::MI][4][2];
-            const float sb0 = sB[kb], sb1 = sB[KB + kb];
+            const float *sAk = reinterpret_cast<const float *>(ssc);
+            // weight block scales: gate_up uses block 0 (gate) for even subtiles and
+            // block 1 (up) for odd ones; down uses the wave's own 128-column block
+            const float sb0 = GATEUP ? sB[kb] : sB[((wn * S::TN) >> 7) * KB + kb];
+            const float sb1 = GATEUP ? sB[KB + kb] : sb0;
+            float c0[S::MI][4], c1[S::MI][4];
 #pragma unroll
             for (int i = 0; i < S::MI; ++i) {
-                v4f sa4 = *reinterpret_cast<const v4f *>(sA + kb * BM + wm * S::TM + 16 * i + 4 * g);
+                v4f sa4 = *reinterpret_cast<const v4f *>(sAk + wm * S::TM + 16 * i + 4 * g);
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    csc[i][v][0] = sa4[v] * sb0;
-                    csc[i][v][1] = sa4[v] * sb1;
+                    c0[i][v] = sa4[v] * sb0;
+                    c1[i][v] = sa4[v] * sb1;
                 }
             }
+            // Software pipeline over the (j, i) subtiles: the partial product of
+            // subtile n is folded after MFMA n + PD has been issued, so the
+            // matrix pipe never waits for the VALU fold (and vice versa).
+            constexpr int NSUB = S::NJ * S::MI, PD = 2;
+            v4f pr[PD + 1];
+            v8i bfr;
 #pragma unroll
-            for (int j = 0; j < S::NJ; ++j) {
-                int vr = wn * S::TN + 16 * j + l16;
-                v4i lo = *reinterpret_cast<const v4i *>(sb_ + vr * 128 + swz8(vr, g) * 16);
-                v4i hi = *reinterpret_cast<const v4i *>(sb_ + vr * 128 + swz8(vr, g + 4) * 16);
-                v8i bfr = cat(lo, hi);
-                const int blk = GATEUP ? (j & 1) : ((wn * S::TN + 16 * j) >> 7);
+            for (int n = 0; n < NSUB + PD; ++n) {
+                if (n < NSUB) {
+                    const int j = n / S::MI, i = n % S::MI;
+                    if (i == 0) {
+                        int vr = wn * S::TN + 16 * j + l16;
+                        v4i lo = *reinterpret_cast<const v4i *>(sb_ + vr * 128 + swz8(vr, g) * 16);
+                        v4i hi = *reinterpret_cast<const v4i *>(sb_ + vr * 128 + swz8(vr, g + 4) * 16);
+                        bfr = cat(lo, hi);
+                    }
+                    pr[n % (PD + 1)] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        afr[i], bfr, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
+                }
+                if (n >= PD) {
+                    const int m = n - PD, j = m / S::MI, i = m % S::MI;
+                    const v4f p = pr[m % (PD + 1)];
 #pragma unroll
-                for (int i = 0; i < S::MI; ++i) {
-                    v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(afr[i], bfr, v4f{0.f, 0.f, 0.f, 0.f},
-                                                                             0, 0, 0, 0, 0, 0);
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], csc[i][v][blk], acc[i][j][v]);
+                    for (int v = 0; v < 4; ++v)
+                        acc[i][j][v] = __builtin_fmaf(p[v], (GATEUP && (j & 1)) ? c1[i][v] : c0[i][v], acc[i][j][v]);
                 }
             }
         }
-        if (kb + 1 < KB) sstore(buf ^ 1);
-        __syncthreads();
     }
+    wait_vmcnt<0>();   // drain the padding DMAs before the stages are reused
+    __syncthreads();
 
     // ------------------------------------------------------------ epilogue
     if (GATEUP) {
@@ -296,9 +345,9 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
                         float x0 = fminf(fmaxf(act[i][p][v] * inv, -448.f), 448.f);
                         float x1 = fminf(fmaxf(act[i][p + 1][v] * inv, -448.f), 448.f);
                         uint32_t pk = e4m3_pack2_hw(x0, x1);
-                        int c0 = (wn * NP + p) * 16 + l16;
-                        stg[r * 128 + c0] = (uint8_t)(pk & 0xff);
-                        stg[r * 128 + c0 + 16] = (uint8_t)(pk >> 8);
+                        int cc = (wn * NP + p) * 16 + l16;
+                        stg[r * 128 + cc] = (uint8_t)(pk & 0xff);
+                        stg[r * 128 + cc + 16] = (uint8_t)(pk >> 8);
                     }
                 }
             __syncthreads();
@@ -326,9 +375,9 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
                         float x0 = fminf(fmaxf(__builtin_ldexpf(act[i][p][v], -se), -448.f), 448.f);
                         float x1 = fminf(fmaxf(__builtin_ldexpf(act[i][p + 1][v], -se), -448.f), 448.f);
                         uint32_t pk = e4m3_pack2_hw(x0, x1);
-                        int c0 = (wn * NP + p) * 16 + l16;
-                        stg[r * 128 + c0] = (uint8_t)(pk & 0xff);
-                        stg[r * 128 + c0 + 16] = (uint8_t)(pk >> 8);
+                        int cc = (wn * NP + p) * 16 + l16;
+                        stg[r * 128 + cc] = (uint8_t)(pk & 0xff);
+                        stg[r * 128 + cc + 16] = (uint8_t)(pk >> 8);
                         if (l16 == 0 && r < rows)
                             Cs8[(size_t)(pos0 + r) * (a.N / 32) + (n0 + (wn * NP + p) * 16) / 32] = (uint8_t)(se + 127);
                     }
@@ -366,12 +415,12 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
 template <int BM, bool GATEUP, bool FP4>
 static size_t gemm_smem_bytes(int K)
 {
-    using S = Shape<BM>;
-    const int KB = K / 128;
-    size_t stage = (size_t)BM * 128 + 256 * (FP4 ? 64 : 128);
-    size_t b = 2 * stage + 4 * (size_t)KB * BM + 4 * (FP4 ? (size_t)KB * 256 : 2 * (size_t)KB) + 4 * (size_t)S::WN * BM;
+    using S = Cfg<BM, FP4>;
+    const size_t KB = (size_t)K / 128;
+    size_t b = (size_t)S::NST * S::STAGE + S::TRASH + 4 * 2 * KB + 4 * (size_t)S::WN * BM;
     size_t epi = GATEUP ? (size_t)BM * 128 : (size_t)BM * 512;
-    return b > epi ? b : epi;   // staging reuses the stage buffers, which precede the scales
+    if (epi > (size_t)S::NST * S::STAGE) b += epi;   // staging reuses the ring when it fits
+    return b;
 }
 
 template <int BM, bool GATEUP, bool FP4>
