@@ -57,7 +57,7 @@ static WsLayout layout(const xs_moe_params *p)
     WsLayout L = {};
     size_t o = 0;
     auto take = [&](size_t &field, size_t bytes) { field = o; o += al(bytes); };
-    take(L.logits, 4 * T * E);
+    take(L.logits, 4 * T * E * (size_t)router_logits_splits(p->T, p->H, p->router_exact, p->x_dtype));
     take(L.idx, 4 * S);
     take(L.w, 4 * S);
     take(L.mask, 4 * W * E);
@@ -135,11 +135,12 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     if ((rc = prof_mark(0, st))) return rc;
     rc = launch_mask_clear(mask, (int64_t)Wd * E, st);
     if (rc) return rc;
-    rc = launch_router_logits(t->x, t->router_w, p->x_dtype, T, E, H, p->router_exact, logits, st);
+    const int nsplit = router_logits_splits(T, H, p->router_exact, p->x_dtype);
+    rc = launch_router_logits(t->x, t->router_w, p->x_dtype, T, E, H, p->router_exact, logits, nsplit, st);
     if (rc) return rc;
     if ((rc = prof_mark(1, st))) return rc;
     rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
-                      p->routed_scaling, idx, w, mask, Wd, st);
+                      p->routed_scaling, idx, w, mask, Wd, nsplit, t->logits, st);
     if (rc) return rc;
     // 2. activation quantization (once per token, gathered by the GEMMs)
     if ((rc = prof_mark(2, st))) return rc;
@@ -261,7 +262,6 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         if (dst && bytes) XS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, st));
         return XS_OK;
     };
-    if ((rc = cp(t->logits, logits, 4 * (size_t)(T * E)))) return rc;
     if ((rc = cp(t->topk_idx, idx, 4 * (size_t)S))) return rc;
     if ((rc = cp(t->topk_w, w, 4 * (size_t)S))) return rc;
     if ((rc = cp(t->counts, po.counts, 4 * (size_t)E))) return rc;

@@ -45,11 +45,17 @@ __device__ __forceinline__ void store8(float *p, const float *v)
 }
 
 // ---- launchers (stream-ordered, no synchronisation) ----
+// Number of K slices the bf16 MFMA router uses for T tokens (1 = no split).
+int router_logits_splits(int64_t T, int64_t H, int exact, int dtype);
+// Writes nsplit partial logit slices [nsplit][T][E] (nsplit = 1: the logits).
 int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
-                         int exact, float *logits, hipStream_t st);
+                         int exact, float *logits, int nsplit, hipStream_t st);
+// Routes on the sum (in slice order) of nsplit partial logit slices; writes the
+// summed logits to logits_out when it is not NULL.
 int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,
                  int64_t n_group, int64_t topk_group, int renorm, float scaling, int32_t *idx,
-                 float *w, uint32_t *mask, int mask_words, hipStream_t st);
+                 float *w, uint32_t *mask, int mask_words, int nsplit, float *logits_out,
+                 hipStream_t st);
 int launch_quant_act(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, void *s,
                      int mx, hipStream_t st);
 

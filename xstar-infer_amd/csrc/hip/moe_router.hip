@@ -12,6 +12,9 @@
 
 namespace xs {
 
+// Upper bound on the K slices of the split-K router GEMM.
+static constexpr int kMaxSplits = 16;
+
 // ------------------------------------------------------------ exact logits
 // 256 threads = 16 tokens x 16 experts; k-chunks of 64 staged in LDS; each
 // thread owns one (t, e) and accumulates sequentially in k with separately
@@ -45,51 +48,65 @@ __global__ __launch_bounds__(256) void router_logits_exact_kernel(const T *__res
 }
 
 // ------------------------------------------------------------- MFMA logits
-// Block = 4 waves, tile 64 tokens x 64 experts.  Wave w owns tokens
-// [16w, 16w+16) against all 64 experts (four 16x16 output subtiles).  Operands
-// come straight from global memory (16 B per lane per MFMA; the router weight
-// is 2 MB and stays L2-resident).  MFMA 16x16x32 bf16: lane l supplies row
-// (l % 16) and k-slice (l / 16) of 8 elements for both A and B, so the
+// Block = 2 x 2 waves; a wave owns MT x NT subtiles of 16 tokens x 16 experts
+// over one K slice (blockIdx.z; several slices = split-K for few tokens, the
+// partials are summed in slice order by the route kernel, so the result does
+// not depend on scheduling).  Operands come straight from global memory, 16 B
+// per lane per MFMA, a whole 128-wide K step in flight at once (the router
+// weight is 2 MB and stays L2-resident).  MFMA 16x16x32 bf16: lane l supplies
+// row (l % 16) and k-slice (l / 16) of 8 elements for both A and B, so the
 // k-pairing is consistent whatever the hardware's internal k order.
+template <int MT, int NT>
 __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t *__restrict__ x,
                                                                  const uint16_t *__restrict__ wr,
-                                                                 int Tn, int E, int H,
-                                                                 float *__restrict__ logits)
+                                                                 int Tn, int E, int H, int klen,
+                                                                 float *__restrict__ part)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int t0 = blockIdx.y * 64 + wave * 16, e0 = blockIdx.x * 64;
-    const int trow = min(t0 + r, Tn - 1);
-    const v8bf *xa = reinterpret_cast<const v8bf *>(x + (size_t)trow * H + g * 8);
-    const v8bf *wb[4];
+    const int wm = wave >> 1, wn = wave & 1;
+    const int t0 = blockIdx.y * (32 * MT) + wm * 16 * MT, e0 = blockIdx.x * (32 * NT) + wn * 16 * NT;
+    const int kbeg = blockIdx.z * klen;
+    const v8bf *xa[MT];
+    const v8bf *wb[NT];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        wb[j] = reinterpret_cast<const v8bf *>(wr + (size_t)min(e0 + 16 * j + r, E - 1) * H + g * 8);
-    v4f acc[4] = {};
-    for (int k = 0; k < H; k += 128) {
-        v8bf a[4], b[4][4];
+    for (int i = 0; i < MT; ++i)
+        xa[i] = reinterpret_cast<const v8bf *>(x + (size_t)min(t0 + 16 * i + r, Tn - 1) * H + kbeg + g * 8);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) a[u] = xa[(k + 32 * u) / 8];
+    for (int j = 0; j < NT; ++j)
+        wb[j] = reinterpret_cast<const v8bf *>(wr + (size_t)min(e0 + 16 * j + r, E - 1) * H + kbeg + g * 8);
+    v4f acc[MT][NT] = {};
+    for (int k = 0; k < klen; k += 128) {
+        v8bf a[MT][4], b[NT][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) a[i][u] = xa[i][(k + 32 * u) / 8];
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int u = 0; u < 4; ++u) b[j][u] = wb[j][(k + 32 * u) / 8];
 #pragma unroll
         for (int u = 0; u < 4; ++u)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], b[j][u], acc[j], 0, 0, 0);
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i][u], b[j][u], acc[i][j], 0, 0, 0);
     }
     // output layout: lane holds column (l % 16), rows 4*(l/16) + v
+    float *out = part + (size_t)blockIdx.z * Tn * E;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        int e = e0 + 16 * j + r;
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            int t = t0 + 4 * g + v;
-            if (t < Tn && e < E) logits[(size_t)t * E + e] = acc[j][v];
+        for (int j = 0; j < NT; ++j) {
+            int e = e0 + 16 * j + r;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                int t = t0 + 16 * i + 4 * g + v;
+                if (t < Tn && e < E) out[(size_t)t * E + e] = acc[i][j][v];
+            }
         }
-    }
 }
 
 // ----------------------------------------------------------------- routing
@@ -127,18 +144,32 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ lo
                                                     int k, int n_group, int topk_group, int renorm,
                                                     float scaling, int32_t *__restrict__ idx,
                                                     float *__restrict__ wout,
-                                                    uint32_t *__restrict__ mask, int mask_words)
+                                                    uint32_t *__restrict__ mask, int mask_words,
+                                                    int nsplit, float *__restrict__ logits_out)
 {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= Tn) return;
     float s[NV], key[NV];
     bool ok[NV];
+    const size_t TE = (size_t)Tn * E;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         int e = lane + 64 * i;
         ok[i] = e < E;
-        float lg = ok[i] ? logits[(size_t)t * E + e] : 0.0f;
+        // split-K partials of the router GEMM, summed in slice order
+        float lg = 0.0f;
+        if (ok[i]) {
+            float part[kMaxSplits];
+#pragma unroll
+            for (int sp = 0; sp < kMaxSplits; ++sp)
+                if (sp < nsplit) part[sp] = logits[sp * TE + (size_t)t * E + e];
+            lg = part[0];
+#pragma unroll
+            for (int sp = 1; sp < kMaxSplits; ++sp)
+                if (sp < nsplit) lg = __fadd_rn(lg, part[sp]);
+            if (logits_out) logits_out[(size_t)t * E + e] = lg;
+        }
         s[i] = xs_sigmoid(lg);
         key[i] = (ok[i] && bias) ? __fadd_rn(s[i], bias[e]) : s[i];
     }
@@ -224,7 +255,8 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ lo
 
 int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,
                  int64_t n_group, int64_t topk_group, int renorm, float scaling, int32_t *idx,
-                 float *w, uint32_t *mask, int mask_words, hipStream_t st)
+                 float *w, uint32_t *mask, int mask_words, int nsplit, float *logits_out,
+                 hipStream_t st)
 {
     if (T == 0) return XS_OK;
     dim3 grid((unsigned)((T + 3) / 4)), block(256);
@@ -232,7 +264,7 @@ int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, i
 #define XS_ROUTE(NVV)                                                                       \
     route_kernel<NVV><<<grid, block, 0, st>>>(logits, bias, (int)T, (int)E, (int)k,         \
                                               (int)n_group, (int)topk_group, renorm, scaling, \
-                                              idx, w, mask, mask_words)
+                                              idx, w, mask, mask_words, nsplit, logits_out)
     if (nv <= 1) XS_ROUTE(1);
     else if (nv <= 2) XS_ROUTE(2);
     else if (nv <= 4) XS_ROUTE(4);
@@ -243,8 +275,16 @@ int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, i
     return XS_OK;
 }
 
+int router_logits_splits(int64_t T, int64_t H, int exact, int dtype)
+{
+    if (exact || dtype == XS_F32) return 1;
+    int ns = T <= 64 ? 16 : (T <= 256 ? 8 : 4);
+    while (ns > 1 && (H % (128 * ns)) != 0) ns >>= 1;
+    return ns;
+}
+
 int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
-                         int exact, float *logits, hipStream_t st)
+                         int exact, float *logits, int nsplit, hipStream_t st)
 {
     if (T == 0) return XS_OK;
     if (exact || dtype == XS_F32) {
@@ -255,10 +295,16 @@ int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, in
         else
             router_logits_exact_kernel<uint16_t><<<grid, block, 0, st>>>(
                 (const uint16_t *)x, (const uint16_t *)wr, (int)T, (int)E, (int)H, logits);
+    } else if (T > 256) {
+        // prefill: 64 tokens x 128 experts per block, K split nsplit ways
+        dim3 grid((unsigned)((E + 127) / 128), (unsigned)((T + 63) / 64), (unsigned)nsplit), block(256);
+        router_logits_mfma_kernel<2, 4><<<grid, block, 0, st>>>((const uint16_t *)x, (const uint16_t *)wr,
+                                                                (int)T, (int)E, (int)H, (int)(H / nsplit), logits);
     } else {
-        dim3 grid((unsigned)((E + 63) / 64), (unsigned)((T + 63) / 64)), block(256);
-        router_logits_mfma_kernel<<<grid, block, 0, st>>>((const uint16_t *)x, (const uint16_t *)wr,
-                                                          (int)T, (int)E, (int)H, logits);
+        // decode: 32 tokens x 64 experts per block, K split nsplit ways
+        dim3 grid((unsigned)((E + 63) / 64), (unsigned)((T + 31) / 32), (unsigned)nsplit), block(256);
+        router_logits_mfma_kernel<1, 2><<<grid, block, 0, st>>>((const uint16_t *)x, (const uint16_t *)wr,
+                                                                (int)T, (int)E, (int)H, (int)(H / nsplit), logits);
     }
     XS_LAUNCH_CHECK();
     return XS_OK;
@@ -421,7 +467,7 @@ int xs_moe_router_logits(const void *x, const void *router_w, int dtype, int64_t
     XS_REQUIRE(x && router_w && logits, "null pointer");
     XS_REQUIRE(dtype == XS_F32 || dtype == XS_BF16, "unsupported dtype");
     XS_REQUIRE(T >= 0 && E >= 1 && H >= 128 && H % 128 == 0, "shape mismatch: H %% 128 != 0");
-    return launch_router_logits(x, router_w, dtype, T, E, H, exact, logits, (hipStream_t)stream);
+    return launch_router_logits(x, router_w, dtype, T, E, H, exact, logits, 1, (hipStream_t)stream);
 }
 
 int xs_moe_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,
@@ -438,7 +484,7 @@ int xs_moe_route(const float *logits, const float *bias, int64_t T, int64_t E, i
                    "topk_group must keep at least top_k experts");
     }
     return launch_route(logits, bias, T, E, k, n_group, topk_group, renormalize, scaling, idx, w,
-                        nullptr, 0, (hipStream_t)stream);
+                        nullptr, 0, 1, nullptr, (hipStream_t)stream);
 }
 
 int xs_quant_act_fp8(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, float *s,
