@@ -64,13 +64,16 @@ def time_forward(layer, x, steps, warmup, profile=False):
     return ms, stages
 
 
-def routed_expert_count(layer, x):
+def routed_counts(layer, x):
     import torch
-    T = x.shape[0]
     dbg = dict(counts=torch.empty(layer.E, dtype=torch.int32, device="cuda"))
     layer.forward(x, debug=dbg)
     torch.cuda.synchronize()
-    return int((dbg["counts"] > 0).sum().item())
+    return dbg["counts"].cpu().numpy()
+
+
+def routed_expert_count(layer, x):
+    return int((routed_counts(layer, x) > 0).sum())
 
 
 def cpu_baseline(g, sample_tokens):
@@ -135,7 +138,8 @@ def main():
     layer = layer_from(g)
     ms, stages = time_forward(layer, g["x"], a.steps, a.warmup, profile=True)
     flops = layer_flops(T, H, I, E, K_TOP)
-    ne = routed_expert_count(layer, g["x"])
+    counts = routed_counts(layer, g["x"])
+    ne = int((counts > 0).sum())
     wbytes = (ne + 1) * expert_bytes(H, I, False) + E * H * 2
     act_bytes = T * H * 2 * 2 + T * H + (T * K_TOP + T) * (I + 2 * H)
     gu_ms = stages["gemm_gate_up"]
@@ -158,6 +162,8 @@ def main():
                    "moe_intermediate": I, "experts": E, "top_k": K_TOP, "shared_experts": 1,
                    "weights": "e4m3 128x128 block scales", "routing": "sigmoid+bias, Zipf(1.1)",
                    "parallelism": "single GPU"},
+        "routing_counts": {"experts_used": ne, "max": int(counts.max()), "min": int(counts.min()),
+                           "top8": sorted(counts.tolist(), reverse=True)[:8]},
         "layer_tflops": flops / (ms * 1e-3) / 1e12,
         "layer_frac_fp8_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
         "layer_hbm_gbs": (wbytes + act_bytes) / (ms * 1e-3) / 1e9,

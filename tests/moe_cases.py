@@ -90,54 +90,14 @@ def max_abs_rel(got, ref):
 
 def make_case_gpu(T, H, I, E, k, *, seed=0, shared=True, bias_std=0.1, fp4=False, zipf=None,
                   host=True):
-    """Large cases: random weights drawn on the GPU (torch, seeded) and quantized
-    by the library's GPU quantizers (pinned bit-exact against the oracle by
-    test_gpu_stages).  Returns (case dict of numpy arrays or None, device dict)."""
+    """Large cases: the benchmark's GPU generator (moe_synth.synth_layer: weights
+    drawn on the GPU and quantized by the library's GPU quantizers, which
+    test_gpu_stages pins bit-exact against the oracle).  Returns (case dict of
+    numpy arrays or None, device dict)."""
     import torch
-    import xs_moe_capi as X
+    from moe_synth import synth_layer
 
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(seed)
-    dev = "cuda"
-    x = torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16)
-    wr = (torch.randn((E, H), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
-    bias = None
-    if bias_std:
-        bias = torch.randn((E,), generator=gen, device=dev) * bias_std
-    if zipf is not None:
-        rng = np.random.default_rng(seed)
-        ranks = rng.permutation(E) + 1
-        p = ranks.astype(np.float64) ** (-zipf)
-        p /= p.sum()
-        lp = torch.from_numpy(np.log(p).astype(np.float32)).to(dev)
-        bias = lp if bias is None else bias + lp
-    g = dict(T=T, H=H, I=I, E=E, k=k, x=x, router_w=wr, bias=bias, fp4=fp4)
-    quant = X.quant_weight_mxfp4 if fp4 else X.quant_weight_fp8_block
-    w13q, w2q, w13s, w2s = [], [], [], []
-    chunk = 16
-    for e0 in range(0, E, chunk):
-        n = min(chunk, E - e0)
-        w13 = torch.randn((n, 2 * I, H), generator=gen, device=dev, dtype=torch.bfloat16) * 0.02
-        q, s = quant(w13)
-        w13q.append(q)
-        w13s.append(s)
-        del w13
-        w2 = torch.randn((n, H, I), generator=gen, device=dev, dtype=torch.bfloat16) * 0.02
-        q, s = quant(w2)
-        w2q.append(q)
-        w2s.append(s)
-        del w2
-    g["w13"], g["s13"] = torch.cat(w13q), torch.cat(w13s)
-    g["w2"], g["s2"] = torch.cat(w2q), torch.cat(w2s)
-    if shared:
-        sw13 = torch.randn((2 * I, H), generator=gen, device=dev, dtype=torch.bfloat16) * 0.02
-        sw2 = torch.randn((H, I), generator=gen, device=dev, dtype=torch.bfloat16) * 0.02
-        q13, s13 = X.quant_weight_fp8_block(sw13)
-        q2, s2 = X.quant_weight_fp8_block(sw2)
-        g["shared"] = (q13, s13, q2, s2)
-    else:
-        g["shared"] = None
-    torch.cuda.synchronize()
+    g = synth_layer(T, H, I, E, k, seed=seed, shared=shared, bias_std=bias_std, fp4=fp4, zipf=zipf)
     if not host:
         return None, g
 

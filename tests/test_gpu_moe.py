@@ -120,7 +120,8 @@ def test_moe_prefill_full_size_properties():
     rc, ro, rp, ri = oracle.permute(ridx, E)
     assert np.array_equal(d["counts"], rc) and np.array_equal(d["offsets"], ro[:E + 1])
     assert np.array_equal(d["perm"], rp) and np.array_equal(d["inv"], ri)
-    assert rc.max() > 8 * rc.mean()                    # skewed as configured
+    # Zipf(1.1) profile: a head of experts with thousands of tokens, every expert used
+    assert rc.max() > 16 * rc.mean() and (rc > 0).all()
     rows = np.array([0, 1, 777, 4096, 5000, 8191])
     r = oracle_forward(c, logits_in=np.ascontiguousarray(d["logits"][rows]), rows=rows)
     got = out.float().cpu().numpy()[rows]

@@ -27,8 +27,12 @@ namespace xs {
 
 template <int BM, bool FP4>
 struct Cfg {
-    static constexpr int WM = BM >= 128 ? 2 : 1;
-    static constexpr int WN = 4 / WM;
+    // 8 waves (two per SIMD, so one wave's LDS latency hides behind the other's
+    // MFMAs) for tall tiles; 4 for the short decode tiles.
+    static constexpr int NW = BM >= 64 ? 8 : 4;
+    static constexpr int NT = 64 * NW;          // threads
+    static constexpr int WM = NW / 4;
+    static constexpr int WN = 4;
     static constexpr int TM = BM / WM;          // wave rows
     static constexpr int TN = 256 / WN;         // wave columns
     static constexpr int MI = TM / 16;
@@ -41,8 +45,8 @@ struct Cfg {
     static constexpr int SB_BYTES = FP4 ? 1024 : 0;              // 256 column scale words (MXFP4)
     static constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES + SB_BYTES;
     static constexpr int A_INSTR = A_BYTES / 1024;               // 1 KB per wave-wide DMA
-    static constexpr int NA_W = A_INSTR >= 4 ? A_INSTR / 4 : 1;  // per wave (dummies pad)
-    static constexpr int NB_W = B_BYTES / 1024 / 4;
+    static constexpr int NA_W = A_INSTR >= NW ? A_INSTR / NW : 1; // per wave (dummies pad)
+    static constexpr int NB_W = B_BYTES / 1024 / NW;
     static constexpr int NS_W = FP4 ? 2 : 1;                     // row-scale (+ column-scale) dwords
     static constexpr int PER_STAGE = NA_W + NB_W + NS_W;         // DMA instructions per wave per stage
     static constexpr int TRASH = 1024;                           // target of padding DMAs
@@ -97,7 +101,7 @@ __device__ __forceinline__ bool find_tile(const GemmArgs &a, int &e, int &m0, in
 }
 
 template <int BM, bool GATEUP, bool FP4>
-__global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
+__global__ __launch_bounds__(BM >= 64 ? 512 : 256) void moe_gemm_kernel(GemmArgs a)
 {
     using S = Cfg<BM, FP4>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -111,7 +115,8 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
     if (rows > BM) rows = BM;
     const bool shared = e == a.E;
     const int pos0 = a.offsets[e] + m0;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / S::WN, wn = wave % S::WN;
     const int l16 = lane & 15, g = lane >> 4;
 
@@ -138,7 +143,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
     uint32_t lA[S::NA_W];
 #pragma unroll
     for (int u = 0; u < S::NA_W; ++u) {
-        const int q = wave + 4 * u;                    // wave-wide instruction index
+        const int q = wave + S::NW * u;                    // wave-wide instruction index
         const int p = 64 * q + lane;                   // LDS chunk written by this lane
         const int r = p >> 3, c = swz8(r, p & 7);
         const bool real = q < S::A_INSTR;
@@ -148,7 +153,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
     const uint8_t *gB[S::NB_W];
 #pragma unroll
     for (int u = 0; u < S::NB_W; ++u) {
-        const int q = wave + 4 * u;
+        const int q = wave + S::NW * u;
         const int p = 64 * q + lane;
         if (FP4) {
             const int vr = p >> 2, c = swz4(vr, p & 3);
@@ -160,6 +165,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
     }
     // row scales: waves 0/1 load rows 64w + lane (waves beyond BM target trash)
     const bool sa_real = wave * 64 < BM;
+    const bool sb_real = wave < 4;            // MXFP4 column scales: 256 words = 4 waves
     const uint8_t *gSA;
     if (FP4)
         gSA = reinterpret_cast<const uint8_t *>(a.As) + (size_t)arow_of(sa_real ? wave * 64 + lane : 0) * (a.K / 32);
@@ -168,12 +174,12 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
     const uint8_t *gSB = nullptr;
     if (FP4)
         gSB = reinterpret_cast<const uint8_t *>(a.Bs) + (size_t)e * Nrows * (a.K / 32) +
-              (size_t)brow_of(wave * 64 + lane) * (a.K / 32);
+              (size_t)brow_of(sb_real ? wave * 64 + lane : 0) * (a.K / 32);
 
     // ---- FP8 weight block scales for the whole tile ----
     if (!FP4) {
         const float *Bsf = shared ? a.Bssh : reinterpret_cast<const float *>(a.Bs) + (size_t)e * (Nrows / 128) * KB;
-        for (int q = tid; q < 2 * KB; q += 256) {
+        for (int q = tid; q < 2 * KB; q += S::NT) {
             int b = q / KB, kb = q % KB;
             int nb;
             if (GATEUP) nb = (b ? a.N + n0 : n0) / 128;
@@ -196,10 +202,10 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
         }
 #pragma unroll
         for (int u = 0; u < S::NB_W; ++u)
-            dma16(gB[u] + (size_t)kk * S::BROW, st + S::A_BYTES + (uint32_t)((wave + 4 * u) * 1024));
+            dma16(gB[u] + (size_t)kk * S::BROW, st + S::A_BYTES + (uint32_t)((wave + S::NW * u) * 1024));
         if (FP4) {
             dma4(gSA + (size_t)kk * 4, sa_real ? st + S::A_BYTES + S::B_BYTES + wave * 256 : trash_lds);
-            dma4(gSB + (size_t)kk * 4, st + S::A_BYTES + S::B_BYTES + S::SA_BYTES + wave * 256);
+            dma4(gSB + (size_t)kk * 4, sb_real ? st + S::A_BYTES + S::B_BYTES + S::SA_BYTES + wave * 256 : trash_lds);
         } else {
             dma4(gSA + (size_t)kk * 4, sa_real ? st + S::A_BYTES + S::B_BYTES + wave * 256 : trash_lds);
         }
@@ -230,30 +236,35 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
         // (element 2i in the low nibble), i.e. 16-byte chunk g of a 64-byte row.
         // The e8m0 scale of (row r, 32-wide K block b) is taken from lane 16b + r.
         // Pinned by the FP8 x FP4 parity tests.
-        v8i afr[S::MI];
+        //
+        // Weights are the MFMA's A operand and activations its B operand, so the
+        // 16x16 result is (weight column n) x (token m): lane 16g + r holds token
+        // r and columns 4g..4g+3 -- one activation scale per lane and subtile,
+        // and four adjacent output columns per lane for the epilogue stores.
+        v8i xfr[S::MI];   // activation fragments, one per 16-token subtile
 #pragma unroll
         for (int i = 0; i < S::MI; ++i) {
             int r = wm * S::TM + 16 * i + l16;
             v4i lo = *reinterpret_cast<const v4i *>(sa_ + r * 128 + swz8(r, g) * 16);
             v4i hi = *reinterpret_cast<const v4i *>(sa_ + r * 128 + swz8(r, g + 4) * 16);
-            afr[i] = cat(lo, hi);
+            xfr[i] = cat(lo, hi);
         }
         if (FP4) {
             const uint32_t *sAw = reinterpret_cast<const uint32_t *>(ssc);
             const uint32_t *sBw = reinterpret_cast<const uint32_t *>(ssc + S::SA_BYTES);
-            int sa_s[S::MI];
+            int sx[S::MI];
 #pragma unroll
-            for (int i = 0; i < S::MI; ++i) sa_s[i] = (int)((sAw[wm * S::TM + 16 * i + l16] >> (8 * g)) & 0xffu);
+            for (int i = 0; i < S::MI; ++i) sx[i] = (int)((sAw[wm * S::TM + 16 * i + l16] >> (8 * g)) & 0xffu);
 #pragma unroll
             for (int j = 0; j < S::NJ; ++j) {
                 int vr = wn * S::TN + 16 * j + l16;
                 v4i b4 = *reinterpret_cast<const v4i *>(sb_ + vr * 64 + swz4(vr, g) * 16);
-                v8i bfr = v8i{b4[0], b4[1], b4[2], b4[3], 0, 0, 0, 0};
-                int sb_s = (int)((sBw[vr] >> (8 * g)) & 0xffu);
+                v8i wfr = v8i{b4[0], b4[1], b4[2], b4[3], 0, 0, 0, 0};
+                int sw = (int)((sBw[vr] >> (8 * g)) & 0xffu);
 #pragma unroll
                 for (int i = 0; i < S::MI; ++i)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(afr[i], bfr, acc[i][j], 0, 4, 0,
-                                                                                sa_s[i], 0, sb_s);
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wfr, xfr[i], acc[i][j], 4, 0, 0,
+                                                                                sw, 0, sx[i]);
             }
         } else {
             const float *sAk = reinterpret_cast<const float *>(ssc);
@@ -261,22 +272,19 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
             // block 1 (up) for odd ones; down uses the wave's own 128-column block
             const float sb0 = GATEUP ? sB[kb] : sB[((wn * S::TN) >> 7) * KB + kb];
             const float sb1 = GATEUP ? sB[KB + kb] : sb0;
-            float c0[S::MI][4], c1[S::MI][4];
+            float c0[S::MI], c1[S::MI];
 #pragma unroll
             for (int i = 0; i < S::MI; ++i) {
-                v4f sa4 = *reinterpret_cast<const v4f *>(sAk + wm * S::TM + 16 * i + 4 * g);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    c0[i][v] = sa4[v] * sb0;
-                    c1[i][v] = sa4[v] * sb1;
-                }
+                const float sx = sAk[wm * S::TM + 16 * i + l16];
+                c0[i] = sx * sb0;
+                c1[i] = sx * sb1;
             }
-            // Software pipeline over the (j, i) subtiles: the partial product of
-            // subtile n is folded after MFMA n + PD has been issued, so the
-            // matrix pipe never waits for the VALU fold (and vice versa).
+            // The partial product of subtile n is folded after MFMA n + PD has
+            // been issued; the group barriers below interleave MFMAs with the
+            // VALU folds so the matrix pipe and the VALU run concurrently.
             constexpr int NSUB = S::NJ * S::MI, PD = 2;
             v4f pr[PD + 1];
-            v8i bfr;
+            v8i wfr;
 #pragma unroll
             for (int n = 0; n < NSUB + PD; ++n) {
                 if (n < NSUB) {
@@ -285,18 +293,24 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
                         int vr = wn * S::TN + 16 * j + l16;
                         v4i lo = *reinterpret_cast<const v4i *>(sb_ + vr * 128 + swz8(vr, g) * 16);
                         v4i hi = *reinterpret_cast<const v4i *>(sb_ + vr * 128 + swz8(vr, g + 4) * 16);
-                        bfr = cat(lo, hi);
+                        wfr = cat(lo, hi);
                     }
                     pr[n % (PD + 1)] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        afr[i], bfr, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
+                        wfr, xfr[i], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
                 }
                 if (n >= PD) {
                     const int m = n - PD, j = m / S::MI, i = m % S::MI;
-                    const v4f p = pr[m % (PD + 1)];
+                    const v4f pp = pr[m % (PD + 1)];
+                    const float c = (GATEUP && (j & 1)) ? c1[i] : c0[i];
 #pragma unroll
-                    for (int v = 0; v < 4; ++v)
-                        acc[i][j][v] = __builtin_fmaf(p[v], (GATEUP && (j & 1)) ? c1[i][v] : c0[i][v], acc[i][j][v]);
+                    for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(pp[v], c, acc[i][j][v]);
                 }
+            }
+#pragma unroll
+            for (int n = 0; n < NSUB; ++n) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);   // then ~5 VALU
+                if ((n & 1) == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // an LDS read
             }
         }
     }
@@ -304,8 +318,10 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
     __syncthreads();
 
     // ------------------------------------------------------------ epilogue
+    // acc[i][j][v]: token row wm*TM + 16i + l16, column 16j + 4g + v of the wave.
     if (GATEUP) {
         constexpr int NP = S::NJ / 2;     // gate/up pairs per wave
+        constexpr int SROW = 144;         // staging row stride (bytes): conflict-free 4-byte writes
         float act[S::MI][NP][4];
 #pragma unroll
         for (int i = 0; i < S::MI; ++i)
@@ -316,43 +332,44 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
                     float gt = acc[i][2 * p][v], up = acc[i][2 * p + 1][v];
                     act[i][p][v] = gt * fast_sigmoid(gt) * up;
                 }
-        uint8_t *stg = smem;   // [BM][128] fp8 staging (stage buffers are free now)
+        uint8_t *stg = smem;   // [BM][SROW] fp8 staging (the ring is free now)
+        auto pack4 = [](float x0, float x1, float x2, float x3) -> uint32_t {
+            return e4m3_pack2_hw(x0, x1) | (e4m3_pack2_hw(x2, x3) << 16);
+        };
         if (!FP4) {
-            // FP8 1x128: row amax over the block's 128 act columns (all waves of a row)
+            // FP8 1x128: token amax over the block's 128 act columns (4 column
+            // groups of a wave, then the WN waves of the row)
 #pragma unroll
-            for (int i = 0; i < S::MI; ++i)
+            for (int i = 0; i < S::MI; ++i) {
+                float m = 0.f;
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    float m = 0.f;
+                for (int p = 0; p < NP; ++p)
 #pragma unroll
-                    for (int p = 0; p < NP; ++p) m = fmaxf(m, __builtin_fabsf(act[i][p][v]));
-#pragma unroll
-                    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, WAVE));
-                    if (l16 == 0) red[wn * BM + wm * S::TM + 16 * i + 4 * g + v] = m;
-                }
+                    for (int v = 0; v < 4; ++v) m = fmaxf(m, __builtin_fabsf(act[i][p][v]));
+                m = fmaxf(m, __shfl_xor(m, 16, WAVE));
+                m = fmaxf(m, __shfl_xor(m, 32, WAVE));
+                if (g == 0) red[wn * BM + wm * S::TM + 16 * i + l16] = m;
+            }
             __syncthreads();
 #pragma unroll
-            for (int i = 0; i < S::MI; ++i)
+            for (int i = 0; i < S::MI; ++i) {
+                const int r = wm * S::TM + 16 * i + l16;
+                float amax = 0.f;
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    int r = wm * S::TM + 16 * i + 4 * g + v;
-                    float amax = 0.f;
+                for (int w = 0; w < S::WN; ++w) amax = fmaxf(amax, red[w * BM + r]);
+                const float inv = amax == 0.f ? 0.f : __fdiv_rn(448.0f, amax);
 #pragma unroll
-                    for (int w = 0; w < S::WN; ++w) amax = fmaxf(amax, red[w * BM + r]);
-                    float inv = amax == 0.f ? 0.f : __fdiv_rn(448.0f, amax);
+                for (int p = 0; p < NP; ++p) {
+                    float q[4];
 #pragma unroll
-                    for (int p = 0; p < NP; p += 2) {
-                        float x0 = fminf(fmaxf(act[i][p][v] * inv, -448.f), 448.f);
-                        float x1 = fminf(fmaxf(act[i][p + 1][v] * inv, -448.f), 448.f);
-                        uint32_t pk = e4m3_pack2_hw(x0, x1);
-                        int cc = (wn * NP + p) * 16 + l16;
-                        stg[r * 128 + cc] = (uint8_t)(pk & 0xff);
-                        stg[r * 128 + cc + 16] = (uint8_t)(pk >> 8);
-                    }
+                    for (int v = 0; v < 4; ++v) q[v] = fminf(fmaxf(act[i][p][v] * inv, -448.f), 448.f);
+                    *reinterpret_cast<uint32_t *>(stg + r * SROW + (wn * NP + p) * 16 + 4 * g) =
+                        pack4(q[0], q[1], q[2], q[3]);
                 }
+            }
             __syncthreads();
             float *Cs = reinterpret_cast<float *>(a.Cs);
-            for (int r = tid; r < rows; r += 256) {
+            for (int r = tid; r < rows; r += S::NT) {
                 float amax = 0.f;
 #pragma unroll
                 for (int w = 0; w < S::WN; ++w) amax = fmaxf(amax, red[w * BM + r]);
@@ -362,52 +379,58 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(GemmArgs a)
             // MXFP8 1x32: a 32-column block is pairs (2q, 2q+1) of one wave
             uint8_t *Cs8 = reinterpret_cast<uint8_t *>(a.Cs);
 #pragma unroll
-            for (int i = 0; i < S::MI; ++i)
+            for (int i = 0; i < S::MI; ++i) {
+                const int r = wm * S::TM + 16 * i + l16;
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    int r = wm * S::TM + 16 * i + 4 * g + v;
+                for (int p = 0; p < NP; p += 2) {
+                    float m = 0.f;
 #pragma unroll
-                    for (int p = 0; p < NP; p += 2) {
-                        float m = fmaxf(__builtin_fabsf(act[i][p][v]), __builtin_fabsf(act[i][p + 1][v]));
+                    for (int v = 0; v < 4; ++v)
+                        m = fmaxf(m, fmaxf(__builtin_fabsf(act[i][p][v]), __builtin_fabsf(act[i][p + 1][v])));
+                    m = fmaxf(m, __shfl_xor(m, 16, WAVE));
+                    m = fmaxf(m, __shfl_xor(m, 32, WAVE));
+                    const int se = mx_exponent(m, 8);
 #pragma unroll
-                        for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, WAVE));
-                        int se = mx_exponent(m, 8);
-                        float x0 = fminf(fmaxf(__builtin_ldexpf(act[i][p][v], -se), -448.f), 448.f);
-                        float x1 = fminf(fmaxf(__builtin_ldexpf(act[i][p + 1][v], -se), -448.f), 448.f);
-                        uint32_t pk = e4m3_pack2_hw(x0, x1);
-                        int cc = (wn * NP + p) * 16 + l16;
-                        stg[r * 128 + cc] = (uint8_t)(pk & 0xff);
-                        stg[r * 128 + cc + 16] = (uint8_t)(pk >> 8);
-                        if (l16 == 0 && r < rows)
-                            Cs8[(size_t)(pos0 + r) * (a.N / 32) + (n0 + (wn * NP + p) * 16) / 32] = (uint8_t)(se + 127);
+                    for (int h = 0; h < 2; ++h) {
+                        float q[4];
+#pragma unroll
+                        for (int v = 0; v < 4; ++v)
+                            q[v] = fminf(fmaxf(__builtin_ldexpf(act[i][p + h][v], -se), -448.f), 448.f);
+                        *reinterpret_cast<uint32_t *>(stg + r * SROW + (wn * NP + p + h) * 16 + 4 * g) =
+                            pack4(q[0], q[1], q[2], q[3]);
                     }
+                    if (g == 0 && r < rows)
+                        Cs8[(size_t)(pos0 + r) * (a.N / 32) + (n0 + (wn * NP + p) * 16) / 32] = (uint8_t)(se + 127);
                 }
+            }
             __syncthreads();
         }
-        for (int q = tid; q < rows * 8; q += 256) {
+        for (int q = tid; q < rows * 8; q += S::NT) {
             int r = q >> 3, c = q & 7;
             *reinterpret_cast<v4i *>(a.Cq + (size_t)(pos0 + r) * a.N + n0 + c * 16) =
-                *reinterpret_cast<const v4i *>(stg + r * 128 + c * 16);
+                *reinterpret_cast<const v4i *>(stg + r * SROW + c * 16);
         }
     } else {
-        uint16_t *stg = reinterpret_cast<uint16_t *>(smem);   // [BM][256] bf16
+        constexpr int SROW = 264;         // staging row stride (bf16 elements): conflict-free 8-byte writes
+        uint16_t *stg = reinterpret_cast<uint16_t *>(smem);   // [BM][SROW] bf16
 #pragma unroll
         for (int i = 0; i < S::MI; ++i)
 #pragma unroll
-            for (int j = 0; j < S::NJ; ++j)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    int r = wm * S::TM + 16 * i + 4 * g + v;
-                    int c = wn * S::TN + 16 * j + l16;
-                    stg[r * 256 + c] = bf16_from_f32(acc[i][j][v]);
-                }
+            for (int j = 0; j < S::NJ; ++j) {
+                const int r = wm * S::TM + 16 * i + l16;
+                const int c = wn * S::TN + 16 * j + 4 * g;
+                v2i pk;
+                pk[0] = (int)((uint32_t)bf16_from_f32(acc[i][j][0]) | ((uint32_t)bf16_from_f32(acc[i][j][1]) << 16));
+                pk[1] = (int)((uint32_t)bf16_from_f32(acc[i][j][2]) | ((uint32_t)bf16_from_f32(acc[i][j][3]) << 16));
+                *reinterpret_cast<v2i *>(stg + r * SROW + c) = pk;
+            }
         __syncthreads();
         const int ncols = min(256, a.N - n0);
-        for (int q = tid; q < rows * 32; q += 256) {
+        for (int q = tid; q < rows * 32; q += S::NT) {
             int r = q >> 5, c = q & 31;
             if (c * 8 < ncols)
                 *reinterpret_cast<v4i *>(a.Cy + (size_t)(pos0 + r) * a.ldc + n0 + c * 8) =
-                    *reinterpret_cast<const v4i *>(stg + r * 256 + c * 8);
+                    *reinterpret_cast<const v4i *>(stg + r * SROW + c * 8);
         }
     }
 }
@@ -418,7 +441,7 @@ static size_t gemm_smem_bytes(int K)
     using S = Cfg<BM, FP4>;
     const size_t KB = (size_t)K / 128;
     size_t b = (size_t)S::NST * S::STAGE + S::TRASH + 4 * 2 * KB + 4 * (size_t)S::WN * BM;
-    size_t epi = GATEUP ? (size_t)BM * 128 : (size_t)BM * 512;
+    size_t epi = GATEUP ? (size_t)BM * 144 : (size_t)BM * 528;
     if (epi > (size_t)S::NST * S::STAGE) b += epi;   // staging reuses the ring when it fits
     return b;
 }
@@ -436,7 +459,7 @@ static int launch_one(const GemmArgs &a, int grid_y, hipStream_t st)
     }
     int grid_x = GATEUP ? a.N / 128 : (a.N + 255) / 256;
     if (grid_y <= 0) return XS_OK;
-    fn<<<dim3((unsigned)grid_x, (unsigned)grid_y), dim3(256), smem, st>>>(a);
+    fn<<<dim3((unsigned)grid_x, (unsigned)grid_y), dim3(Cfg<BM, FP4>::NT), smem, st>>>(a);
     XS_LAUNCH_CHECK();
     return XS_OK;
 }

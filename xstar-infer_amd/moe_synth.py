@@ -3,12 +3,40 @@
 Weights ~ N(0, 0.02) are drawn with a seeded torch generator and quantized by
 the library's own quantizers (xs_quant_weight_fp8_block / xs_quant_weight_mxfp4)
 -- there is no network for checkpoints.  Activations x ~ N(0, 1) in bf16,
-router bias ~ N(0, 0.1), optional Zipf(s) expert popularity folded into the
-bias (log of a Zipf rank distribution under a random expert <-> rank map).
+router weights ~ N(0, 0.02), router bias ~ N(0, 0.1) (or zero for uniform
+routing).
+
+Zipf(s) expert popularity (zipf=s): each token ranks the experts by
+log p_e + Gumbel noise, with p a Zipf(s) rank distribution under a random
+expert <-> rank map (Plackett-Luce sampling, so the realised per-expert token
+counts follow the Zipf profile: a few experts near T tokens, a tail of ~T*k*p_256
+tokens, all experts used).  The router is built to reproduce that ranking:
+router rows are orthonormal (entries ~ N(0, 1/H), close to the N(0, 0.02) of
+the plain case), the logits are chosen so that sigmoid(logit) + bias is an
+increasing function of the key, and x = logits . W_r + (noise orthogonal to the
+router rows), so x . W_r^T gives back the logits.
 """
 from __future__ import annotations
 
 import numpy as np
+
+
+def _zipf_router(T, H, E, gen, bias, zipf, seed, dev):
+    import torch
+    rng = np.random.default_rng(seed)
+    p = (np.arange(E) + 1.0) ** (-zipf)
+    p /= p.sum()
+    logp = torch.from_numpy(np.log(p[rng.permutation(E)]).astype(np.float32)).to(dev)
+    u = torch.rand((T, E), generator=gen, device=dev).clamp_(1e-12, 1.0 - 1e-7)
+    key = logp + (-torch.log(-torch.log(u)))
+    b = bias if bias is not None else torch.zeros(E, device=dev)
+    s = (0.5 + 0.03 * key - b).clamp_(0.004, 0.996)
+    logits = torch.log(s / (1.0 - s))
+    q, _ = torch.linalg.qr(torch.randn((H, E), generator=gen, device=dev))
+    wr = q.t().contiguous()                                  # [E, H], orthonormal rows
+    z = torch.randn((T, H), generator=gen, device=dev)
+    x = logits @ wr + (z - (z @ wr.t()) @ wr)
+    return x.to(torch.bfloat16), wr.to(torch.bfloat16)
 
 
 def synth_layer(T, H, I, E, k, *, seed=0, shared=True, bias_std=0.1, fp4=False, zipf=None,
@@ -19,16 +47,12 @@ def synth_layer(T, H, I, E, k, *, seed=0, shared=True, bias_std=0.1, fp4=False, 
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
     dev = "cuda"
-    x = torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16)
-    wr = (torch.randn((E, H), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
     bias = torch.randn((E,), generator=gen, device=dev) * bias_std if bias_std else None
     if zipf is not None:
-        rng = np.random.default_rng(seed)
-        ranks = rng.permutation(E) + 1
-        p = ranks.astype(np.float64) ** (-zipf)
-        p /= p.sum()
-        lp = torch.from_numpy(np.log(p).astype(np.float32)).to(dev)
-        bias = lp if bias is None else bias + lp
+        x, wr = _zipf_router(T, H, E, gen, bias, zipf, seed, dev)
+    else:
+        x = torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16)
+        wr = (torch.randn((E, H), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
     g = dict(T=T, H=H, I=I, E=E, k=k, x=x, router_w=wr, bias=bias, fp4=fp4)
     quant = X.quant_weight_mxfp4 if fp4 else X.quant_weight_fp8_block
     if fp4:
