@@ -32,6 +32,21 @@ PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 METRIC = "MoE-layer tokens/s + TFLOP/s (% FP8 MFMA peak) and decode HBM GB/s, hid4096"
 
 
+PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "moe_gemm_prefill8192.md")
+
+
+def measured_traffic():
+    """HBM bytes per gate_up dispatch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated against a 1 GiB copy), or None."""
+    try:
+        for line in open(PROFILE_SUMMARY):
+            if line.startswith("traffic_bytes_gate_up:"):
+                return float(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -170,7 +185,8 @@ def main():
         "stage_ms": stages,
         "roofline": {"kernel": "moe_gemm_kernel<gate_up> (grouped FP8 gate_up GEMM + SwiGLU)",
                      "bound": "mfma", "achieved": achieved, "peak": PEAK_FP8_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP8_TFLOPS, "traffic": None},
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP8_TFLOPS, "traffic": measured_traffic(),
+                     "algorithmic_flop": gu_flops, "launch_ms": gu_ms},
     }
     del layer
     if not a.no_cpu:
