@@ -72,6 +72,17 @@ def test_moe_bf16_shapes(T, H, I, E, k, shared):
     _run_and_check(c, g, router_exact=False)
 
 
+@pytest.mark.parametrize("T,E,k,zipf,seed", [(700, 16, 4, 1.1, 21), (40, 4, 4, None, 22), (1000, 8, 2, 0.6, 23)])
+def test_moe_wide_tiles(T, E, k, zipf, seed):
+    """192 x 256-tile FP8 GEMMs (H, I multiples of 1024; experts averaging 32+
+    rows): skewed routing gives segments of 1..6 32-row subtiles, multi-tile
+    experts and the shared segment; exact and MFMA routers."""
+    c = make_case(T, 1024, 1024, E, k, seed=seed, zipf=zipf)
+    g = to_device(c)
+    _run_and_check(c, g, router_exact=True)
+    _run_and_check(c, g, router_exact=False)
+
+
 def test_moe_group_limited_and_scaling():
     c = make_case(96, 512, 128, 32, 4, seed=3)
     g = to_device(c)

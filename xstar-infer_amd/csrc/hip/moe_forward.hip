@@ -7,6 +7,9 @@
 // workspace, laid out by WsLayout below.
 #include "moe_gemm.hpp"
 
+#include <cstdlib>
+#include <cstring>
+
 namespace xs {
 
 static size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -46,6 +49,18 @@ static int pick_bm(double rows_per_tile_group)
     if (rows_per_tile_group >= 48) return 64;
     if (rows_per_tile_group >= 24) return 32;
     return 16;
+}
+
+// GEMM family for the FP8 layer: the 192 x 256-tile kernels (moe_gemm_wide.hip)
+// once experts average 32+ rows and K is a multiple of 1024, else the
+// 16..128-row tiles.  XS_MOE_GEMM=wide|tiled overrides (benchmarks, tests).
+static bool use_wide(const xs_moe_params *p)
+{
+    if (p->routed_format != XS_FP8_E4M3 || p->H % 1024 || p->I % 1024) return false;
+    static const char *force = getenv("XS_MOE_GEMM");
+    if (force && !strcmp(force, "wide")) return true;
+    if (force && !strcmp(force, "tiled")) return false;
+    return p->T * p->top_k >= 32 * p->E;
 }
 
 static WsLayout layout(const xs_moe_params *p)
@@ -154,7 +169,8 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     }
     // 3. permute: (expert, token)-sorted positions, tile offsets
     if ((rc = prof_mark(3, st))) return rc;
-    const int bm = pick_bm((double)S / (double)E);
+    const bool wide = use_wide(p);
+    const int bm = wide ? wide_tile_rows() : pick_bm((double)S / (double)E);
     PermuteOut po = {};
     po.counts = WS(int32_t, counts);
     po.offsets = offsets;
@@ -208,13 +224,15 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g1.Cs = WS(float, acts);
         g1.e_lo = 0;
         g1.e_hi = (int)E + (shared_rows ? 1 : 0);
-        rc = launch_gemm(g1, true, false, routed_tiles + shared_tiles, st);
+        rc = wide ? launch_gemm_wide(g1, true, routed_tiles + shared_tiles, st)
+                  : launch_gemm(g1, true, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
         if ((rc = prof_mark(5, st))) return rc;
         g2.As = WS(float, acts);
         g2.e_lo = 0;
         g2.e_hi = g1.e_hi;
-        rc = launch_gemm(g2, false, false, routed_tiles + shared_tiles, st);
+        rc = wide ? launch_gemm_wide(g2, false, routed_tiles + shared_tiles, st)
+                  : launch_gemm(g2, false, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
     } else {
         GemmArgs r1 = g1;

@@ -27,6 +27,10 @@ struct GemmArgs {
 };
 
 int launch_gemm(const GemmArgs &a, bool gateup, bool fp4, int grid_y, hipStream_t st);
+// 192 x 256 tiles, FP8 only, K a multiple of 1024 (moe_gemm_wide.hip); a.bm must be
+// wide_tile_rows().
+int wide_tile_rows();
+int launch_gemm_wide(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st);
 int launch_combine(const uint16_t *y, const int32_t *inv, const float *w, int64_t T, int64_t k,
                    int64_t H, int64_t shared_base, int has_shared, void *out, int out_dtype,
                    hipStream_t st);
