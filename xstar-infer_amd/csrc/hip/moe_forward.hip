@@ -38,7 +38,7 @@ static int prof_mark(int stage, hipStream_t st)
 }
 
 struct WsLayout {
-    size_t logits, idx, w, mask, wordprefix, counts, offsets, perm, inv, row_token, tiles;
+    size_t logits, idx, w, mask, wordprefix, counts, offsets, perm, inv, row_token, tiles, tiletab;
     size_t xq, xs, xmq, xms, actq, acts, actms, y;
     size_t total;
 };
@@ -51,12 +51,11 @@ static int pick_bm(double rows_per_tile_group)
     return 16;
 }
 
-// GEMM family for the FP8 layer: the 192 x 256-tile kernels (moe_gemm_wide.hip)
-// once experts average 32+ rows and K is a multiple of 1024, else the
-// 16..128-row tiles.  XS_MOE_GEMM=wide|tiled overrides (benchmarks, tests).
+// GEMM family for the FP8 layer: the tall-tile kernels (moe_gemm_wide.hip) once
+// experts average 32+ rows, else the 16..128-row tiles.  XS_MOE_GEMM=wide|tiled overrides (benchmarks, tests).
 static bool use_wide(const xs_moe_params *p)
 {
-    if (p->routed_format != XS_FP8_E4M3 || p->H % 1024 || p->I % 1024) return false;
+    if (p->routed_format != XS_FP8_E4M3) return false;
     static const char *force = getenv("XS_MOE_GEMM");
     if (force && !strcmp(force, "wide")) return true;
     if (force && !strcmp(force, "tiled")) return false;
@@ -83,6 +82,7 @@ static WsLayout layout(const xs_moe_params *p)
     take(L.inv, 4 * S);
     take(L.row_token, 4 * R);
     take(L.tiles, 4 * (E + 2));
+    take(L.tiletab, wide_tile_table_bytes((int64_t)S, p->has_shared ? (int64_t)T : 0, (int64_t)E));
     take(L.xq, T * H);
     take(L.xs, 4 * T * (H / 128));
     take(L.xmq, fp4 ? T * H : 0);
@@ -224,6 +224,11 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g1.Cs = WS(float, acts);
         g1.e_lo = 0;
         g1.e_hi = (int)E + (shared_rows ? 1 : 0);
+        if (wide) {
+            g1.tile_tab = WS(int32_t, tiletab);
+            rc = launch_tile_table(g1, st);
+            if (rc) return rc;
+        }
         rc = wide ? launch_gemm_wide(g1, true, routed_tiles + shared_tiles, st)
                   : launch_gemm(g1, true, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
@@ -231,6 +236,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g2.As = WS(float, acts);
         g2.e_lo = 0;
         g2.e_hi = g1.e_hi;
+        g2.tile_tab = g1.tile_tab;
         rc = wide ? launch_gemm_wide(g2, false, routed_tiles + shared_tiles, st)
                   : launch_gemm(g2, false, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;

@@ -1,32 +1,33 @@
-// moe_gemm_wide.hip -- grouped FP8 block-scaled expert GEMMs on 192 x 256 tiles
-// (gfx950), the prefill path of the MoE layer.
+// moe_gemm_wide.hip -- grouped FP8 block-scaled expert GEMMs on tall tiles (gfx950),
+// the prefill path of the MoE layer.
 //
 // Nearest reference code: gemm_silu_and_mul_kernel (xstar_cpp/src/ops/mlp.cu:52-200)
 // and gemm_kernel (xstar_cpp/src/ops/gemm.cu:41-210); numerics as the FP8 tiles of
 // moe_gemm.hip (f32 accumulation of each 128-K block, scaled by the activation row
 // scale times the weight block scale; SwiGLU in f32; 1x128 FP8 requantization).
 //
-// Structure, chosen for CDNA4's fetch and LDS budgets:
-//   * a block owns up to 192 rows of one expert and a 256-column weight slab
-//     (gate_up: 128 gate + the matching 128 up rows; down: 256 rows of W2), so
-//     each K step moves 56 KB into the CU for 12.6 MFLOP -- 37 B/clk per CU at
-//     the MFMA rate, about half of what L2 delivers to a CU (taller tiles would
-//     need more than the 256 VGPRs of two waves per SIMD);
-//   * 8 waves split the slab: wave w owns 32 weight rows for ALL of the
-//     block's tokens.  Its weights are private, so they go global -> VGPR with
-//     no LDS round trip; the activation rows, shared by all 8 waves, go
-//     global -> LDS by DMA (global_load_lds_dwordx4) into a ring;
-//   * v_mfma_f32_32x32x64_f8f6f4 with weights as operand A (rows 0..15 gate,
-//     16..31 up for gate_up) and 32 tokens as operand B: a lane's 16 results
-//     belong to one token, and its gate and matching up values sit in the same
-//     lane, so SwiGLU and the requantization are register epilogues;
-//   * the main loop is instantiated per number NS of 32-row token subtiles
-//     (1..6), so a short expert segment moves and multiplies only the rows it
-//     has, and uses the registers the missing accumulators free for a deeper
-//     weight prefetch (the short tiles are bandwidth bound);
-//   * every vector-memory load of the loop is issued from inline asm and the
-//     waits are explicit s_waitcnt vmcnt(N) with the exact count of loads
-//     allowed in flight (the compiler's own accounting would not see the DMAs).
+// Structure, chosen from measurements of CDNA4's per-CU budgets (a CU's vector
+// memory path moves ~16 clk per fully coalesced KB but ~4x that when one
+// instruction touches 16+ rows; LDS reads ~256 B/clk; 16x16x128 FP8 MFMA 32
+// clk per SIMD):
+//   * a block owns BM (128 or 192) rows of one expert and a 256-column weight
+//     slab (gate_up: 128 gate + the matching 128 up rows; down: 256 rows of W2);
+//   * both operand tiles move global -> LDS by DMA (global_load_lds_dwordx4,
+//     8 lanes per 128-byte row, so every load instruction is fully coalesced)
+//     into a ring of NST stages; 16-byte chunks are XOR-swizzled per row so the
+//     MFMA fragment reads are bank-conflict free;
+//   * 8 waves as 2 (tokens) x 4 (weight columns): a wave owns 64 weight rows
+//     (gate_up: 32 gate + the matching 32 up) and the 16-token subtiles of its
+//     parity, so a partially filled tile still splits evenly over both halves;
+//   * v_mfma_f32_16x16x128_f8f6f4 with weights as operand A and tokens as
+//     operand B: a lane's 4 results belong to one token (one activation scale)
+//     and a lane holds gate and matching up values, so SwiGLU and the
+//     requantization are register epilogues;
+//   * per K step each subtile's 4 products are folded into the f32
+//     accumulators with (row scale x block scale) one subtile later, while the
+//     next subtile's MFMAs run; subtiles past the tile's rows are skipped;
+//   * tile descriptors (expert, first row, rows) come from a table built once
+//     per launch, so a block starts with one load instead of a search.
 #include "moe_gemm.hpp"
 
 namespace xs {
@@ -34,31 +35,23 @@ namespace {
 
 constexpr int kNW = 8;               // waves per block
 constexpr int kNT = 64 * kNW;        // threads
-constexpr int kBM = 192;             // tile rows (6 subtiles of 32: the register budget of 2 waves/SIMD)
-constexpr int kRing = 136 * 1024;    // LDS bytes of the activation ring
+constexpr int kRing = 148 * 1024;    // LDS bytes of the operand ring
 constexpr int kTrash = 1024;         // LDS target of padding DMAs
 
-typedef float v16f __attribute__((ext_vector_type(16)));
-
-template <int NS>
+template <int BM>
 struct WCfg {
-    static constexpr int A_BYTES = NS * 32 * 128;          // activation rows of one K step
-    static constexpr int NSA = (NS + 1) / 2;               // 64-row scale DMAs per step
-    static constexpr int S_BYTES = 256 * NSA;
-    static constexpr int STAGE = A_BYTES + S_BYTES;
-    static constexpr int NST = kRing / STAGE >= 8 ? 8 : kRing / STAGE;   // ring stages
-    static constexpr int A_INSTR = 4 * NS;                 // 1 KB DMAs per step
-    static constexpr int NA = (A_INSTR + kNW - 1) / kNW;   // per wave (padding DMAs even it out)
-    static constexpr int NWB = NS <= 2 ? 8 : 4;            // weight buffers (divide K/128)
-    static constexpr int PER_STEP = 4 + NA + 1;            // loads per wave per step: W, A, row scales
-    // At the top of step kb this wave needs W(kb) (issued NWB-1 iterations
-    // earlier, followed by that iteration's A/scale DMAs) and A(kb) (issued
-    // NST-1 iterations earlier).  Loads retire in order, so waiting until at
-    // most X are outstanding retires both.
-    static constexpr int XW = NA + 1 + (NWB - 2) * PER_STEP;
-    static constexpr int XA = (NST - 2) * PER_STEP;
-    static constexpr int X = XW < XA ? XW : XA;
-    static constexpr int PRO = (NST > NWB ? NST : NWB) - 1; // prologue iterations
+    static constexpr int NS16 = BM / 16;                   // 16-token subtiles per tile
+    static constexpr int MI = NS16 / 2;                    // per wave row
+    static constexpr int A_BYTES = BM * 128;               // activation rows of one K step
+    static constexpr int W_BYTES = 256 * 128;              // weight rows of one K step
+    static constexpr int S_BYTES = BM * 4;                 // activation row scales
+    static constexpr int STAGE = A_BYTES + W_BYTES + S_BYTES;
+    static constexpr int NST = kRing / STAGE;              // ring stages
+    static constexpr int NA = BM / 8 / kNW;                // 1 KB activation DMAs per wave and step
+    static constexpr int NB = 256 / 8 / kNW;               // 1 KB weight DMAs per wave and step
+    static constexpr int NSA = S_BYTES / 256;              // scale DMAs (waves 0 .. NSA-1)
+    static constexpr int PER_STEP = NA + NB + 1;           // loads per wave per step
+    static_assert(BM % 64 == 0 && NST >= 2, "tile");
 };
 
 __device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }
@@ -81,275 +74,248 @@ __device__ __forceinline__ void dma4(const uint8_t *sbase, uint32_t voff, uint32
 {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
-
-// The four 16-byte weight chunks of one K step of this lane's row:
-// K bytes 16h + {0, 32, 64, 96} (h = lane / 32).  Results arrive
-// asynchronously; wait_w() orders their use after the matching s_waitcnt.
-__device__ __forceinline__ void load_w(v4i (&w)[4], const uint8_t *sbase, uint32_t voff)
-{
-    asm volatile(
-        "global_load_dwordx4 %0, %4, %5\n\t"
-        "global_load_dwordx4 %1, %4, %5 offset:32\n\t"
-        "global_load_dwordx4 %2, %4, %5 offset:64\n\t"
-        "global_load_dwordx4 %3, %4, %5 offset:96"
-        : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3])
-        : "v"(voff), "s"(sbase)
-        : "memory");
-}
-template <int N>
-__device__ __forceinline__ void wait_w(v4i (&w)[4])
-{
-    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]) : "n"(N) : "memory");
-}
 template <int N>
 __device__ __forceinline__ void wait_vm()
 {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-__device__ __forceinline__ bool find_tile(const GemmArgs &a, int &e, int &m0, int &rows)
+template <int BM, bool GATEUP>
+__device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int rows, int slab, uint8_t *smem)
 {
-    const int i = a.tile_off[a.e_lo] + (int)blockIdx.y;
-    if (i >= a.tile_off[a.e_hi]) return false;
-    int lo = a.e_lo, hi = a.e_hi - 1;   // largest e with tile_off[e] <= i
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (a.tile_off[mid] <= i) lo = mid; else hi = mid - 1;
-    }
-    e = lo;
-    m0 = (i - a.tile_off[e]) * kBM;
-    rows = a.offsets[e + 1] - a.offsets[e] - m0;
-    return rows > 0;
-}
+    using C = WCfg<BM>;
+    const int KB = a.K / 128;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int n0 = slab * (GATEUP ? 128 : 256);
+    const bool shared = e == a.E;
+    const int Nrows = GATEUP ? 2 * a.N : a.N;
+    const uint8_t *Bexp = shared ? a.Bsh : a.B + (size_t)e * Nrows * a.K;
 
-struct TileCtx {
-    int e, rows, pos0, KB, n0, wave, lane, r, h;
-    const uint8_t *Bexp;       // this expert's weight rows
-    const float *sB;           // LDS: weight block scales [2][KB]
-    uint8_t *smem;
-};
-
-template <bool GATEUP, int NS>
-__device__ __forceinline__ void run_tile(const GemmArgs &a, const TileCtx &t)
-{
-    using C = WCfg<NS>;
-    const int KB = t.KB, lane = t.lane, wave = t.wave, r = t.r, h = t.h;
-    uint8_t *smem = t.smem;
     uint8_t *trash = smem + kRing;
+    float *sB = reinterpret_cast<float *>(trash + kTrash);                 // [2][KB]
+    float *red = sB + 2 * KB;                                              // [4][BM]
     const uint32_t ring_lds = lds_addr(smem), trash_lds = lds_addr(trash);
 
-    auto token_of = [&](int row) -> int {
-        const int p = t.pos0 + min(row, t.rows - 1);
-        return a.row_token ? a.row_token[p] : p;
-    };
+    // ---- weight block scales of the slab: gate_up [gate blk][KB], [up blk][KB];
+    //      down [n0/128][KB], [n0/128 + 1][KB]
+    {
+        const float *Bsf = shared ? a.Bssh : reinterpret_cast<const float *>(a.Bs) + (size_t)e * (Nrows / 128) * KB;
+        for (int q = tid; q < 2 * KB; q += kNT) {
+            const int b = q / KB, kb = q % KB;
+            const int nb = GATEUP ? (b ? a.N + n0 : n0) / 128 : n0 / 128 + b;
+            sB[q] = Bsf[(size_t)nb * KB + kb];
+        }
+    }
 
     // ---- per-lane DMA source offsets (the K offset goes into the scalar base) ----
-    uint32_t oA[C::NA];
+    auto token_of = [&](int row) -> int {
+        const int p = pos0 + min(row, rows - 1);
+        return a.row_token ? a.row_token[p] : p;
+    };
+    uint32_t oA[C::NA], oW[C::NB];
 #pragma unroll
     for (int u = 0; u < C::NA; ++u) {
-        const int q = wave + kNW * u;                 // 1 KB DMA instruction of the step
-        const int row = q < C::A_INSTR ? 8 * q + (lane >> 3) : 0;
+        const int row = 8 * (wave + kNW * u) + (lane >> 3);
         oA[u] = (uint32_t)token_of(row) * (uint32_t)a.K + (uint32_t)(swz8(row, lane & 7) * 16);
+    }
+#pragma unroll
+    for (int u = 0; u < C::NB; ++u) {
+        const int R = 8 * (wave + kNW * u) + (lane >> 3);        // weight row of the LDS tile
+        const int wr = GATEUP ? (R < 128 ? n0 + R : a.N + n0 + R - 128) : n0 + R;
+        oW[u] = (uint32_t)wr * (uint32_t)a.K + (uint32_t)(swz8(R, lane & 7) * 16);
     }
     const bool sa_real = wave < C::NSA;
     const uint32_t oS = (uint32_t)token_of(sa_real ? 64 * wave + lane : 0) * (uint32_t)(KB * 4);
-    // this lane's weight row: A-operand row r of the wave's 32
-    int wrow;
-    if (GATEUP) wrow = (r < 16 ? 0 : a.N) + t.n0 + 16 * wave + (r & 15);
-    else wrow = t.n0 + 32 * wave + r;
-    const uint32_t oW = (uint32_t)wrow * (uint32_t)a.K + 16 * h;
     const uint8_t *gS = reinterpret_cast<const uint8_t *>(a.As);
 
-    auto issue_a = [&](int kb) {   // A rows + row scales of step kb into its ring stage
-        const int kk = kb < 0 ? 0 : (kb < KB ? kb : KB - 1);
-        const bool live = kb >= 0;
-        const uint32_t st = ring_lds + (uint32_t)((live ? kb % C::NST : 0) * C::STAGE);
+    auto issue = [&](int kb) {   // operands of step kb into ring stage kb % NST (past the end: reload)
+        const int kk = kb < KB ? kb : KB - 1;
+        const uint32_t st = ring_lds + (uint32_t)((kb % C::NST) * C::STAGE);
 #pragma unroll
-        for (int u = 0; u < C::NA; ++u) {
-            const int q = wave + kNW * u;
-            dma16(a.A + (size_t)kk * 128, oA[u], (live && q < C::A_INSTR) ? st + 1024 * q : trash_lds);
-        }
-        dma4(gS + (size_t)kk * 4, oS, (live && sa_real) ? st + C::A_BYTES + 256 * wave : trash_lds);
+        for (int u = 0; u < C::NA; ++u) dma16(a.A + (size_t)kk * 128, oA[u], st + 1024 * (wave + kNW * u));
+#pragma unroll
+        for (int u = 0; u < C::NB; ++u)
+            dma16(Bexp + (size_t)kk * 128, oW[u], st + C::A_BYTES + 1024 * (wave + kNW * u));
+        dma4(gS + (size_t)kk * 4, oS, sa_real ? st + C::A_BYTES + C::W_BYTES + 256 * wave : trash_lds);
     };
 
-    v4i wb[C::NWB][4];
+    // the wave's four 16-row A tiles (rows of the LDS weight tile)
+    int wrow[4];
 #pragma unroll
-    for (int b = 0; b < C::NWB; ++b)
+    for (int j = 0; j < 4; ++j)
+        wrow[j] = GATEUP ? (j < 2 ? 0 : 128) + 32 * wn + 16 * (j & 1) + r16 : 64 * wn + 16 * j + r16;
+    // 16-token subtiles of this wave: s16 = wm + 2 i, live when 16 s16 < rows
+    int nlive = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) wb[b][j] = v4i{0, 0, 0, 0};
+    for (int i = 0; i < C::MI; ++i) nlive += 16 * (wm + 2 * i) < rows ? 1 : 0;
 
-    v16f acc[NS];
+    v4f acc[C::MI][4];
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
+    for (int i = 0; i < C::MI; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[s][v] = 0.f;
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    __syncthreads();   // weight scale table visible; previous users of the ring done
-    // prologue: the steady-state issue pattern for iterations -PRO .. -1
+    __syncthreads();   // sB visible
 #pragma unroll
-    for (int j = -C::PRO; j < 0; ++j) {
-        const int kw = j + C::NWB - 1;
-        load_w(wb[((kw % C::NWB) + C::NWB) % C::NWB], t.Bexp + (size_t)(kw < 0 ? 0 : (kw < KB ? kw : KB - 1)) * 128, oW);
-        issue_a(j + C::NST - 1);
-    }
+    for (int s = 0; s < C::NST - 1; ++s) issue(s);
 
-    const int wblk = GATEUP ? 0 : (wave >> 2);       // down: the wave's 128-row scale block
-    for (int kb0 = 0; kb0 < KB; kb0 += C::NWB) {
+    const int sbi = GATEUP ? 0 : (wn >> 1);   // down: the wave's 128-row scale block
+    for (int kb = 0; kb < KB; ++kb) {
+        wait_vm<(C::NST - 2) * C::PER_STEP>();   // this wave's DMAs of step kb landed
+        __syncthreads();                          // ... and every wave's; stage kb-1 is free
+        issue(kb + C::NST - 1);
+        const uint8_t *sA = smem + (kb % C::NST) * C::STAGE;
+        const uint8_t *sW = sA + C::A_BYTES;
+        const float *sS = reinterpret_cast<const float *>(sW + C::W_BYTES);
+        const float sb0 = sB[sbi * KB + kb];
+        const float sb1 = GATEUP ? sB[KB + kb] : sb0;
+
+        // Operand layout of v_mfma_f32_16x16x128_f8f6f4: lane 16g + r holds row r
+        // with K bytes [16g, 16g+16) and [64+16g, 64+16g+16): LDS chunks g, g+4.
+        v8i wf[4];
 #pragma unroll
-        for (int u = 0; u < C::NWB; ++u) {   // K/128 is a multiple of NWB: no guards
-            const int kb = kb0 + u;
-            {
-                wait_w<C::X>(wb[u]);
-                __syncthreads();                      // A(kb) of every wave landed; stage kb-1 free
-                {
-                    const int kw = kb + C::NWB - 1;
-                    load_w(wb[(u + C::NWB - 1) % C::NWB], t.Bexp + (size_t)(kw < KB ? kw : KB - 1) * 128, oW);
-                    issue_a(kb + C::NST - 1);
-                }
-                const uint8_t *sA = smem + (kb % C::NST) * C::STAGE;
-                const float *sS = reinterpret_cast<const float *>(sA + C::A_BYTES);
-                const float sb0 = t.sB[wblk * KB + kb];
-                const float sb1 = GATEUP ? t.sB[KB + kb] : sb0;
-                const v8i w01 = cat(wb[u][0], wb[u][1]), w23 = cat(wb[u][2], wb[u][3]);
-                // One subtile at a time (the other wave of the SIMD covers the LDS
-                // latency); the scheduling barrier keeps the compiler from hoisting
-                // every subtile's reads to the top of the step (NS x 16 live VGPRs).
-                auto read_b = [&](int s, v4i (&b)[4]) {
-                    const int row = 32 * s + r;
-                    const uint8_t *rp = sA + row * 128;
+        for (int j = 0; j < 4; ++j) {
+            const uint8_t *rp = sW + wrow[j] * 128;
+            wf[j] = cat(*reinterpret_cast<const v4i *>(rp + swz8(wrow[j], g) * 16),
+                        *reinterpret_cast<const v4i *>(rp + swz8(wrow[j], g + 4) * 16));
+        }
+        auto read_b = [&](int i) -> v8i {
+            const int row = 16 * (wm + 2 * i) + r16;
+            const uint8_t *rp = sA + row * 128;
+            return cat(*reinterpret_cast<const v4i *>(rp + swz8(row, g) * 16),
+                       *reinterpret_cast<const v4i *>(rp + swz8(row, g + 4) * 16));
+        };
+        // Subtile i: read B(i+1), 4 MFMAs on B(i), fold the products of i-1.
+        v8i bx = read_b(0);
+        v4f q[2][4];
+        float cq0[2], cq1[2];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const v4i *>(rp + swz8(row, 2 * j + h) * 16);
-                };
+        for (int i = 0; i <= C::MI; ++i) {
+            if (i < C::MI && i < nlive) {
+                const v8i bc = bx;
+                if (i + 1 < C::MI && i + 1 < nlive) bx = read_b(i + 1);
+                const float sa = sS[16 * (wm + 2 * i) + r16];
 #pragma unroll
-                for (int s = 0; s < NS; ++s) {
-                    v4i bc[4];
-                    read_b(s, bc);
-                    const float sa = sS[32 * s + r];
-                    v16f p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w01, cat(bc[0], bc[1]), v16f{}, 0, 0, 0, 0, 0, 0);
-                    p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w23, cat(bc[2], bc[3]), p, 0, 0, 0, 0, 0, 0);
-                    const float c0 = sa * sb0, c1 = sa * sb1;
+                for (int j = 0; j < 4; ++j)
+                    q[i & 1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[j], bc, v4f{0.f, 0.f, 0.f, 0.f},
+                                                                                  0, 0, 0, 0, 0, 0);
+                cq0[i & 1] = sa * sb0;
+                cq1[i & 1] = sa * sb1;
+            }
+            if (i >= 1 && i - 1 < nlive) {
+                const int m = i - 1;
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) acc[s][v] = __builtin_fmaf(p[v], v < 8 ? c0 : c1, acc[s][v]);
-                    __builtin_amdgcn_sched_barrier(0);
+                for (int j = 0; j < 4; ++j) {
+                    const float c = (GATEUP && j >= 2) ? cq1[m & 1] : cq0[m & 1];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[m][j][v] = __builtin_fmaf(q[m & 1][j][v], c, acc[m][j][v]);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
-    wait_vm<0>();      // the clamped DMAs past the last step must land before the ring is reused
-    __syncthreads();
+    wait_vm<0>();      // the clamped DMAs past the last step land before the block ends
 
     // ------------------------------------------------------------ epilogue
-    // acc[s][v]: token row 32 s + r; A-operand row 8 (v / 4) + 4 h + (v % 4).
+    // acc[i][j][v]: token row 16 (wm + 2 i) + r16; A-tile j row 4 g + v.
     if (GATEUP) {
-        // act feature (within the block's 128 columns) of v < 8: 16 w + 8 (v/4) + 4 h + v%4
-        float *red = reinterpret_cast<float *>(smem);          // [kNW][kBM] wave amax per token
-        float act[NS][8];
+        // act feature (within the block's 128): 32 wn + 16 jj + 4 g + v, jj = 0, 1
+        float act[C::MI][2][4];
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
+        for (int i = 0; i < C::MI; ++i) {
             float m = 0.f;
 #pragma unroll
-            for (int v = 0; v < 8; ++v) {
-                const float g = acc[s][v], u = acc[s][v + 8];
-                act[s][v] = g * fast_sigmoid(g) * u;
-                m = fmaxf(m, __builtin_fabsf(act[s][v]));
-            }
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float gt = acc[i][jj][v], up = acc[i][jj + 2][v];
+                    act[i][jj][v] = gt * fast_sigmoid(gt) * up;
+                    m = fmaxf(m, __builtin_fabsf(act[i][jj][v]));
+                }
+            m = fmaxf(m, __shfl_xor(m, 16, WAVE));
             m = fmaxf(m, __shfl_xor(m, 32, WAVE));
-            if (h == 0) red[wave * kBM + 32 * s + r] = m;
+            if (g == 0) red[wn * BM + 16 * (wm + 2 * i) + r16] = m;
         }
         __syncthreads();
         float *Cs = reinterpret_cast<float *>(a.Cs);
         const int nsc = a.N / 128;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int row = 32 * s + r;
+        for (int i = 0; i < C::MI; ++i) {
+            const int row = 16 * (wm + 2 * i) + r16;
             float amax = 0.f;
 #pragma unroll
-            for (int w = 0; w < kNW; ++w) amax = fmaxf(amax, red[w * kBM + row]);
+            for (int w = 0; w < 4; ++w) amax = fmaxf(amax, red[w * BM + row]);
             const float inv = amax == 0.f ? 0.f : __fdiv_rn(448.0f, amax);
-            if (row < t.rows) {
-                const size_t pos = (size_t)(t.pos0 + row);
-                uint8_t *dst = a.Cq + pos * a.N + t.n0 + 16 * wave + 4 * h;
+            if (row < rows) {
+                const size_t pos = (size_t)(pos0 + row);
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
+                for (int jj = 0; jj < 2; ++jj) {
                     float x[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) x[i] = fminf(fmaxf(act[s][4 * q + i] * inv, -448.f), 448.f);
-                    *reinterpret_cast<uint32_t *>(dst + 8 * q) =
+                    for (int v = 0; v < 4; ++v) x[v] = fminf(fmaxf(act[i][jj][v] * inv, -448.f), 448.f);
+                    *reinterpret_cast<uint32_t *>(a.Cq + pos * a.N + n0 + 32 * wn + 16 * jj + 4 * g) =
                         e4m3_pack2_hw(x[0], x[1]) | (e4m3_pack2_hw(x[2], x[3]) << 16);
                 }
-                if (wave == 0 && h == 0) Cs[pos * nsc + t.n0 / 128] = amax == 0.f ? 1.0f : __fdiv_rn(amax, 448.0f);
+                if (wn == 0 && g == 0) Cs[pos * nsc + n0 / 128] = amax == 0.f ? 1.0f : __fdiv_rn(amax, 448.0f);
             }
         }
     } else {
-        // output column n0 + 32 w + 8 q + 4 h + i holds acc[s][4 q + i]
+        // output column n0 + 64 wn + 16 j + 4 g + v
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int row = 32 * s + r;
-            if (row < t.rows) {
-                uint16_t *dst = a.Cy + (size_t)(t.pos0 + row) * a.ldc + t.n0 + 32 * wave + 4 * h;
+        for (int i = 0; i < C::MI; ++i) {
+            const int row = 16 * (wm + 2 * i) + r16;
+            if (row < rows) {
+                uint16_t *dst = a.Cy + (size_t)(pos0 + row) * a.ldc + n0 + 64 * wn + 4 * g;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int j = 0; j < 4; ++j) {
                     v2i pk;
-                    pk[0] = (int)((uint32_t)bf16_from_f32(acc[s][4 * q]) | ((uint32_t)bf16_from_f32(acc[s][4 * q + 1]) << 16));
-                    pk[1] = (int)((uint32_t)bf16_from_f32(acc[s][4 * q + 2]) |
-                                  ((uint32_t)bf16_from_f32(acc[s][4 * q + 3]) << 16));
-                    *reinterpret_cast<v2i *>(dst + 8 * q) = pk;
+                    pk[0] = (int)((uint32_t)bf16_from_f32(acc[i][j][0]) | ((uint32_t)bf16_from_f32(acc[i][j][1]) << 16));
+                    pk[1] = (int)((uint32_t)bf16_from_f32(acc[i][j][2]) | ((uint32_t)bf16_from_f32(acc[i][j][3]) << 16));
+                    *reinterpret_cast<v2i *>(dst + 16 * j) = pk;
                 }
             }
         }
     }
 }
 
-template <bool GATEUP>
+template <int BM, bool GATEUP>
 __global__ __launch_bounds__(kNT) void moe_gemm_wide_kernel(GemmArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    TileCtx t;
-    int m0;
-    if (!find_tile(a, t.e, m0, t.rows)) return;
-    if (t.rows > kBM) t.rows = kBM;
-    const bool shared = t.e == a.E;
-    t.pos0 = a.offsets[t.e] + m0;
-    t.KB = a.K / 128;
-    t.lane = threadIdx.x & 63;
-    t.wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    t.r = t.lane & 31;
-    t.h = t.lane >> 5;
-    t.n0 = blockIdx.x * (GATEUP ? 128 : 256);
-    t.smem = smem;
-    const int Nrows = GATEUP ? 2 * a.N : a.N;
-    t.Bexp = shared ? a.Bsh : a.B + (size_t)t.e * Nrows * a.K;
-
-    // weight block scales of the slab: gate_up [gate block][KB], [up block][KB];
-    // down [n0/128][KB], [n0/128 + 1][KB]
-    float *sB = reinterpret_cast<float *>(smem + kRing + kTrash);
-    {
-        const float *Bsf = shared ? a.Bssh : reinterpret_cast<const float *>(a.Bs) + (size_t)t.e * (Nrows / 128) * t.KB;
-        for (int q = threadIdx.x; q < 2 * t.KB; q += kNT) {
-            const int b = q / t.KB, kb = q % t.KB;
-            const int nb = GATEUP ? (b ? a.N + t.n0 : t.n0) / 128 : t.n0 / 128 + b;
-            sB[q] = Bsf[(size_t)nb * t.KB + kb];
-        }
-    }
-    t.sB = sB;
-
-    switch ((t.rows + 31) >> 5) {
-    case 1: run_tile<GATEUP, 1>(a, t); break;
-    case 2: run_tile<GATEUP, 2>(a, t); break;
-    case 3: run_tile<GATEUP, 3>(a, t); break;
-    case 4: run_tile<GATEUP, 4>(a, t); break;
-    case 5: run_tile<GATEUP, 5>(a, t); break;
-    default: run_tile<GATEUP, 6>(a, t); break;
-    }
+    const int4 *tab = reinterpret_cast<const int4 *>(a.tile_tab);
+    if ((int)blockIdx.y >= tab[0].x) return;
+    const int4 d = tab[1 + blockIdx.y];   // {expert, first position, rows}
+    const int slab = (int)blockIdx.x;
+    run_tile<BM, GATEUP>(a, d.x, d.y, d.z, slab, smem);
 }
 
-template <bool GATEUP>
+// Tile table for tiles of bm rows over the segments [e_lo, e_hi): entry 0 holds
+// the tile count, entries 1.. {expert, first position, rows, 0}.  The shared
+// segment (e == E), when included, comes first: its tiles are full and long.
+__global__ void build_tiles_kernel(const int32_t *__restrict__ offsets, const int32_t *__restrict__ tile_off,
+                                   int e_lo, int e_hi, int E, int bm, int4 *__restrict__ tab)
+{
+    const int e = e_lo + (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    const bool with_shared = e_hi > E;
+    const int nsh = with_shared ? tile_off[E + 1] - tile_off[E] : 0;
+    if (e == e_lo) tab[0] = int4{tile_off[e_hi] - tile_off[e_lo], 0, 0, 0};
+    if (e >= e_hi) return;
+    const int cnt = offsets[e + 1] - offsets[e];
+    const int base = e == E ? 0 : nsh + tile_off[e] - tile_off[e_lo];
+    for (int t = 0; t * bm < cnt; ++t)
+        tab[1 + base + t] = int4{e, offsets[e] + t * bm, min(bm, cnt - t * bm), 0};
+}
+
+template <int BM, bool GATEUP>
 int launch_wide(const GemmArgs &a, int grid_y, hipStream_t st)
 {
     if (grid_y <= 0) return XS_OK;
-    const size_t smem = (size_t)kRing + kTrash + 8 * (size_t)(a.K / 128);
+    const size_t smem = (size_t)kRing + kTrash + 8 * (size_t)(a.K / 128) + 4 * 4 * BM;
     if (smem > 160 * 1024) return set_error(XS_ERR_UNSUPPORTED, "K=%d needs %zu bytes of LDS", a.K, smem);
-    auto fn = moe_gemm_wide_kernel<GATEUP>;
+    auto fn = moe_gemm_wide_kernel<BM, GATEUP>;
     static bool attr_set = false;
     if (!attr_set) {
         XS_HIP(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
@@ -363,14 +329,33 @@ int launch_wide(const GemmArgs &a, int grid_y, hipStream_t st)
 
 }  // namespace
 
-int wide_tile_rows() { return kBM; }
+// 192-row tiles: 2 ring stages; 128-row tiles (3 stages) measured slower on the
+// V4-Flash prefill layer (more weight re-reads across an expert's tiles).
+constexpr int kWideBM = 192;
+int wide_tile_rows() { return kWideBM; }
+
+size_t wide_tile_table_bytes(int64_t rows_routed, int64_t rows_shared, int64_t E)
+{
+    const int64_t bm = wide_tile_rows();
+    return (size_t)16 * (size_t)(rows_routed / bm + E + rows_shared / bm + 3);
+}
+
+int launch_tile_table(const GemmArgs &a, hipStream_t st)
+{
+    const int n = a.e_hi - a.e_lo;
+    if (n <= 0) return XS_OK;
+    build_tiles_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(
+        a.offsets, a.tile_off, a.e_lo, a.e_hi, a.E, a.bm, reinterpret_cast<int4 *>(const_cast<int32_t *>(a.tile_tab)));
+    XS_LAUNCH_CHECK();
+    return XS_OK;
+}
 
 int launch_gemm_wide(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
 {
-    if (a.bm != kBM) return set_error(XS_ERR_INVALID, "wide GEMM needs tile offsets for %d-row tiles", kBM);
-    if (a.K % 1024 || (gateup ? a.N % 128 : a.N % 256))
+    if (a.bm != wide_tile_rows()) return set_error(XS_ERR_INVALID, "wide GEMM needs %d-row tiles", wide_tile_rows());
+    if (a.K % 128 || (gateup ? a.N % 128 : a.N % 256) || !a.tile_tab)
         return set_error(XS_ERR_UNSUPPORTED, "wide GEMM shape K=%d N=%d", a.K, a.N);
-    return gateup ? launch_wide<true>(a, grid_y, st) : launch_wide<false>(a, grid_y, st);
+    return gateup ? launch_wide<kWideBM, true>(a, grid_y, st) : launch_wide<kWideBM, false>(a, grid_y, st);
 }
 
 }  // namespace xs
