@@ -132,6 +132,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="prefill only, no extra configs")
+    ap.add_argument("--sections", default="prefill,decode,gemm,fp4",
+                    help="comma list of prefill,decode,gemm,fp4 (the JSON line needs prefill)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=8)
     a = ap.parse_args()
@@ -147,7 +149,24 @@ def main():
 
     dev_name = torch.cuda.get_device_name(0)
     log(f"device: {dev_name}")
-    # ---------------- prefill (headline) ----------------
+    sections = set(a.sections.split(","))
+    if a.quick:
+        sections &= {"prefill"}
+    res = {}
+    if "prefill" in sections:
+        res = prefill(a, X, torch)
+    if "decode" in sections:
+        res["decode"] = decode(a, X, torch)
+    if "gemm" in sections:
+        res["gemm_fp8_512x4096x4096"] = single_gemm(a, X, torch)
+    if "fp4" in sections:
+        res["fp4_2048"] = fp4_layer(a, X, torch)
+    print(json.dumps(res))
+    return 0
+
+
+def prefill(a, X, torch):
+    from moe_synth import synth_layer, layer_from, expert_bytes, layer_flops
     T = 8192
     g = synth_layer(T, H, I, E, K_TOP, seed=0, zipf=1.1)
     layer = layer_from(g)
@@ -195,56 +214,66 @@ def main():
         res["cpu_baseline"] = {kk: cb[kk] for kk in ("value", "unit", "cores", "kind", "sample")}
     del g
     torch.cuda.empty_cache()
+    return res
 
-    if not a.quick:
-        # ---------------- decode (HBM-bound) ----------------
-        dec = {}
-        gd = synth_layer(256, H, I, E, K_TOP, seed=1, bias_std=0.0)
-        for Td in (1, 16, 64, 256):
-            L = layer_from(gd)
-            xd = gd["x"][:Td].contiguous()
-            msd, st = time_forward(L, xd, max(a.steps, 50), a.warmup, profile=True)
-            ned = routed_expert_count(L, xd)
-            by = (ned + 1) * expert_bytes(H, I, False) + E * H * 2 + Td * H * 4
-            dec[str(Td)] = {"ms": msd, "experts_touched": ned + 1, "hbm_gbs": by / (msd * 1e-3) / 1e9,
-                            "frac_hbm_peak": by / (msd * 1e-3) / 1e9 / PEAK_HBM_GBS,
-                            "tokens_per_s": Td / (msd * 1e-3), "stage_ms": st}
-        res["decode"] = dec
-        del gd
-        torch.cuda.empty_cache()
-        # ---------------- single FP8 GEMM ----------------
-        gen = torch.Generator(device="cuda")
-        gen.manual_seed(2)
-        A = torch.randn((512, 4096), generator=gen, device="cuda").to(torch.bfloat16)
-        Wt = torch.randn((4096, 4096), generator=gen, device="cuda", dtype=torch.bfloat16) * 0.02
-        bq, bs = X.quant_weight_fp8_block(Wt)
-        C_ = torch.empty((512, 4096), dtype=torch.bfloat16, device="cuda")
-        ws = torch.empty(X.lib().xs_gemm_fp8_blockscale_workspace_size(512, 4096), dtype=torch.uint8, device="cuda")
-        for _ in range(a.warmup):
-            X.gemm_fp8_blockscale(A, bq, bs, out=C_, workspace=ws)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        n = 50
-        for _ in range(n):
-            X.gemm_fp8_blockscale(A, bq, bs, out=C_, workspace=ws)
-        e1.record()
-        torch.cuda.synchronize()
-        gms = e0.elapsed_time(e1) / n
-        gfl = 2 * 512 * 4096 * 4096
-        res["gemm_fp8_512x4096x4096"] = {"ms": gms, "tflops": gfl / (gms * 1e-3) / 1e12,
-                                         "frac_fp8_peak": gfl / (gms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS}
-        # ---------------- MXFP4 routed experts ----------------
-        g4 = synth_layer(2048, H, I, E, K_TOP, seed=3, fp4=True)
-        L4 = layer_from(g4)
-        ms4, st4 = time_forward(L4, g4["x"], a.steps, a.warmup, profile=True)
-        ne4 = routed_expert_count(L4, g4["x"])
-        by4 = ne4 * expert_bytes(H, I, True) + expert_bytes(H, I, False) + E * H * 2
-        fl4 = layer_flops(2048, H, I, E, K_TOP)
-        res["fp4_2048"] = {"ms": ms4, "tokens_per_s": 2048 / (ms4 * 1e-3), "tflops": fl4 / (ms4 * 1e-3) / 1e12,
-                           "hbm_gbs_weights": by4 / (ms4 * 1e-3) / 1e9, "stage_ms": st4}
-    print(json.dumps(res))
-    return 0
+
+def decode(a, X, torch):
+    """T in {1, 16, 64, 256}, uniform routing; HBM bytes = weights of
+    the experts touched + shared + router + activations."""
+    from moe_synth import synth_layer, layer_from, expert_bytes
+    dec = {}
+    gd = synth_layer(256, H, I, E, K_TOP, seed=1, bias_std=0.0)
+    for Td in (1, 16, 64, 256):
+        L = layer_from(gd)
+        xd = gd["x"][:Td].contiguous()
+        msd, st = time_forward(L, xd, max(a.steps, 50), a.warmup, profile=True)
+        ned = routed_expert_count(L, xd)
+        by = (ned + 1) * expert_bytes(H, I, False) + E * H * 2 + Td * H * 4
+        dec[str(Td)] = {"ms": msd, "experts_touched": ned + 1, "hbm_gbs": by / (msd * 1e-3) / 1e9,
+                        "frac_hbm_peak": by / (msd * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                        "tokens_per_s": Td / (msd * 1e-3), "stage_ms": st}
+    del gd
+    torch.cuda.empty_cache()
+    return dec
+
+
+def single_gemm(a, X, torch):
+    """one FP8 block-scaled GEMM 512 x 4096 x 4096 (bf16 A, e4m3 B)."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2)
+    A = torch.randn((512, 4096), generator=gen, device="cuda").to(torch.bfloat16)
+    Wt = torch.randn((4096, 4096), generator=gen, device="cuda", dtype=torch.bfloat16) * 0.02
+    bq, bs = X.quant_weight_fp8_block(Wt)
+    C_ = torch.empty((512, 4096), dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(X.lib().xs_gemm_fp8_blockscale_workspace_size(512, 4096), dtype=torch.uint8, device="cuda")
+    for _ in range(a.warmup):
+        X.gemm_fp8_blockscale(A, bq, bs, out=C_, workspace=ws)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    n = 50
+    for _ in range(n):
+        X.gemm_fp8_blockscale(A, bq, bs, out=C_, workspace=ws)
+    e1.record()
+    torch.cuda.synchronize()
+    gms = e0.elapsed_time(e1) / n
+    gfl = 2 * 512 * 4096 * 4096
+    return {"ms": gms, "tflops": gfl / (gms * 1e-3) / 1e12, "frac_fp8_peak": gfl / (gms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS}
+
+
+def fp4_layer(a, X, torch):
+    """MXFP4 routed experts (FP8 shared), 2048 tokens."""
+    from moe_synth import synth_layer, layer_from, expert_bytes, layer_flops
+    g4 = synth_layer(2048, H, I, E, K_TOP, seed=3, fp4=True)
+    L4 = layer_from(g4)
+    ms4, st4 = time_forward(L4, g4["x"], a.steps, a.warmup, profile=True)
+    ne4 = routed_expert_count(L4, g4["x"])
+    by4 = ne4 * expert_bytes(H, I, True) + expert_bytes(H, I, False) + E * H * 2
+    fl4 = layer_flops(2048, H, I, E, K_TOP)
+    return {"ms": ms4, "tokens_per_s": 2048 / (ms4 * 1e-3), "tflops": fl4 / (ms4 * 1e-3) / 1e12,
+            "hbm_gbs_weights": by4 / (ms4 * 1e-3) / 1e9, "stage_ms": st4}
+
+
 
 
 if __name__ == "__main__":

@@ -82,7 +82,7 @@ static WsLayout layout(const xs_moe_params *p)
     take(L.inv, 4 * S);
     take(L.row_token, 4 * R);
     take(L.tiles, 4 * (E + 2));
-    take(L.tiletab, wide_tile_table_bytes((int64_t)S, p->has_shared ? (int64_t)T : 0, (int64_t)E));
+    take(L.tiletab, tile_table_bytes((int64_t)S, p->has_shared ? (int64_t)T : 0, (int64_t)E, 16));
     take(L.xq, T * H);
     take(L.xs, 4 * T * (H / 128));
     take(L.xmq, fp4 ? T * H : 0);
@@ -177,9 +177,9 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     po.perm = WS(int32_t, perm);
     po.inv = inv;
     po.row_token = WS(int32_t, row_token);
-    po.tile_off[0] = tiles;
-    po.tile_bm[0] = bm;
-    po.n_tile_sizes = 1;
+    po.tile_off = tiles;
+    po.tab = WS(int32_t, tiletab);
+    po.tile_bm = bm;
     po.offsets_ext = 1;
     rc = launch_permute(idx, mask, T, E, k, shared_rows, WS(int32_t, wordprefix), po, st);
     if (rc) return rc;
@@ -196,6 +196,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     g1.Bssh = t->shared_w13_scale;
     g1.offsets = offsets;
     g1.tile_off = tiles;
+    g1.tile_tab = po.tab;
     g1.E = (int)E;
     g1.K = (int)H;
     g1.N = (int)I;
@@ -210,6 +211,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     g2.Bssh = t->shared_w2_scale;
     g2.offsets = offsets;
     g2.tile_off = tiles;
+    g2.tile_tab = po.tab;
     g2.E = (int)E;
     g2.K = (int)I;
     g2.N = (int)H;
@@ -224,11 +226,6 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g1.Cs = WS(float, acts);
         g1.e_lo = 0;
         g1.e_hi = (int)E + (shared_rows ? 1 : 0);
-        if (wide) {
-            g1.tile_tab = WS(int32_t, tiletab);
-            rc = launch_tile_table(g1, st);
-            if (rc) return rc;
-        }
         rc = wide ? launch_gemm_wide(g1, true, routed_tiles + shared_tiles, st)
                   : launch_gemm(g1, true, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
@@ -236,7 +233,6 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g2.As = WS(float, acts);
         g2.e_lo = 0;
         g2.e_hi = g1.e_hi;
-        g2.tile_tab = g1.tile_tab;
         rc = wide ? launch_gemm_wide(g2, false, routed_tiles + shared_tiles, st)
                   : launch_gemm(g2, false, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
@@ -297,14 +293,18 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
 }
 
 // --------------------------------------------------- single FP8 GEMM (C = A.B^T)
-__global__ void single_segment_kernel(int32_t *offsets, int32_t *tiles, int M, int bm)
+// One segment of M rows: offsets and the tile table (entry 0: {tiles, 0}).
+__global__ void single_segment_kernel(int32_t *offsets, int4 *tab, int M, int bm)
 {
-    offsets[0] = 0;
-    offsets[1] = M;
-    offsets[2] = M;
-    tiles[0] = 0;
-    tiles[1] = (M + bm - 1) / bm;
-    tiles[2] = tiles[1];
+    const int nt = (M + bm - 1) / bm;
+    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i == 0) {
+        offsets[0] = 0;
+        offsets[1] = M;
+        offsets[2] = M;
+        tab[0] = int4{nt, 0, 0, 0};
+    }
+    if (i < nt) tab[1 + i] = int4{0, i * bm, min(bm, M - i * bm), 0};
 }
 
 static size_t gemm_ws(int64_t M, int64_t K, size_t *o_s, size_t *o_meta)
@@ -313,7 +313,7 @@ static size_t gemm_ws(int64_t M, int64_t K, size_t *o_s, size_t *o_meta)
     size_t s = al(4 * (size_t)M * (K / 128));
     *o_s = q;
     *o_meta = q + s;
-    return q + s + 256;
+    return q + s + 256 + al(tile_table_bytes(M, 0, 1, 16));
 }
 
 }  // namespace xs
@@ -380,9 +380,10 @@ int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int
     int rc = launch_quant_act(A, XS_BF16, M, K, (uint8_t *)ws, ws + o_s, 0, st);
     if (rc) return rc;
     int32_t *offsets = (int32_t *)(ws + o_meta);
-    int32_t *tiles = offsets + 4;
+    int4 *tab = reinterpret_cast<int4 *>(ws + o_meta + 256);
     const int bm = M >= 2048 ? 128 : (M >= 1024 ? 64 : (M >= 256 ? 32 : 16));
-    single_segment_kernel<<<1, 1, 0, st>>>(offsets, tiles, (int)M, bm);
+    const int nt = (int)((M + bm - 1) / bm);
+    single_segment_kernel<<<dim3((unsigned)((nt + 256) / 256)), dim3(256), 0, st>>>(offsets, tab, (int)M, bm);
     XS_LAUNCH_CHECK();
     GemmArgs g = {};
     g.A = (const uint8_t *)ws;
@@ -390,7 +391,8 @@ int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int
     g.B = B;
     g.Bs = Bs;
     g.offsets = offsets;
-    g.tile_off = tiles;
+    g.tile_off = nullptr;
+    g.tile_tab = reinterpret_cast<const int32_t *>(tab);
     g.e_lo = 0;
     g.e_hi = 1;
     g.E = 1;

@@ -83,20 +83,22 @@ __device__ __forceinline__ void wait_vmcnt()
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Locate the tile of blockIdx.y: expert e and first row m0 within the expert.
-__device__ __forceinline__ bool find_tile(const GemmArgs &a, int &e, int &m0, int &rows)
+// The tile of blockIdx.y from the tile table (entry 0: {tiles, shared tiles},
+// then {expert, first position, rows}, shared tiles first): a launch over the
+// shared segment only, the routed experts only, or both.
+__device__ __forceinline__ bool find_tile(const GemmArgs &a, int &e, int &pos0, int &rows)
 {
-    const int base = a.tile_off[a.e_lo];
-    const int i = base + (int)blockIdx.y;
-    if (i >= a.tile_off[a.e_hi]) return false;
-    int lo = a.e_lo, hi = a.e_hi - 1;   // largest e with tile_off[e] <= i
-    while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (a.tile_off[mid] <= i) lo = mid; else hi = mid - 1;
-    }
-    e = lo;
-    m0 = (i - a.tile_off[e]) * a.bm;
-    rows = a.offsets[e + 1] - a.offsets[e] - m0;
+    const int4 *tab = reinterpret_cast<const int4 *>(a.tile_tab);
+    const int4 h = tab[0];
+    int lo = 0, hi = h.x;
+    if (a.e_lo >= a.E) hi = h.y;          // shared segment only
+    else if (a.e_hi <= a.E) lo = h.y;     // routed experts only
+    const int i = lo + (int)blockIdx.y;
+    if (i >= hi) return false;
+    const int4 d = tab[1 + i];
+    e = d.x;
+    pos0 = d.y;
+    rows = d.z;
     return rows > 0;
 }
 
@@ -110,11 +112,10 @@ __global__ __launch_bounds__(BM >= 64 ? 512 : 256) void moe_gemm_kernel(GemmArgs
     float *sB = reinterpret_cast<float *>(trash + S::TRASH);          // FP8: [2][KB]
     float *red = sB + 2 * KB;                                         // [WN][BM]
 
-    int e, m0, rows;
-    if (!find_tile(a, e, m0, rows)) return;
+    int e, pos0, rows;
+    if (!find_tile(a, e, pos0, rows)) return;
     if (rows > BM) rows = BM;
     const bool shared = e == a.E;
-    const int pos0 = a.offsets[e] + m0;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / S::WN, wn = wave % S::WN;

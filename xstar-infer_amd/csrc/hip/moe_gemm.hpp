@@ -15,7 +15,7 @@ struct GemmArgs {
     const float *Bssh;         // shared expert scales
     const int32_t *offsets;    // [E+2] row offsets per expert (E = shared segment)
     const int32_t *tile_off;   // [E+2] tile offsets for tile height bm
-    const int32_t *tile_tab;   // wide GEMMs: tile table (launch_tile_table)
+    const int32_t *tile_tab;   // tile table (PermuteOut::tab) for tile height bm
     int e_lo, e_hi;            // experts covered by this launch: [e_lo, e_hi)
     int E;
     int K;                     // reduction length
@@ -29,10 +29,8 @@ struct GemmArgs {
 
 int launch_gemm(const GemmArgs &a, bool gateup, bool fp4, int grid_y, hipStream_t st);
 // Tall-tile FP8 GEMMs (moe_gemm_wide.hip): a.bm must be wide_tile_rows() and
-// a.tile_tab a table filled by launch_tile_table() (wide_tile_table_bytes()).
+// a.tile_tab the tile table for that height.
 int wide_tile_rows();
-size_t wide_tile_table_bytes(int64_t rows_routed, int64_t rows_shared, int64_t E);
-int launch_tile_table(const GemmArgs &a, hipStream_t st);
 int launch_gemm_wide(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st);
 int launch_combine(const uint16_t *y, const int32_t *inv, const float *w, int64_t T, int64_t k,
                    int64_t H, int64_t shared_base, int has_shared, void *out, int out_dtype,

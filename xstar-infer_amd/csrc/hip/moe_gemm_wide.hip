@@ -26,8 +26,8 @@
 //   * per K step each subtile's 4 products are folded into the f32
 //     accumulators with (row scale x block scale) one subtile later, while the
 //     next subtile's MFMAs run; subtiles past the tile's rows are skipped;
-//   * tile descriptors (expert, first row, rows) come from a table built once
-//     per launch, so a block starts with one load instead of a search.
+//   * tile descriptors (expert, first row, rows) come from the table the
+//     permute builds, so a block starts with one load instead of a search.
 #include "moe_gemm.hpp"
 
 namespace xs {
@@ -285,28 +285,11 @@ template <int BM, bool GATEUP>
 __global__ __launch_bounds__(kNT) void moe_gemm_wide_kernel(GemmArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int4 *tab = reinterpret_cast<const int4 *>(a.tile_tab);
+    const int4 *tab = reinterpret_cast<const int4 *>(a.tile_tab);   // shared + routed tiles
     if ((int)blockIdx.y >= tab[0].x) return;
     const int4 d = tab[1 + blockIdx.y];   // {expert, first position, rows}
     const int slab = (int)blockIdx.x;
     run_tile<BM, GATEUP>(a, d.x, d.y, d.z, slab, smem);
-}
-
-// Tile table for tiles of bm rows over the segments [e_lo, e_hi): entry 0 holds
-// the tile count, entries 1.. {expert, first position, rows, 0}.  The shared
-// segment (e == E), when included, comes first: its tiles are full and long.
-__global__ void build_tiles_kernel(const int32_t *__restrict__ offsets, const int32_t *__restrict__ tile_off,
-                                   int e_lo, int e_hi, int E, int bm, int4 *__restrict__ tab)
-{
-    const int e = e_lo + (int)(blockIdx.x * blockDim.x + threadIdx.x);
-    const bool with_shared = e_hi > E;
-    const int nsh = with_shared ? tile_off[E + 1] - tile_off[E] : 0;
-    if (e == e_lo) tab[0] = int4{tile_off[e_hi] - tile_off[e_lo], 0, 0, 0};
-    if (e >= e_hi) return;
-    const int cnt = offsets[e + 1] - offsets[e];
-    const int base = e == E ? 0 : nsh + tile_off[e] - tile_off[e_lo];
-    for (int t = 0; t * bm < cnt; ++t)
-        tab[1 + base + t] = int4{e, offsets[e] + t * bm, min(bm, cnt - t * bm), 0};
 }
 
 template <int BM, bool GATEUP>
@@ -333,22 +316,6 @@ int launch_wide(const GemmArgs &a, int grid_y, hipStream_t st)
 // V4-Flash prefill layer (more weight re-reads across an expert's tiles).
 constexpr int kWideBM = 192;
 int wide_tile_rows() { return kWideBM; }
-
-size_t wide_tile_table_bytes(int64_t rows_routed, int64_t rows_shared, int64_t E)
-{
-    const int64_t bm = wide_tile_rows();
-    return (size_t)16 * (size_t)(rows_routed / bm + E + rows_shared / bm + 3);
-}
-
-int launch_tile_table(const GemmArgs &a, hipStream_t st)
-{
-    const int n = a.e_hi - a.e_lo;
-    if (n <= 0) return XS_OK;
-    build_tiles_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(
-        a.offsets, a.tile_off, a.e_lo, a.e_hi, a.E, a.bm, reinterpret_cast<int4 *>(const_cast<int32_t *>(a.tile_tab)));
-    XS_LAUNCH_CHECK();
-    return XS_OK;
-}
 
 int launch_gemm_wide(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
 {

@@ -65,17 +65,19 @@ int launch_quant_act(const void *x, int dtype, int64_t rows, int64_t cols, uint8
 // shared_rows != 0.
 struct PermuteOut {
     int32_t *counts;      // [E]
-    int32_t *offsets;     // [E+2]: routed offsets, offsets[E+1] = end of the shared segment
-    int32_t *perm;        // [T*k] position -> slot
-    int32_t *inv;         // [T*k] slot -> position
-    int32_t *row_token;   // [T*k + T] position -> token
-    int32_t *tile_off[3]; // per tile size: [E+2] exclusive scan of ceil(count/BM) (incl. shared)
-    int tile_bm[3];
-    int n_tile_sizes;
-    int offsets_ext;      // offsets has E+2 entries
+    int32_t *offsets;     // [E+1], or [E+2] with offsets_ext (shared-segment end at [E+1])
+    int32_t *perm;        // position -> slot (or NULL)
+    int32_t *inv;         // slot -> position (or NULL)
+    int32_t *row_token;   // position -> token, routed then shared rows (or NULL)
+    int32_t *tile_off;    // [E+2] exclusive scan of ceil(count / tile_bm), shared tiles last (or NULL)
+    int32_t *tab;         // tile table (or NULL): entry 0 {tiles, shared tiles}, then
+                          // {expert, first position, rows}, the shared segment's tiles first
+    int tile_bm;
+    int offsets_ext;
 };
 int mask_words_for(int64_t T);
 int launch_mask_clear(uint32_t *mask, int64_t words, hipStream_t st);
+size_t tile_table_bytes(int64_t rows_routed, int64_t rows_shared, int64_t E, int bm);
 int launch_permute(const int32_t *idx, const uint32_t *mask, int64_t T, int64_t E, int64_t k,
                    int shared_rows, int32_t *wordprefix, const PermuteOut &o, hipStream_t st);
 

@@ -68,76 +68,114 @@ __device__ int block_exclusive_scan(int v, int *lds_waves, int *total)
     return r;
 }
 
-struct ScanArgs {
-    const uint32_t *mask;
-    int32_t *wordprefix;
-    int32_t *counts;
-    int32_t *offsets;
-    int32_t *tile_off0, *tile_off1, *tile_off2;
-    int bm0, bm1, bm2;
-    int E, W, shared_rows;
-    int offsets_ext;   // 1: offsets has E+2 entries (shared-segment end at [E+1])
-};
-
-// One block of 1024 threads; thread e < E owns expert e.
-__global__ __launch_bounds__(1024) void permute_scan_kernel(ScanArgs a)
+// Per-expert word prefixes and token counts, one block per expert (large T).
+__global__ __launch_bounds__(256) void permute_count_kernel(const uint32_t *__restrict__ mask, int W,
+                                                            int32_t *__restrict__ wordprefix,
+                                                            int32_t *__restrict__ counts)
 {
     __shared__ int lds[17];
-    const int e = threadIdx.x;
-    int cnt = 0;
-    if (e < a.E) {
-        const uint32_t *m = a.mask + (size_t)e * a.W;
-        int32_t *wp = a.wordprefix + (size_t)e * a.W;
-        for (int w = 0; w < a.W; ++w) {
-            wp[w] = cnt;
-            cnt += __builtin_popcount(m[w]);
-        }
-        a.counts[e] = cnt;
+    const int e = blockIdx.x;
+    int run = 0;
+    for (int base = 0; base < W; base += 256) {
+        const int w = base + (int)threadIdx.x;
+        const int c = w < W ? __builtin_popcount(mask[(size_t)e * W + w]) : 0;
+        int tot;
+        const int ex = block_exclusive_scan(c, lds, &tot);
+        if (w < W) wordprefix[(size_t)e * W + w] = run + ex;
+        run += tot;
     }
-    int total;
-    int off = block_exclusive_scan(e < a.E ? cnt : 0, lds, &total);
-    if (e < a.E) a.offsets[e] = off;
-    if (e == 0) {
-        a.offsets[a.E] = total;
-        if (a.offsets_ext) a.offsets[a.E + 1] = total + a.shared_rows;
-    }
-    int32_t *tiles[3] = {a.tile_off0, a.tile_off1, a.tile_off2};
-    int bms[3] = {a.bm0, a.bm1, a.bm2};
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        if (!tiles[i]) continue;
-        int nt = e < a.E ? (cnt + bms[i] - 1) / bms[i] : 0;
-        int tt;
-        int toff = block_exclusive_scan(nt, lds, &tt);
-        if (e < a.E) tiles[i][e] = toff;
-        if (e == 0) {
-            tiles[i][a.E] = tt;
-            tiles[i][a.E + 1] = tt + (a.shared_rows + bms[i] - 1) / bms[i];
-        }
-    }
+    if (threadIdx.x == 0) counts[e] = run;
 }
 
-__global__ void permute_scatter_kernel(const int32_t *__restrict__ idx, const uint32_t *__restrict__ mask,
-                                       const int32_t *__restrict__ wordprefix,
-                                       const int32_t *__restrict__ offsets, int64_t T, int k, int E,
-                                       int W, int shared_rows, int32_t *__restrict__ perm,
-                                       int32_t *__restrict__ inv, int32_t *__restrict__ row_token)
+struct ScatterArgs {
+    const int32_t *idx;
+    const uint32_t *mask;
+    const int32_t *wordprefix;   // NULL: W <= kSmallWords, prefixes counted inline
+    int32_t *counts;             // computed here when wordprefix is NULL, else read
+    int32_t *offsets;
+    int32_t *tile_off;           // [E+2] or NULL
+    int4 *tab;                   // tile table or NULL
+    int bm;
+    int64_t T;
+    int k, E, W, shared_rows, offsets_ext;
+    int32_t *perm, *inv, *row_token;
+};
+constexpr int kSmallWords = 8;
+
+// 1024 threads per block: every block scans the E counts (thread e owns expert
+// e) into LDS offsets; block 0 also writes counts, offsets, tile offsets and
+// the tile table; then each thread places one slot (or one shared row).
+__global__ __launch_bounds__(1024) void permute_scatter_kernel(ScatterArgs a)
 {
-    const int64_t S = T * k;
-    int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    __shared__ int lds[17];
+    __shared__ int offs[1024];
+    const int e = threadIdx.x;
+    const bool small = a.wordprefix == nullptr;
+    int cnt = 0;
+    if (e < a.E) {
+        if (small) {
+            for (int w = 0; w < a.W; ++w) cnt += __builtin_popcount(a.mask[(size_t)e * a.W + w]);
+        } else {
+            cnt = a.counts[e];
+        }
+    }
+    int total;
+    const int off = block_exclusive_scan(cnt, lds, &total);
+    if (e < a.E) offs[e] = off;
+    if (blockIdx.x == 0) {
+        if (e < a.E) {
+            if (small) a.counts[e] = cnt;
+            a.offsets[e] = off;
+        }
+        if (e == 0) {
+            a.offsets[a.E] = total;
+            if (a.offsets_ext) a.offsets[a.E + 1] = total + a.shared_rows;
+        }
+        if (a.tile_off || a.tab) {
+            const int nt = e < a.E ? (cnt + a.bm - 1) / a.bm : 0;
+            int tt;
+            const int toff = block_exclusive_scan(nt, lds, &tt);
+            const int nsh = (a.shared_rows + a.bm - 1) / a.bm;
+            if (a.tile_off) {
+                if (e < a.E) a.tile_off[e] = toff;
+                if (e == 0) {
+                    a.tile_off[a.E] = tt;
+                    a.tile_off[a.E + 1] = tt + nsh;
+                }
+            }
+            if (a.tab) {
+                // entry 0: {tiles, shared tiles}; the shared segment's tiles first
+                if (e == 0) a.tab[0] = int4{tt + nsh, nsh, 0, 0};
+                if (e < a.E)
+                    for (int t = 0; t < nt; ++t)
+                        a.tab[1 + nsh + toff + t] = int4{e, off + t * a.bm, min(a.bm, cnt - t * a.bm), 0};
+                for (int t = e; t < nsh; t += blockDim.x)
+                    a.tab[1 + t] = int4{a.E, total + t * a.bm, min(a.bm, a.shared_rows - t * a.bm), 0};
+            }
+        }
+    }
+    __syncthreads();
+    const int64_t S = a.T * a.k;
+    const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (s < S) {
-        int e = idx[s];
-        if (e < 0 || e >= E) return;
-        int t = (int)(s / k);
-        size_t wi = (size_t)e * W + (t >> 5);
-        uint32_t below = mask[wi] & ((1u << (t & 31)) - 1u);
-        int pos = offsets[e] + wordprefix[wi] + __builtin_popcount(below);
-        if (perm) perm[pos] = (int32_t)s;
-        if (inv) inv[s] = pos;
-        if (row_token) row_token[pos] = t;
-    } else if (s < S + shared_rows) {
-        int t = (int)(s - S);
-        if (row_token) row_token[S + t] = t;
+        const int ex = a.idx[s];
+        if (ex < 0 || ex >= a.E) return;
+        const int t = (int)(s / a.k);
+        const int wi = t >> 5;
+        const uint32_t *m = a.mask + (size_t)ex * a.W;
+        int pre = __builtin_popcount(m[wi] & ((1u << (t & 31)) - 1u));
+        if (small) {
+            for (int w = 0; w < wi; ++w) pre += __builtin_popcount(m[w]);
+        } else {
+            pre += a.wordprefix[(size_t)ex * a.W + wi];
+        }
+        const int pos = offs[ex] + pre;
+        if (a.perm) a.perm[pos] = (int32_t)s;
+        if (a.inv) a.inv[s] = pos;
+        if (a.row_token) a.row_token[pos] = t;
+    } else if (s < S + a.shared_rows) {
+        const int t = (int)(s - S);
+        if (a.row_token) a.row_token[S + t] = t;
     }
 }
 
@@ -145,31 +183,39 @@ int launch_permute(const int32_t *idx, const uint32_t *mask, int64_t T, int64_t 
                    int shared_rows, int32_t *wordprefix, const PermuteOut &o, hipStream_t st)
 {
     const int W = mask_words_for(T);
-    ScanArgs a;
+    const bool small = W <= kSmallWords;
+    if (!small && W > 0) {
+        permute_count_kernel<<<dim3((unsigned)E), dim3(256), 0, st>>>(mask, W, wordprefix, o.counts);
+        XS_LAUNCH_CHECK();
+    }
+    ScatterArgs a;
+    a.idx = idx;
     a.mask = mask;
-    a.wordprefix = wordprefix;
+    a.wordprefix = small ? nullptr : wordprefix;
     a.counts = o.counts;
     a.offsets = o.offsets;
-    a.tile_off0 = o.n_tile_sizes > 0 ? o.tile_off[0] : nullptr;
-    a.tile_off1 = o.n_tile_sizes > 1 ? o.tile_off[1] : nullptr;
-    a.tile_off2 = o.n_tile_sizes > 2 ? o.tile_off[2] : nullptr;
-    a.bm0 = o.tile_bm[0];
-    a.bm1 = o.tile_bm[1];
-    a.bm2 = o.tile_bm[2];
+    a.tile_off = o.tile_off;
+    a.tab = reinterpret_cast<int4 *>(o.tab);
+    a.bm = o.tile_bm > 0 ? o.tile_bm : 1;
+    a.T = T;
+    a.k = (int)k;
     a.E = (int)E;
     a.W = W;
     a.shared_rows = shared_rows;
     a.offsets_ext = o.offsets_ext;
-    permute_scan_kernel<<<dim3(1), dim3(1024), 0, st>>>(a);
+    a.perm = o.perm;
+    a.inv = o.inv;
+    a.row_token = o.row_token;
+    const int64_t n = T * k + shared_rows;
+    const unsigned blocks = (unsigned)(n > 0 ? (n + 1023) / 1024 : 1);
+    permute_scatter_kernel<<<dim3(blocks), dim3(1024), 0, st>>>(a);
     XS_LAUNCH_CHECK();
-    int64_t n = T * k + shared_rows;
-    if (n > 0) {
-        permute_scatter_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(
-            idx, mask, wordprefix, o.offsets, T, (int)k, (int)E, W, shared_rows, o.perm, o.inv,
-            o.row_token);
-        XS_LAUNCH_CHECK();
-    }
     return XS_OK;
+}
+
+size_t tile_table_bytes(int64_t rows_routed, int64_t rows_shared, int64_t E, int bm)
+{
+    return (size_t)16 * (size_t)(rows_routed / bm + E + rows_shared / bm + 3);
 }
 
 }  // namespace xs
@@ -211,8 +257,6 @@ int xs_moe_permute(const int32_t *idx, int64_t T, int64_t E, int64_t k, int32_t 
     o.offsets = offsets;
     o.perm = perm;
     o.inv = inv;
-    o.row_token = nullptr;
-    o.n_tile_sizes = 0;
     return launch_permute(idx, mask, T, E, k, 0, wordprefix, o, st);
 }
 
