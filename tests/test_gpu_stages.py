@@ -78,9 +78,10 @@ def test_quant_weight_fp8_and_mxfp4_bitexact():
 
 
 def test_hw_fp8_pack_matches_software_rne():
-    """The GEMM epilogue packs with the hardware converter: pin it against the
-    software RNE encoder over every e4m3 code boundary (midpoints and
-    neighbours) in [-448, 448]."""
+    """The activation quantizer and the GEMM epilogue pack with the hardware
+    converter (after clamping to +-448): pin it against the software RNE
+    encoder of the oracle over every e4m3 code boundary (midpoints and
+    neighbours, subnormals included) in [-448, 448]."""
     import xs_moe_capi as X
     tab = oracle.e4m3_table()
     fin = np.unique(np.abs(tab[np.isfinite(tab)]))

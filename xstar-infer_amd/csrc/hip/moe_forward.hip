@@ -148,10 +148,9 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
 
     // 1. router: logits -> top-k + per-expert token masks
     if ((rc = prof_mark(0, st))) return rc;
-    rc = launch_mask_clear(mask, (int64_t)Wd * E, st);
-    if (rc) return rc;
     const int nsplit = router_logits_splits(T, H, p->router_exact, p->x_dtype);
-    rc = launch_router_logits(t->x, t->router_w, p->x_dtype, T, E, H, p->router_exact, logits, nsplit, st);
+    rc = launch_router_logits(t->x, t->router_w, p->x_dtype, T, E, H, p->router_exact, logits, nsplit, st, mask,
+                              (int64_t)Wd * E);
     if (rc) return rc;
     if ((rc = prof_mark(1, st))) return rc;
     rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,

@@ -21,6 +21,7 @@ struct GemmArgs {
     int K;                     // reduction length
     int N;                     // gate_up: I (output act columns); down: H
     int bm;                    // tile rows: 16, 32, 64 or 128
+    int stream_w;              // tiled kernels: non-temporal weight loads (large launches)
     uint8_t *Cq;               // gate_up: act rows [*, I] FP8
     void *Cs;                  // gate_up: f32 [*, I/128] or e8m0 [*, I/32]
     uint16_t *Cy;              // down: bf16 rows [*, ldc]

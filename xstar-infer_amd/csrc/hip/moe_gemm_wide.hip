@@ -70,6 +70,11 @@ __device__ __forceinline__ void dma16(const uint8_t *sbase, uint32_t voff, uint3
 {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
+// Non-temporal variant for weights read by a single tile (streamed once).
+__device__ __forceinline__ void dma16_nt(const uint8_t *sbase, uint32_t voff, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
 __device__ __forceinline__ void dma4(const uint8_t *sbase, uint32_t voff, uint32_t lds)
 {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
@@ -130,15 +135,23 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
     const bool sa_real = wave < C::NSA;
     const uint32_t oS = (uint32_t)token_of(sa_real ? 64 * wave + lane : 0) * (uint32_t)(KB * 4);
     const uint8_t *gS = reinterpret_cast<const uint8_t *>(a.As);
+    // an expert whose rows fit one tile reads its weights once: stream them
+    const bool stream_w = a.offsets[e + 1] - a.offsets[e] <= BM;
 
     auto issue = [&](int kb) {   // operands of step kb into ring stage kb % NST (past the end: reload)
         const int kk = kb < KB ? kb : KB - 1;
         const uint32_t st = ring_lds + (uint32_t)((kb % C::NST) * C::STAGE);
 #pragma unroll
         for (int u = 0; u < C::NA; ++u) dma16(a.A + (size_t)kk * 128, oA[u], st + 1024 * (wave + kNW * u));
+        if (stream_w) {
 #pragma unroll
-        for (int u = 0; u < C::NB; ++u)
-            dma16(Bexp + (size_t)kk * 128, oW[u], st + C::A_BYTES + 1024 * (wave + kNW * u));
+            for (int u = 0; u < C::NB; ++u)
+                dma16_nt(Bexp + (size_t)kk * 128, oW[u], st + C::A_BYTES + 1024 * (wave + kNW * u));
+        } else {
+#pragma unroll
+            for (int u = 0; u < C::NB; ++u)
+                dma16(Bexp + (size_t)kk * 128, oW[u], st + C::A_BYTES + 1024 * (wave + kNW * u));
+        }
         dma4(gS + (size_t)kk * 4, oS, sa_real ? st + C::A_BYTES + C::W_BYTES + 256 * wave : trash_lds);
     };
 

@@ -48,8 +48,10 @@ __device__ __forceinline__ void store8(float *p, const float *v)
 // Number of K slices the bf16 MFMA router uses for T tokens (1 = no split).
 int router_logits_splits(int64_t T, int64_t H, int exact, int dtype);
 // Writes nsplit partial logit slices [nsplit][T][E] (nsplit = 1: the logits).
+// mask_clear (optional): a [mask_words] bitmask zeroed by the same launch.
 int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
-                         int exact, float *logits, int nsplit, hipStream_t st);
+                         int exact, float *logits, int nsplit, hipStream_t st,
+                         uint32_t *mask_clear = nullptr, int64_t mask_words = 0);
 // Routes on the sum (in slice order) of nsplit partial logit slices; writes the
 // summed logits to logits_out when it is not NULL.
 int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,

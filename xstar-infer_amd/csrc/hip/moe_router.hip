@@ -15,6 +15,16 @@ namespace xs {
 // Upper bound on the K slices of the split-K router GEMM.
 static constexpr int kMaxSplits = 16;
 
+// Zero the per-expert token bitmask the route kernel ORs into (folded into the
+// router launch so the layer needs no separate fill).
+__device__ __forceinline__ void clear_mask(uint32_t *mask, int64_t words)
+{
+    if (!mask) return;
+    const int64_t nb = (int64_t)gridDim.x * gridDim.y * gridDim.z;
+    const int64_t b = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    for (int64_t i = b * blockDim.x + threadIdx.x; i < words; i += nb * blockDim.x) mask[i] = 0u;
+}
+
 // ------------------------------------------------------------ exact logits
 // 256 threads = 16 tokens x 16 experts; k-chunks of 64 staged in LDS; each
 // thread owns one (t, e) and accumulates sequentially in k with separately
@@ -23,9 +33,11 @@ template <typename T>
 __global__ __launch_bounds__(256) void router_logits_exact_kernel(const T *__restrict__ x,
                                                                   const T *__restrict__ wr,
                                                                   int Tn, int E, int H,
-                                                                  float *__restrict__ logits)
+                                                                  float *__restrict__ logits,
+                                                                  uint32_t *__restrict__ mask, int64_t mask_words)
 {
 #pragma clang fp contract(off)
+    clear_mask(mask, mask_words);
     __shared__ float xs_[16][65];
     __shared__ float ws_[16][65];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
@@ -60,8 +72,10 @@ template <int MT, int NT>
 __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t *__restrict__ x,
                                                                  const uint16_t *__restrict__ wr,
                                                                  int Tn, int E, int H, int klen,
-                                                                 float *__restrict__ part)
+                                                                 float *__restrict__ part,
+                                                                 uint32_t *__restrict__ mask, int64_t mask_words)
 {
+    clear_mask(mask, mask_words);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int wm = wave >> 1, wn = wave & 1;
@@ -284,34 +298,64 @@ int router_logits_splits(int64_t T, int64_t H, int exact, int dtype)
 }
 
 int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
-                         int exact, float *logits, int nsplit, hipStream_t st)
+                         int exact, float *logits, int nsplit, hipStream_t st, uint32_t *mask_clear,
+                         int64_t mask_words)
 {
     if (T == 0) return XS_OK;
     if (exact || dtype == XS_F32) {
         dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16)), block(256);
         if (dtype == XS_F32)
             router_logits_exact_kernel<float><<<grid, block, 0, st>>>((const float *)x, (const float *)wr,
-                                                                      (int)T, (int)E, (int)H, logits);
+                                                                      (int)T, (int)E, (int)H, logits,
+                                                                      mask_clear, mask_words);
         else
             router_logits_exact_kernel<uint16_t><<<grid, block, 0, st>>>(
-                (const uint16_t *)x, (const uint16_t *)wr, (int)T, (int)E, (int)H, logits);
+                (const uint16_t *)x, (const uint16_t *)wr, (int)T, (int)E, (int)H, logits, mask_clear, mask_words);
     } else if (T > 256) {
         // prefill: 64 tokens x 128 experts per block, K split nsplit ways
         dim3 grid((unsigned)((E + 127) / 128), (unsigned)((T + 63) / 64), (unsigned)nsplit), block(256);
         router_logits_mfma_kernel<2, 4><<<grid, block, 0, st>>>((const uint16_t *)x, (const uint16_t *)wr,
-                                                                (int)T, (int)E, (int)H, (int)(H / nsplit), logits);
+                                                                (int)T, (int)E, (int)H, (int)(H / nsplit), logits,
+                                                                mask_clear, mask_words);
     } else {
         // decode: 32 tokens x 64 experts per block, K split nsplit ways
         dim3 grid((unsigned)((E + 63) / 64), (unsigned)((T + 31) / 32), (unsigned)nsplit), block(256);
         router_logits_mfma_kernel<1, 2><<<grid, block, 0, st>>>((const uint16_t *)x, (const uint16_t *)wr,
-                                                                (int)T, (int)E, (int)H, (int)(H / nsplit), logits);
+                                                                (int)T, (int)E, (int)H, (int)(H / nsplit), logits,
+                                                                mask_clear, mask_words);
     }
     XS_LAUNCH_CHECK();
     return XS_OK;
 }
 
 // ---------------------------------------------------- activation quantizers
-// FP8 1x128: each thread owns 8 consecutive columns, 16 lanes share a group.
+// FP8 1x128 of one 8-column chunk c8 of a row: the 16 lanes of an aligned
+// 16-lane group hold the 16 chunks of one 128-column group.
+template <typename T>
+__device__ __forceinline__ void quant_chunk_fp8(const T *__restrict__ xr, int cols, int c8,
+                                                uint8_t *__restrict__ qr, float *__restrict__ sr)
+{
+    float v[8];
+    load8(xr + c8 * 8, v);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, WAVE));
+    float inv = amax == 0.0f ? 0.0f : __fdiv_rn(448.0f, amax);
+    // |v * inv| <= 448 (1 + 2^-22): clamped to the e4m3 range, the hardware
+    // RNE converter gives the software encoder's codes (pinned by the GPU tests)
+    float q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = fminf(fmaxf(__fmul_rn(v[i], inv), -448.0f), 448.0f);
+    const uint32_t lo = e4m3_pack2_hw(q[0], q[1]) | (e4m3_pack2_hw(q[2], q[3]) << 16);
+    const uint32_t hi = e4m3_pack2_hw(q[4], q[5]) | (e4m3_pack2_hw(q[6], q[7]) << 16);
+    *reinterpret_cast<v2i *>(qr + c8 * 8) = v2i{(int)lo, (int)hi};
+    if ((c8 & 15) == 0) sr[c8 / 16] = amax == 0.0f ? 1.0f : __fdiv_rn(amax, 448.0f);
+}
+
+// Each thread owns 8 consecutive columns (rows are whole multiples of 16
+// threads, so the 16-lane groups stay aligned).
 template <typename T>
 __global__ __launch_bounds__(256) void quant_act_fp8_kernel(const T *__restrict__ x, int64_t rows,
                                                             int cols, uint8_t *__restrict__ q,
@@ -320,23 +364,8 @@ __global__ __launch_bounds__(256) void quant_act_fp8_kernel(const T *__restrict_
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int per_row = cols / 8;
     const int64_t row = gid / per_row;
-    if (row >= rows) return;   // rows are whole multiples of 16 threads: groups stay aligned
-    const int c8 = (int)(gid - row * per_row);
-    float v[8];
-    load8(x + row * cols + c8 * 8, v);
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, WAVE));
-    float inv = amax == 0.0f ? 0.0f : __fdiv_rn(448.0f, amax);
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lo |= e4m3_encode_sw(__fmul_rn(v[i], inv)) << (8 * i);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hi |= e4m3_encode_sw(__fmul_rn(v[4 + i], inv)) << (8 * i);
-    *reinterpret_cast<v2i *>(q + row * cols + c8 * 8) = v2i{(int)lo, (int)hi};
-    if ((c8 & 15) == 0) s[row * (cols / 128) + c8 / 16] = amax == 0.0f ? 1.0f : __fdiv_rn(amax, 448.0f);
+    if (row >= rows) return;
+    quant_chunk_fp8(x + row * cols, cols, (int)(gid - row * per_row), q + row * cols, s + row * (cols / 128));
 }
 
 // MXFP8 1x32: 4 lanes per block of 32.
