@@ -202,7 +202,7 @@ def prefill(a, X, torch):
         "layer_frac_fp8_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
         "layer_hbm_gbs": (wbytes + act_bytes) / (ms * 1e-3) / 1e9,
         "stage_ms": stages,
-        "roofline": {"kernel": "moe_gemm_kernel<gate_up> (grouped FP8 gate_up GEMM + SwiGLU)",
+        "roofline": {"kernel": "moe_gemm_wide_kernel<192, gate_up> (grouped FP8 gate_up GEMM + SwiGLU + requant)",
                      "bound": "mfma", "achieved": achieved, "peak": PEAK_FP8_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_FP8_TFLOPS, "traffic": measured_traffic(),
                      "algorithmic_flop": gu_flops, "launch_ms": gu_ms},
