@@ -14,8 +14,9 @@
 //     slab (gate_up: 128 gate + the matching 128 up rows; down: 256 rows of W2);
 //   * both operand tiles move global -> LDS by DMA (global_load_lds_dwordx4,
 //     8 lanes per 128-byte row, so every load instruction is fully coalesced)
-//     into a ring of NST stages; 16-byte chunks are XOR-swizzled per row so the
-//     MFMA fragment reads are bank-conflict free;
+//     into two rings (activations 2 deep, weights 3 deep: first-touch weight
+//     reads from HBM have the longer latency); 16-byte chunks are
+//     XOR-swizzled per row so the MFMA fragment reads are bank-conflict free;
 //   * 8 waves as 2 (tokens) x 4 (weight columns): a wave owns 64 weight rows
 //     (gate_up: 32 gate + the matching 32 up) and the 16-token subtiles of its
 //     parity, so a partially filled tile still splits evenly over both halves;
@@ -45,13 +46,26 @@ struct WCfg {
     static constexpr int A_BYTES = BM * 128;               // activation rows of one K step
     static constexpr int W_BYTES = 256 * 128;              // weight rows of one K step
     static constexpr int S_BYTES = BM * 4;                 // activation row scales
-    static constexpr int STAGE = A_BYTES + W_BYTES + S_BYTES;
-    static constexpr int NST = kRing / STAGE;              // ring stages
+    static constexpr int AS_BYTES = A_BYTES + S_BYTES;     // activation ring stage
+    // Two rings: activations (+ row scales) NAR deep, weights NWR deep, so the
+    // LDS left over by whole stages buys one more step of prefetch for one
+    // operand (prefetch distances NAR-1 and NWR-1 steps).
+    static constexpr int NAR = 2;
+    static constexpr int NWR = 3;
+    static constexpr int DA = NAR - 1, DW = NWR - 1;
     static constexpr int NA = BM / 8 / kNW;                // 1 KB activation DMAs per wave and step
     static constexpr int NB = 256 / 8 / kNW;               // 1 KB weight DMAs per wave and step
     static constexpr int NSA = S_BYTES / 256;              // scale DMAs (waves 0 .. NSA-1)
     static constexpr int PER_STEP = NA + NB + 1;           // loads per wave per step
-    static_assert(BM % 64 == 0 && NST >= 2, "tile");
+    // Each iteration issues the operand with the shorter prefetch distance first.
+    // Loads retire in order: at the top of step kb at most X may be outstanding
+    // for both W(kb) and A(kb) to have landed.
+    static constexpr bool W_FIRST = DA >= DW;
+    static constexpr int XW = W_FIRST ? (NA + 1) + (DW - 1) * PER_STEP : (DW - 1) * PER_STEP;
+    static constexpr int XA = W_FIRST ? (DA - 1) * PER_STEP : NB + (DA - 1) * PER_STEP;
+    static constexpr int X = XW < XA ? XW : XA;
+    static constexpr int PRO = DA > DW ? DA : DW;          // prologue iterations
+    static_assert(BM % 64 == 0 && DA >= 1 && DW >= 1 && NAR * AS_BYTES + NWR * W_BYTES <= kRing, "tile");
 };
 
 __device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }
@@ -138,21 +152,39 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
     // an expert whose rows fit one tile reads its weights once: stream them
     const bool stream_w = a.offsets[e + 1] - a.offsets[e] <= BM;
 
-    auto issue = [&](int kb) {   // operands of step kb into ring stage kb % NST (past the end: reload)
-        const int kk = kb < KB ? kb : KB - 1;
-        const uint32_t st = ring_lds + (uint32_t)((kb % C::NST) * C::STAGE);
+    const uint32_t wring_lds = ring_lds + (uint32_t)(C::NAR * C::AS_BYTES);
+    // operands of step kb into ring slot kb % depth; kb < 0 (prologue padding)
+    // goes to the trash line, kb >= KB reloads the last step into a slot that is
+    // not read again: every iteration issues the same number of loads
+    auto issue_a = [&](int kb) {
+        const int kk = kb < 0 ? 0 : (kb < KB ? kb : KB - 1);
+        const uint32_t st = ring_lds + (uint32_t)(((kb < 0 ? 0 : kb) % C::NAR) * C::AS_BYTES);
 #pragma unroll
-        for (int u = 0; u < C::NA; ++u) dma16(a.A + (size_t)kk * 128, oA[u], st + 1024 * (wave + kNW * u));
+        for (int u = 0; u < C::NA; ++u)
+            dma16(a.A + (size_t)kk * 128, oA[u], kb < 0 ? trash_lds : st + 1024 * (wave + kNW * u));
+        dma4(gS + (size_t)kk * 4, oS, (kb >= 0 && sa_real) ? st + C::A_BYTES + 256 * wave : trash_lds);
+    };
+    auto issue_w = [&](int kb) {
+        const int kk = kb < 0 ? 0 : (kb < KB ? kb : KB - 1);
+        const uint32_t st = wring_lds + (uint32_t)(((kb < 0 ? 0 : kb) % C::NWR) * C::W_BYTES);
         if (stream_w) {
 #pragma unroll
             for (int u = 0; u < C::NB; ++u)
-                dma16_nt(Bexp + (size_t)kk * 128, oW[u], st + C::A_BYTES + 1024 * (wave + kNW * u));
+                dma16_nt(Bexp + (size_t)kk * 128, oW[u], kb < 0 ? trash_lds : st + 1024 * (wave + kNW * u));
         } else {
 #pragma unroll
             for (int u = 0; u < C::NB; ++u)
-                dma16(Bexp + (size_t)kk * 128, oW[u], st + C::A_BYTES + 1024 * (wave + kNW * u));
+                dma16(Bexp + (size_t)kk * 128, oW[u], kb < 0 ? trash_lds : st + 1024 * (wave + kNW * u));
         }
-        dma4(gS + (size_t)kk * 4, oS, sa_real ? st + C::A_BYTES + C::W_BYTES + 256 * wave : trash_lds);
+    };
+    auto issue = [&](int kb) {   // the loads of iteration kb: A(kb + DA), W(kb + DW)
+        if (C::W_FIRST) {
+            issue_w(kb + C::DW);
+            issue_a(kb + C::DA);
+        } else {
+            issue_a(kb + C::DA);
+            issue_w(kb + C::DW);
+        }
     };
 
     // the wave's four 16-row A tiles (rows of the LDS weight tile)
@@ -173,16 +205,16 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
 
     __syncthreads();   // sB visible
 #pragma unroll
-    for (int s = 0; s < C::NST - 1; ++s) issue(s);
+    for (int j = -C::PRO; j < 0; ++j) issue(j);
 
     const int sbi = GATEUP ? 0 : (wn >> 1);   // down: the wave's 128-row scale block
     for (int kb = 0; kb < KB; ++kb) {
-        wait_vm<(C::NST - 2) * C::PER_STEP>();   // this wave's DMAs of step kb landed
-        __syncthreads();                          // ... and every wave's; stage kb-1 is free
-        issue(kb + C::NST - 1);
-        const uint8_t *sA = smem + (kb % C::NST) * C::STAGE;
-        const uint8_t *sW = sA + C::A_BYTES;
-        const float *sS = reinterpret_cast<const float *>(sW + C::W_BYTES);
+        wait_vm<C::X>();          // this wave's loads of step kb landed
+        __syncthreads();          // ... and every wave's; the slots of step kb-1 are free
+        issue(kb);
+        const uint8_t *sA = smem + (kb % C::NAR) * C::AS_BYTES;
+        const float *sS = reinterpret_cast<const float *>(sA + C::A_BYTES);
+        const uint8_t *sW = smem + C::NAR * C::AS_BYTES + (kb % C::NWR) * C::W_BYTES;
         const float sb0 = sB[sbi * KB + kb];
         const float sb1 = GATEUP ? sB[KB + kb] : sb0;
 
