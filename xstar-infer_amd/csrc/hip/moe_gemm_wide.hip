@@ -99,7 +99,7 @@ __device__ __forceinline__ void wait_vm()
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int BM, bool GATEUP>
+template <int BM, bool GATEUP, bool FULL>
 __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int rows, int slab, uint8_t *smem)
 {
     using C = WCfg<BM>;
@@ -218,6 +218,12 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
         const float sb0 = sB[sbi * KB + kb];
         const float sb1 = GATEUP ? sB[KB + kb] : sb0;
 
+        // The step's activation scales first: LDS reads retire in order, so a
+        // scale read queued behind the fragment prefetch would make every fold
+        // wait for that prefetch.
+        float sav[C::MI];
+#pragma unroll
+        for (int i = 0; i < C::MI; ++i) sav[i] = (FULL || i < nlive) ? sS[16 * (wm + 2 * i) + r16] : 0.f;
         // Operand layout of v_mfma_f32_16x16x128_f8f6f4: lane 16g + r holds row r
         // with K bytes [16g, 16g+16) and [64+16g, 64+16g+16): LDS chunks g, g+4.
         v8i wf[4];
@@ -233,28 +239,29 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
             return cat(*reinterpret_cast<const v4i *>(rp + swz8(row, g) * 16),
                        *reinterpret_cast<const v4i *>(rp + swz8(row, g + 4) * 16));
         };
-        // Subtile i: read B(i+1), 4 MFMAs on B(i), fold the products of i-1.
-        v8i bx = read_b(0);
+        // Subtile i: read B(i+2), 4 MFMAs on B(i), fold the products of i-1.
+        // Full tiles run branch free; partial ones skip the subtiles past rows.
+        constexpr int PB = 2;                       // fragment prefetch distance (subtiles)
+        v8i bx[PB + 1];
+#pragma unroll
+        for (int i = 0; i < PB; ++i)
+            if (i < C::MI && (FULL || i < nlive)) bx[i] = read_b(i);
         v4f q[2][4];
-        float cq0[2], cq1[2];
 #pragma unroll
         for (int i = 0; i <= C::MI; ++i) {
-            if (i < C::MI && i < nlive) {
-                const v8i bc = bx;
-                if (i + 1 < C::MI && i + 1 < nlive) bx = read_b(i + 1);
-                const float sa = sS[16 * (wm + 2 * i) + r16];
+            if (i < C::MI && (FULL || i < nlive)) {
+                if (i + PB < C::MI && (FULL || i + PB < nlive)) bx[(i + PB) % (PB + 1)] = read_b(i + PB);
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    q[i & 1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[j], bc, v4f{0.f, 0.f, 0.f, 0.f},
-                                                                                  0, 0, 0, 0, 0, 0);
-                cq0[i & 1] = sa * sb0;
-                cq1[i & 1] = sa * sb1;
+                    q[i & 1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        wf[j], bx[i % (PB + 1)], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
             }
-            if (i >= 1 && i - 1 < nlive) {
+            if (i >= 1 && (FULL || i - 1 < nlive)) {
                 const int m = i - 1;
+                const float c0 = sav[m] * sb0, c1 = sav[m] * sb1;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float c = (GATEUP && j >= 2) ? cq1[m & 1] : cq0[m & 1];
+                    const float c = (GATEUP && j >= 2) ? c1 : c0;
 #pragma unroll
                     for (int v = 0; v < 4; ++v) acc[m][j][v] = __builtin_fmaf(q[m & 1][j][v], c, acc[m][j][v]);
                 }
@@ -334,7 +341,8 @@ __global__ __launch_bounds__(kNT) void moe_gemm_wide_kernel(GemmArgs a)
     if ((int)blockIdx.y >= tab[0].x) return;
     const int4 d = tab[1 + blockIdx.y];   // {expert, first position, rows}
     const int slab = (int)blockIdx.x;
-    run_tile<BM, GATEUP>(a, d.x, d.y, d.z, slab, smem);
+    if (d.z >= BM) run_tile<BM, GATEUP, true>(a, d.x, d.y, BM, slab, smem);
+    else run_tile<BM, GATEUP, false>(a, d.x, d.y, d.z, slab, smem);
 }
 
 template <int BM, bool GATEUP>
