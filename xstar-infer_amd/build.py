@@ -26,6 +26,10 @@ HIP_FLAGS = [
     "-Wno-unused-result",
     # MFMA results in VGPRs: the FP8 kernels fold every partial product with VALU FMAs
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # atomics stay as written: the wave-aggregating rewrite reads an atomic's
+    # result right after issuing it, which would stall the persistent GEMMs'
+    # scheduler wave (it reads a claim several steps later)
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 ]
 
 

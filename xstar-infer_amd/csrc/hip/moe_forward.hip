@@ -38,7 +38,7 @@ static int prof_mark(int stage, hipStream_t st)
 }
 
 struct WsLayout {
-    size_t logits, idx, w, mask, wordprefix, counts, offsets, perm, inv, row_token, tiles, tiletab;
+    size_t logits, idx, w, mask, wordprefix, counts, offsets, perm, inv, row_token, tiles, tiletab, part, cnt1, cnt2;
     size_t xq, xs, xmq, xms, actq, acts, actms, y;
     size_t total;
 };
@@ -62,6 +62,24 @@ static bool use_wide(const xs_moe_params *p)
     return p->T * p->top_k >= 32 * p->E;
 }
 
+// Decode-sized FP8 layers may run the persistent GEMMs (moe_gemm_stream.hip):
+// 0 never, 1 by size, 2 always.  XS_MOE_STREAM=0|1 forces (benchmarks, tests).
+static int use_stream(const xs_moe_params *p)
+{
+    if (p->routed_format != XS_FP8_E4M3 || use_wide(p)) return 0;
+    const char *force = getenv("XS_MOE_STREAM");   // read per call: tests switch it
+    if (force && !strcmp(force, "0")) return 0;
+    if (force && !strcmp(force, "1")) return 2;
+    return 1;
+}
+
+// Upper bound of the tile count at 16-row tiles (the smallest height).
+static int64_t tiles16_max(const xs_moe_params *p)
+{
+    const int64_t S = p->T * p->top_k;
+    return S / 16 + (p->E < S ? p->E : S) + (p->has_shared ? (p->T + 15) / 16 : 0);
+}
+
 static WsLayout layout(const xs_moe_params *p)
 {
     const size_t T = (size_t)p->T, H = (size_t)p->H, I = (size_t)p->I, E = (size_t)p->E, k = (size_t)p->top_k;
@@ -83,6 +101,15 @@ static WsLayout layout(const xs_moe_params *p)
     take(L.row_token, 4 * R);
     take(L.tiles, 4 * (E + 2));
     take(L.tiletab, tile_table_bytes((int64_t)S, p->has_shared ? (int64_t)T : 0, (int64_t)E, 16));
+    {
+        const bool st = use_stream(p);
+        const int64_t n1 = st ? stream_items(true, (int)I, tiles16_max(p)) : 0;
+        const int64_t n2 = st ? stream_items(false, (int)H, tiles16_max(p)) : 0;
+        const size_t p1 = st ? stream_part_bytes(n1, (int)H, 32) : 0, p2 = st ? stream_part_bytes(n2, (int)I, 32) : 0;
+        take(L.part, p1 > p2 ? p1 : p2);
+        take(L.cnt1, st ? 4 * (size_t)(n1 + 1) : 0);
+        take(L.cnt2, st ? 4 * (size_t)(n2 + 1) : 0);
+    }
     take(L.xq, T * H);
     take(L.xs, 4 * T * (H / 128));
     take(L.xmq, fp4 ? T * H : 0);
@@ -180,11 +207,23 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     po.tab = WS(int32_t, tiletab);
     po.tile_bm = bm;
     po.offsets_ext = 1;
-    rc = launch_permute(idx, mask, T, E, k, shared_rows, WS(int32_t, wordprefix), po, st);
-    if (rc) return rc;
 
     const int routed_tiles = (int)(S / bm + (E < S ? E : S));
     const int shared_tiles = (int)((shared_rows + bm - 1) / bm);
+    // Persistent GEMMs once the gate_up work (items of one tile x one 256-row
+    // slab) fills every CU twice; below that, whole items per block split
+    // less and the one-block-per-tile kernels are faster.
+    const int sm = use_stream(p);
+    const int64_t rows_all = S + shared_rows;
+    const bool stream = stream_fits(bm, routed_tiles + shared_tiles, rows_all) &&
+                        (sm == 2 || (sm == 1 && stream_items(true, (int)I, routed_tiles + shared_tiles) >=
+                                                    2 * (int64_t)stream_blocks()));
+    if (stream) {
+        po.zero = WS(int32_t, cnt1);
+        po.zero_n = stream_items(true, (int)I, tiles16_max(p)) + 1;
+    }
+    rc = launch_permute(idx, mask, T, E, k, shared_rows, WS(int32_t, wordprefix), po, st);
+    if (rc) return rc;
 
     // 4. gate_up GEMM + SwiGLU + activation re-quant
     GemmArgs g1 = {};
@@ -225,15 +264,23 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g1.Cs = WS(float, acts);
         g1.e_lo = 0;
         g1.e_hi = (int)E + (shared_rows ? 1 : 0);
-        rc = wide ? launch_gemm_wide(g1, true, routed_tiles + shared_tiles, st)
-                  : launch_gemm(g1, true, false, routed_tiles + shared_tiles, st);
+        if (stream) {
+            g1.part = g2.part = WS(float, part);
+            g1.cnt = WS(int32_t, cnt1);
+            g2.cnt = g1.zero_cnt = WS(int32_t, cnt2);
+            g1.zero_n = (int)stream_items(false, (int)H, tiles16_max(p)) + 1;
+        }
+        rc = stream ? launch_gemm_stream(g1, true, routed_tiles + shared_tiles, rows_all, st)
+             : wide ? launch_gemm_wide(g1, true, routed_tiles + shared_tiles, st)
+                    : launch_gemm(g1, true, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
         if ((rc = prof_mark(5, st))) return rc;
         g2.As = WS(float, acts);
         g2.e_lo = 0;
         g2.e_hi = g1.e_hi;
-        rc = wide ? launch_gemm_wide(g2, false, routed_tiles + shared_tiles, st)
-                  : launch_gemm(g2, false, false, routed_tiles + shared_tiles, st);
+        rc = stream ? launch_gemm_stream(g2, false, routed_tiles + shared_tiles, rows_all, st)
+             : wide ? launch_gemm_wide(g2, false, routed_tiles + shared_tiles, st)
+                    : launch_gemm(g2, false, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
     } else {
         GemmArgs r1 = g1;
@@ -303,7 +350,7 @@ __global__ void single_segment_kernel(int32_t *offsets, int4 *tab, int M, int bm
         offsets[2] = M;
         tab[0] = int4{nt, 0, 0, 0};
     }
-    if (i < nt) tab[1 + i] = int4{0, i * bm, min(bm, M - i * bm), 0};
+    if (i < nt) tab[1 + i] = int4{0, i * bm, min(bm, M - i * bm), (i & 0xffff) | (min(nt, 0x7fff) << 16)};
 }
 
 static size_t gemm_ws(int64_t M, int64_t K, size_t *o_s, size_t *o_meta)

@@ -73,9 +73,13 @@ struct PermuteOut {
     int32_t *row_token;   // position -> token, routed then shared rows (or NULL)
     int32_t *tile_off;    // [E+2] exclusive scan of ceil(count / tile_bm), shared tiles last (or NULL)
     int32_t *tab;         // tile table (or NULL): entry 0 {tiles, shared tiles}, then
-                          // {expert, first position, rows}, the shared segment's tiles first
+                          // {expert, first position, rows, t | nt << 16} (t: tile index within
+                          // the expert, nt: the expert's tiles, both below 2^15 where used),
+                          // the shared segment's tiles first
     int tile_bm;
     int offsets_ext;
+    int32_t *zero;        // int32 words cleared by the scatter (or NULL): GEMM counters
+    int64_t zero_n;
 };
 int mask_words_for(int64_t T);
 int launch_mask_clear(uint32_t *mask, int64_t words, hipStream_t st);

@@ -99,6 +99,8 @@ struct ScatterArgs {
     int64_t T;
     int k, E, W, shared_rows, offsets_ext;
     int32_t *perm, *inv, *row_token;
+    int32_t *zero;
+    int64_t zero_n;
 };
 constexpr int kSmallWords = 8;
 
@@ -148,12 +150,15 @@ __global__ __launch_bounds__(1024) void permute_scatter_kernel(ScatterArgs a)
                 if (e == 0) a.tab[0] = int4{tt + nsh, nsh, 0, 0};
                 if (e < a.E)
                     for (int t = 0; t < nt; ++t)
-                        a.tab[1 + nsh + toff + t] = int4{e, off + t * a.bm, min(a.bm, cnt - t * a.bm), 0};
+                        a.tab[1 + nsh + toff + t] = int4{e, off + t * a.bm, min(a.bm, cnt - t * a.bm), t | (min(nt, 0x7fff) << 16)};
                 for (int t = e; t < nsh; t += blockDim.x)
-                    a.tab[1 + t] = int4{a.E, total + t * a.bm, min(a.bm, a.shared_rows - t * a.bm), 0};
+                    a.tab[1 + t] = int4{a.E, total + t * a.bm, min(a.bm, a.shared_rows - t * a.bm), t | (min(nsh, 0x7fff) << 16)};
             }
         }
     }
+    if (a.zero)
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.zero_n; i += (int64_t)gridDim.x * blockDim.x)
+            a.zero[i] = 0;
     __syncthreads();
     const int64_t S = a.T * a.k;
     const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -206,6 +211,8 @@ int launch_permute(const int32_t *idx, const uint32_t *mask, int64_t T, int64_t 
     a.perm = o.perm;
     a.inv = o.inv;
     a.row_token = o.row_token;
+    a.zero = o.zero;
+    a.zero_n = o.zero ? o.zero_n : 0;
     const int64_t n = T * k + shared_rows;
     const unsigned blocks = (unsigned)(n > 0 ? (n + 1023) / 1024 : 1);
     permute_scatter_kernel<<<dim3(blocks), dim3(1024), 0, st>>>(a);
