@@ -120,10 +120,12 @@ def test_router_logits_exact_bitexact(bf16):
     assert np.array_equal(got, ref)
 
 
-def test_router_logits_mfma_tolerance():
+@pytest.mark.parametrize("T,E,H", [(130, 256, 4096), (1000, 256, 4096), (2048, 198, 1024), (300, 130, 512)])
+def test_router_logits_mfma_tolerance(T, E, H):
+    """Decode (T <= 256: fragments from global memory) and prefill (LDS-tiled
+    kernel, ragged token and expert tiles) bf16 MFMA router logits."""
     import xs_moe_capi as X
-    rng = np.random.default_rng(5)
-    T, E, H = 130, 256, 4096
+    rng = np.random.default_rng(5 + T)
     xb = oracle.bf16_from_f32(rng.standard_normal((T, H)).astype(np.float32))
     wb = oracle.bf16_from_f32((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
     got = X.router_logits(_bf16_dev(xb), _bf16_dev(wb), exact=False).cpu().numpy()

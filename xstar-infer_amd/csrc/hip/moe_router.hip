@@ -123,6 +123,123 @@ __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t 
         }
 }
 
+// ------------------------------------------------------- tiled MFMA logits
+// Prefill (many tokens): 128 tokens x 128 experts per block over one K slice.
+// Both operand tiles move global -> LDS by wave-wide DMA (global_load_lds,
+// 8 lanes per 128-byte row, so each load instruction is fully coalesced) into a
+// 3-stage ring of 64-wide K steps; 16-byte chunks are XOR-swizzled per row so
+// the fragment reads are bank-conflict free.  (Loading MFMA fragments straight
+// from global memory touches 16 rows per instruction, which the vector memory
+// path serves ~4x slower than coalesced rows.)  4 waves as 2 x 2, each 64 x 64;
+// v_mfma_f32_16x16x32_bf16 with the router weight as operand A, so a lane's 4
+// results are 4 consecutive experts of one token (one 16-byte store).
+namespace {
+constexpr int kRtBT = 128, kRtBE = 128, kRtNST = 3;
+constexpr int kRtStage = (kRtBT + kRtBE) * 128;       // bytes per K step of 64
+
+__device__ __forceinline__ int rt_swz(int r, int c) { return c ^ ((r >> 1) & 7); }
+__device__ __forceinline__ uint32_t rt_lds(const void *p)
+{
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+// Wave-wide DMA global -> LDS: lane i's 16 bytes land at lds + 16 i.  M0 carries
+// the wave-uniform LDS base; it is written only here.
+__device__ __forceinline__ void rt_dma16(const void *g, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+template <int N>
+__device__ __forceinline__ void rt_wait_vm()
+{
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+}  // namespace
+
+__global__ __launch_bounds__(256) void router_logits_tile_kernel(const uint16_t *__restrict__ x,
+                                                                 const uint16_t *__restrict__ wr,
+                                                                 int Tn, int E, int H, int klen,
+                                                                 float *__restrict__ part,
+                                                                 uint32_t *__restrict__ mask, int64_t mask_words)
+{
+    clear_mask(mask, mask_words);
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int t0 = blockIdx.y * kRtBT, e0 = blockIdx.x * kRtBE;
+    const int kbeg = blockIdx.z * klen, KS = klen / 64;
+
+    // DMA sources: instruction q = wave + 4 u covers LDS rows 8q .. 8q+7 (rows
+    // 0..127 tokens, 128..255 experts), lane -> (row, swizzled 16-byte chunk).
+    const uint16_t *src[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int p = 64 * (wave + 4 * u) + lane, row = p >> 3, c = rt_swz(row, p & 7);
+        const uint16_t *base = row < kRtBT ? x + (size_t)min(t0 + row, Tn - 1) * H
+                                           : wr + (size_t)min(e0 + row - kRtBT, E - 1) * H;
+        src[u] = base + kbeg + c * 8;
+    }
+    const uint32_t ring = __builtin_amdgcn_readfirstlane(rt_lds(smem));
+    auto issue = [&](int ks) {
+        const int kk = ks < KS ? ks : KS - 1;      // past the end: reload the last step (never read)
+        const uint32_t st = ring + (uint32_t)((ks % kRtNST) * kRtStage);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) rt_dma16(src[u] + (size_t)kk * 64, st + (uint32_t)((wave + 4 * u) * 1024));
+    };
+
+    v4f acc[4][4] = {};        // [expert subtile j][token subtile i]
+#pragma unroll
+    for (int s = 0; s < kRtNST - 1; ++s) issue(s);
+    for (int ks = 0; ks < KS; ++ks) {
+        rt_wait_vm<(kRtNST - 2) * 8>();     // this wave's loads of step ks landed
+        __syncthreads();                    // ... and every wave's; stage (ks-1) % NST is free
+        issue(ks + kRtNST - 1);
+        const uint8_t *st = smem + (ks % kRtNST) * kRtStage;
+        // bf16 16x16x32 operands: lane 16g + r holds row r, K elements [8g, 8g+8)
+        // of the 32-wide slice: 16-byte chunk 4u + g of the 128-byte row for
+        // slice u of this 64-wide step.
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            v8bf xf[4], wf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = wm * 64 + 16 * i + l16;
+                xf[i] = *reinterpret_cast<const v8bf *>(st + row * 128 + rt_swz(row, 4 * u + g) * 16);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = kRtBT + wn * 64 + 16 * j + l16;
+                wf[j] = *reinterpret_cast<const v8bf *>(st + row * 128 + rt_swz(row, 4 * u + g) * 16);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+        }
+    }
+    rt_wait_vm<0>();
+    // result layout: lane 16g + r holds token r and experts 4g..4g+3 of the subtile
+    float *out = part + (size_t)blockIdx.z * Tn * E;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = t0 + wm * 64 + 16 * i + l16;
+        if (t >= Tn) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = e0 + wn * 64 + 16 * j + 4 * g;
+            if (e + 3 < E && (E & 3) == 0) {
+                *reinterpret_cast<v4f *>(out + (size_t)t * E + e) = acc[j][i];
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (e + v < E) out[(size_t)t * E + e + v] = acc[j][i][v];
+            }
+        }
+    }
+}
+
 // ----------------------------------------------------------------- routing
 struct Cand {
     float key;
@@ -292,7 +409,9 @@ int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, i
 int router_logits_splits(int64_t T, int64_t H, int exact, int dtype)
 {
     if (exact || dtype == XS_F32) return 1;
-    int ns = T <= 64 ? 16 : (T <= 256 ? 8 : 4);
+    // decode: enough K slices to fill the GPU; prefill (tiled kernel, 64-wide
+    // K steps): 2 slices from 2048 tokens, 4 below
+    int ns = T <= 64 ? 16 : (T <= 256 ? 8 : (T < 2048 ? 4 : 2));
     while (ns > 1 && (H % (128 * ns)) != 0) ns >>= 1;
     return ns;
 }
@@ -312,11 +431,17 @@ int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, in
             router_logits_exact_kernel<uint16_t><<<grid, block, 0, st>>>(
                 (const uint16_t *)x, (const uint16_t *)wr, (int)T, (int)E, (int)H, logits, mask_clear, mask_words);
     } else if (T > 256) {
-        // prefill: 64 tokens x 128 experts per block, K split nsplit ways
-        dim3 grid((unsigned)((E + 127) / 128), (unsigned)((T + 63) / 64), (unsigned)nsplit), block(256);
-        router_logits_mfma_kernel<2, 4><<<grid, block, 0, st>>>((const uint16_t *)x, (const uint16_t *)wr,
-                                                                (int)T, (int)E, (int)H, (int)(H / nsplit), logits,
-                                                                mask_clear, mask_words);
+        // prefill: 128 tokens x 128 experts per block through an LDS ring, K split nsplit ways
+        static bool attr_set = false;
+        if (!attr_set) {
+            XS_HIP(hipFuncSetAttribute((const void *)router_logits_tile_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kRtNST * kRtStage));
+            attr_set = true;
+        }
+        dim3 grid((unsigned)((E + kRtBE - 1) / kRtBE), (unsigned)((T + kRtBT - 1) / kRtBT), (unsigned)nsplit), block(256);
+        router_logits_tile_kernel<<<grid, block, kRtNST * kRtStage, st>>>((const uint16_t *)x, (const uint16_t *)wr,
+                                                                          (int)T, (int)E, (int)H, (int)(H / nsplit),
+                                                                          logits, mask_clear, mask_words);
     } else {
         // decode: 32 tokens x 64 experts per block, K split nsplit ways
         dim3 grid((unsigned)((E + 63) / 64), (unsigned)((T + 31) / 32), (unsigned)nsplit), block(256);
