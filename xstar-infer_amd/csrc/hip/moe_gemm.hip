@@ -501,8 +501,11 @@ int launch_gemm(const GemmArgs &a, bool gateup, bool fp4, int grid_y, hipStream_
 
 // --------------------------------------------------------------- combine
 // out[t] = y_shared[t] + sum_j w[t,j] * y[inv[t*k+j]]  (f32, slot order, one cast)
+// One block per token, one pass over the row when H <= 8 * blockDim (the
+// launch picks blockDim = H / 8 up to 512), so all k + 1 row loads of a thread
+// are in flight together.
 template <typename OutT>
-__global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict__ y,
+__global__ __launch_bounds__(512) void combine_kernel(const uint16_t *__restrict__ y,
                                                       const int32_t *__restrict__ inv,
                                                       const float *__restrict__ w, int k, int H,
                                                       int64_t shared_base, int has_shared,
@@ -517,7 +520,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict
             pos[j] = inv[(size_t)t * k + j];
             wt[j] = w[(size_t)t * k + j];
         }
-    for (int c = threadIdx.x * 8; c < H; c += 256 * 8) {
+    for (int c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
         float acc[8];
         if (has_shared) load8(y + (size_t)(shared_base + t) * H + c, acc);
         else
@@ -541,12 +544,13 @@ int launch_combine(const uint16_t *y, const int32_t *inv, const float *w, int64_
                    hipStream_t st)
 {
     if (T == 0) return XS_OK;
+    const int nt = (int)(H / 8 < 64 ? 64 : (H / 8 > 512 ? 512 : (H / 8 + 63) / 64 * 64));
     if (out_dtype == XS_BF16)
-        combine_kernel<uint16_t><<<dim3((unsigned)T), dim3(256), 0, st>>>(y, inv, w, (int)k, (int)H, shared_base,
-                                                                          has_shared, (uint16_t *)out);
+        combine_kernel<uint16_t><<<dim3((unsigned)T), dim3(nt), 0, st>>>(y, inv, w, (int)k, (int)H, shared_base,
+                                                                         has_shared, (uint16_t *)out);
     else
-        combine_kernel<float><<<dim3((unsigned)T), dim3(256), 0, st>>>(y, inv, w, (int)k, (int)H, shared_base,
-                                                                       has_shared, (float *)out);
+        combine_kernel<float><<<dim3((unsigned)T), dim3(nt), 0, st>>>(y, inv, w, (int)k, (int)H, shared_base,
+                                                                      has_shared, (float *)out);
     XS_LAUNCH_CHECK();
     return XS_OK;
 }
