@@ -116,9 +116,11 @@ def test_moe_group_limited_and_scaling():
     assert max_abs_rel(out.float().cpu().numpy(), r["out_f32"]) <= TOL
 
 
-def test_moe_fp4_small():
-    """C5 structure at small size: MXFP4 routed experts, FP8 shared expert."""
-    c = make_case(48, 512, 256, 16, 6, seed=5, fp4=True)
+@pytest.mark.parametrize("T", [48, 80, 160, 300])
+def test_moe_fp4_small(T):
+    """C5 structure at small size: MXFP4 routed experts, FP8 shared expert;
+    18 / 30 / 60 / 112 rows per expert select 16- to 128-row tiles."""
+    c = make_case(T, 512, 256, 16, 6, seed=5 + T, fp4=True)
     g = to_device(c)
     _run_and_check(c, g, router_exact=True)
     _run_and_check(c, g, router_exact=False)

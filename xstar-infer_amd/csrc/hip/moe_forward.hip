@@ -134,6 +134,8 @@ static int check_params(const xs_moe_params *p)
     XS_REQUIRE(p->routed_format == XS_FP8_E4M3 || p->routed_format == XS_FP4_E2M1X2,
                "unsupported routed expert format");
     XS_REQUIRE(p->T * p->top_k + p->T < ((int64_t)1 << 31), "too many rows");
+    XS_REQUIRE(p->routed_format != XS_FP4_E2M1X2 || p->I % 256 == 0,
+               "shape mismatch: MXFP4 experts need I to be a multiple of 256");
     if (p->n_group > 1) {
         XS_REQUIRE(p->n_group <= 64 && p->E % p->n_group == 0 && p->E / p->n_group >= 2,
                    "n_group must divide E into groups of >= 2 (n_group <= 64)");

@@ -37,24 +37,29 @@ struct Cfg {
     static constexpr int TN = 256 / WN;         // wave columns
     static constexpr int MI = TM / 16;
     static constexpr int NJ = TN / 16;
-    static constexpr int NST = BM <= 32 ? 4 : 3;                 // LDS ring stages
-    static constexpr int BROW = FP4 ? 64 : 128;                  // B bytes per row per K step
-    static constexpr int A_BYTES = BM * 128;
+    // A K step is 128 wide for FP8 and 256 wide for MXFP4, so every weight row
+    // is read as whole 128-byte lines (a 64-byte half-line step fetched the
+    // streamed lines twice).
+    static constexpr int KSTEP = FP4 ? 256 : 128;
+    static constexpr int NST = FP4 ? (BM <= 16 ? 4 : (BM <= 64 ? 3 : 2)) : (BM <= 32 ? 4 : 3);   // LDS ring stages
+    static constexpr int AROW = FP4 ? 256 : 128;                 // A bytes per row per K step (FP8 / MXFP8)
+    static constexpr int BROW = 128;                             // B bytes per row per K step
+    static constexpr int A_BYTES = BM * AROW;
     static constexpr int B_BYTES = 256 * BROW;
-    static constexpr int SA_BYTES = 512;                         // 128 row scales (f32 or 4 x e8m0)
-    static constexpr int SB_BYTES = FP4 ? 1024 : 0;              // 256 column scale words (MXFP4)
+    static constexpr int SA_BYTES = FP4 ? 1024 : 512;            // row scales: 128 f32, or [2][128] x 4 e8m0
+    static constexpr int SB_BYTES = FP4 ? 2048 : 0;              // MXFP4 column scales: [2][256] x 4 e8m0
     static constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES + SB_BYTES;
     static constexpr int A_INSTR = A_BYTES / 1024;               // 1 KB per wave-wide DMA
     static constexpr int NA_W = A_INSTR >= NW ? A_INSTR / NW : 1; // per wave (dummies pad)
     static constexpr int NB_W = B_BYTES / 1024 / NW;
-    static constexpr int NS_W = FP4 ? 2 : 1;                     // row-scale (+ column-scale) dwords
+    static constexpr int NS_W = FP4 ? 4 : 1;                     // row-scale (+ column-scale) dwords
     static constexpr int PER_STAGE = NA_W + NB_W + NS_W;         // DMA instructions per wave per stage
     static constexpr int TRASH = 1024;                           // target of padding DMAs
 };
 
 // LDS row swizzles: 16-byte chunk c of row r lives at physical chunk c ^ f(r).
 __device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }   // 128-byte rows
-__device__ __forceinline__ int swz4(int r, int c) { return c ^ ((r >> 2) & 3); }   // 64-byte rows
+__device__ __forceinline__ int swz16(int r, int c) { return c ^ (r & 15); }        // 256-byte rows
 
 __device__ __forceinline__ v8i cat(v4i a, v4i b) { return v8i{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}; }
 
@@ -155,7 +160,7 @@ __global__ __launch_bounds__(BM >= 64 ? 512 : 256) void moe_gemm_kernel(GemmArgs
     for (int u = 0; u < S::NA_W; ++u) {
         const int q = wave + S::NW * u;                    // wave-wide instruction index
         const int p = 64 * q + lane;                   // LDS chunk written by this lane
-        const int r = p >> 3, c = swz8(r, p & 7);
+        const int r = FP4 ? p >> 4 : p >> 3, c = FP4 ? swz16(r, p & 15) : swz8(r, p & 7);
         const bool real = q < S::A_INSTR;
         gA[u] = a.A + (size_t)arow_of(real ? r : 0) * a.K + c * 16;
         lA[u] = real ? (uint32_t)(64 * q * 16) : 0xFFFFFFFFu;
@@ -166,7 +171,7 @@ __global__ __launch_bounds__(BM >= 64 ? 512 : 256) void moe_gemm_kernel(GemmArgs
         const int q = wave + S::NW * u;
         const int p = 64 * q + lane;
         if (FP4) {
-            const int vr = p >> 2, c = swz4(vr, p & 3);
+            const int vr = p >> 3, c = swz8(vr, p & 7);
             gB[u] = Bexp + (size_t)brow_of(vr) * (a.K / 2) + c * 16;
         } else {
             const int vr = p >> 3, c = swz8(vr, p & 7);
@@ -202,13 +207,14 @@ __global__ __launch_bounds__(BM >= 64 ? 512 : 256) void moe_gemm_kernel(GemmArgs
     const uint32_t trash_lds = __builtin_amdgcn_readfirstlane(lds_off(trash));
     // Issue the DMAs of K step kb into ring stage kb % NST.  Steps past the end
     // reload the last step (the stage is never read again): counts stay uniform.
+    const int KS = a.K / S::KSTEP;   // K steps
     auto issue = [&](int kb) {
-        const int kk = kb < KB ? kb : KB - 1;
+        const int kk = kb < KS ? kb : KS - 1;
         const uint32_t st = __builtin_amdgcn_readfirstlane(smem_base + (uint32_t)((kb % S::NST) * S::STAGE));
 #pragma unroll
         for (int u = 0; u < S::NA_W; ++u) {
             const uint32_t dst = lA[u] == 0xFFFFFFFFu ? trash_lds : st + __builtin_amdgcn_readfirstlane(lA[u]);
-            dma16(gA[u] + (size_t)kk * 128, dst);
+            dma16(gA[u] + (size_t)kk * S::AROW, dst);
         }
 #pragma unroll
         for (int u = 0; u < S::NB_W; ++u)
@@ -217,9 +223,13 @@ __global__ __launch_bounds__(BM >= 64 ? 512 : 256) void moe_gemm_kernel(GemmArgs
             if (a.stream_w) dma16_nt(gB[u] + (size_t)kk * S::BROW, d);
             else dma16(gB[u] + (size_t)kk * S::BROW, d);
         }
-        if (FP4) {
-            dma4(gSA + (size_t)kk * 4, sa_real ? st + S::A_BYTES + S::B_BYTES + wave * 256 : trash_lds);
-            dma4(gSB + (size_t)kk * 4, sb_real ? st + S::A_BYTES + S::B_BYTES + S::SA_BYTES + wave * 256 : trash_lds);
+        if (FP4) {         // 8 e8m0 per row per step: two words, halves h of the scale areas
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                dma4(gSA + (size_t)kk * 8 + 4 * h, sa_real ? st + S::A_BYTES + S::B_BYTES + h * 512 + wave * 256 : trash_lds);
+                dma4(gSB + (size_t)kk * 8 + 4 * h,
+                     sb_real ? st + S::A_BYTES + S::B_BYTES + S::SA_BYTES + h * 1024 + wave * 256 : trash_lds);
+            }
         } else {
             dma4(gSA + (size_t)kk * 4, sa_real ? st + S::A_BYTES + S::B_BYTES + wave * 256 : trash_lds);
         }
@@ -235,7 +245,7 @@ __global__ __launch_bounds__(BM >= 64 ? 512 : 256) void moe_gemm_kernel(GemmArgs
 #pragma unroll
     for (int s = 0; s < S::NST - 1; ++s) issue(s);
 
-    for (int kb = 0; kb < KB; ++kb) {
+    for (int kb = 0; kb < KS; ++kb) {
         wait_vmcnt<(S::NST - 2) * S::PER_STAGE>();   // this wave's DMAs for step kb have landed
         __syncthreads();                             // ... and every other wave's
         issue(kb + S::NST - 1);                      // refills the stage consumed at kb - 1
@@ -247,7 +257,7 @@ __global__ __launch_bounds__(BM >= 64 ? 512 : 256) void moe_gemm_kernel(GemmArgs
         // operand, lane 16g + r holds row r with K = [16g, 16g+16) in bytes 0..15
         // and K = [64+16g, 64+16g+16) in bytes 16..31, i.e. LDS chunks g and g+4
         // of the row; for an FP4 operand, lane 16g + r holds K = [32g, 32g+32)
-        // (element 2i in the low nibble), i.e. 16-byte chunk g of a 64-byte row.
+        // (element 2i in the low nibble), i.e. 16-byte chunk g of the slice's 64 bytes.
         // The e8m0 scale of (row r, 32-wide K block b) is taken from lane 16b + r.
         // Pinned by the FP8 x FP4 parity tests.
         //
@@ -256,31 +266,42 @@ __global__ __launch_bounds__(BM >= 64 ? 512 : 256) void moe_gemm_kernel(GemmArgs
         // r and columns 4g..4g+3 -- one activation scale per lane and subtile,
         // and four adjacent output columns per lane for the epilogue stores.
         v8i xfr[S::MI];   // activation fragments, one per 16-token subtile
-#pragma unroll
-        for (int i = 0; i < S::MI; ++i) {
-            int r = wm * S::TM + 16 * i + l16;
-            v4i lo = *reinterpret_cast<const v4i *>(sa_ + r * 128 + swz8(r, g) * 16);
-            v4i hi = *reinterpret_cast<const v4i *>(sa_ + r * 128 + swz8(r, g + 4) * 16);
-            xfr[i] = cat(lo, hi);
-        }
         if (FP4) {
+            // two 128-wide slices u per step: activation chunks 8u+g, 8u+g+4 of a
+            // 256-byte row; weight chunk 4u+g of a 128-byte row; scale words [u][row]
             const uint32_t *sAw = reinterpret_cast<const uint32_t *>(ssc);
             const uint32_t *sBw = reinterpret_cast<const uint32_t *>(ssc + S::SA_BYTES);
-            int sx[S::MI];
 #pragma unroll
-            for (int i = 0; i < S::MI; ++i) sx[i] = (int)((sAw[wm * S::TM + 16 * i + l16] >> (8 * g)) & 0xffu);
+            for (int u = 0; u < 2; ++u) {
+                int sx[S::MI];
 #pragma unroll
-            for (int j = 0; j < S::NJ; ++j) {
-                int vr = wn * S::TN + 16 * j + l16;
-                v4i b4 = *reinterpret_cast<const v4i *>(sb_ + vr * 64 + swz4(vr, g) * 16);
-                v8i wfr = v8i{b4[0], b4[1], b4[2], b4[3], 0, 0, 0, 0};
-                int sw = (int)((sBw[vr] >> (8 * g)) & 0xffu);
+                for (int i = 0; i < S::MI; ++i) {
+                    const int r = wm * S::TM + 16 * i + l16;
+                    v4i lo = *reinterpret_cast<const v4i *>(sa_ + r * 256 + swz16(r, 8 * u + g) * 16);
+                    v4i hi = *reinterpret_cast<const v4i *>(sa_ + r * 256 + swz16(r, 8 * u + g + 4) * 16);
+                    xfr[i] = cat(lo, hi);
+                    sx[i] = (int)((sAw[128 * u + r] >> (8 * g)) & 0xffu);
+                }
 #pragma unroll
-                for (int i = 0; i < S::MI; ++i)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wfr, xfr[i], acc[i][j], 4, 0, 0,
-                                                                                sw, 0, sx[i]);
+                for (int j = 0; j < S::NJ; ++j) {
+                    const int vr = wn * S::TN + 16 * j + l16;
+                    v4i b4 = *reinterpret_cast<const v4i *>(sb_ + vr * 128 + swz8(vr, 4 * u + g) * 16);
+                    v8i wfr = v8i{b4[0], b4[1], b4[2], b4[3], 0, 0, 0, 0};
+                    const int sw = (int)((sBw[256 * u + vr] >> (8 * g)) & 0xffu);
+#pragma unroll
+                    for (int i = 0; i < S::MI; ++i)
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wfr, xfr[i], acc[i][j], 4, 0, 0,
+                                                                                    sw, 0, sx[i]);
+                }
             }
         } else {
+#pragma unroll
+            for (int i = 0; i < S::MI; ++i) {
+                int r = wm * S::TM + 16 * i + l16;
+                v4i lo = *reinterpret_cast<const v4i *>(sa_ + r * 128 + swz8(r, g) * 16);
+                v4i hi = *reinterpret_cast<const v4i *>(sa_ + r * 128 + swz8(r, g + 4) * 16);
+                xfr[i] = cat(lo, hi);
+            }
             const float *sAk = reinterpret_cast<const float *>(ssc);
             // weight block scales: gate_up uses block 0 (gate) for even subtiles and
             // block 1 (up) for odd ones; down uses the wave's own 128-column block
@@ -463,6 +484,7 @@ static size_t gemm_smem_bytes(int K)
 template <int BM, bool GATEUP, bool FP4>
 static int launch_one(const GemmArgs &a, int grid_y, hipStream_t st)
 {
+    if (FP4 && a.K % 256 != 0) return set_error(XS_ERR_UNSUPPORTED, "MXFP4 GEMM: K=%d is not a multiple of 256", a.K);
     size_t smem = gemm_smem_bytes<BM, GATEUP, FP4>(a.K);
     if (smem > 160 * 1024) return set_error(XS_ERR_UNSUPPORTED, "K=%d needs %zu bytes of LDS", a.K, smem);
     auto fn = moe_gemm_kernel<BM, GATEUP, FP4>;
