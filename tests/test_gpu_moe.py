@@ -116,11 +116,15 @@ def test_moe_group_limited_and_scaling():
     assert max_abs_rel(out.float().cpu().numpy(), r["out_f32"]) <= TOL
 
 
+@pytest.mark.parametrize("mode", ["0", "1"])
 @pytest.mark.parametrize("T", [48, 80, 160, 300])
-def test_moe_fp4_small(T):
+def test_moe_fp4_small(T, mode, monkeypatch):
     """C5 structure at small size: MXFP4 routed experts, FP8 shared expert;
-    18 / 30 / 60 / 112 rows per expert select 16- to 128-row tiles."""
-    c = make_case(T, 512, 256, 16, 6, seed=5 + T, fp4=True)
+    18 / 30 / 60 / 112 rows per expert select 16- to 128-row tiles; the
+    one-block-per-tile kernels (mode 0) and the persistent ones (mode 1, 16- to
+    64-row tiles; K steps in pairs, so H and I are multiples of 512)."""
+    monkeypatch.setenv("XS_MOE_STREAM", mode)
+    c = make_case(T, 512, 512, 16, 6, seed=5 + T, fp4=True)
     g = to_device(c)
     _run_and_check(c, g, router_exact=True)
     _run_and_check(c, g, router_exact=False)

@@ -62,11 +62,12 @@ static bool use_wide(const xs_moe_params *p)
     return p->T * p->top_k >= 32 * p->E;
 }
 
-// Decode-sized FP8 layers may run the persistent GEMMs (moe_gemm_stream.hip):
+// The routed (FP8: and shared) GEMMs may run the persistent kernels
+// (moe_gemm_stream.hip) when the tall-tile FP8 kernels are not used:
 // 0 never, 1 by size, 2 always.  XS_MOE_STREAM=0|1 forces (benchmarks, tests).
 static int use_stream(const xs_moe_params *p)
 {
-    if (p->routed_format != XS_FP8_E4M3 || use_wide(p)) return 0;
+    if (p->routed_format == XS_FP8_E4M3 && use_wide(p)) return 0;
     const char *force = getenv("XS_MOE_STREAM");   // read per call: tests switch it
     if (force && !strcmp(force, "0")) return 0;
     if (force && !strcmp(force, "1")) return 2;
@@ -105,7 +106,8 @@ static WsLayout layout(const xs_moe_params *p)
         const bool st = use_stream(p);
         const int64_t n1 = st ? stream_items(true, (int)I, tiles16_max(p)) : 0;
         const int64_t n2 = st ? stream_items(false, (int)H, tiles16_max(p)) : 0;
-        const size_t p1 = st ? stream_part_bytes(n1, (int)H, 32) : 0, p2 = st ? stream_part_bytes(n2, (int)I, 32) : 0;
+        const int pbm = fp4 ? 64 : 32;
+        const size_t p1 = st ? stream_part_bytes(n1, (int)H, pbm) : 0, p2 = st ? stream_part_bytes(n2, (int)I, pbm) : 0;
         take(L.part, p1 > p2 ? p1 : p2);
         take(L.cnt1, st ? 4 * (size_t)(n1 + 1) : 0);
         take(L.cnt2, st ? 4 * (size_t)(n2 + 1) : 0);
@@ -217,9 +219,11 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     // less and the one-block-per-tile kernels are faster.
     const int sm = use_stream(p);
     const int64_t rows_all = S + shared_rows;
-    const bool stream = stream_fits(bm, routed_tiles + shared_tiles, rows_all) &&
-                        (sm == 2 || (sm == 1 && stream_items(true, (int)I, routed_tiles + shared_tiles) >=
-                                                    2 * (int64_t)stream_blocks()));
+    // FP8: all tiles in one launch; MXFP4: the routed tiles (the FP8 shared
+    // expert runs the tiled kernel)
+    const int stream_tiles = fp4 ? routed_tiles : routed_tiles + shared_tiles;
+    const bool stream = stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
+                        (sm == 2 || (sm == 1 && stream_items(true, (int)I, stream_tiles) >= 2 * (int64_t)stream_blocks()));
     if (stream) {
         po.zero = WS(int32_t, cnt1);
         po.zero_n = stream_items(true, (int)I, tiles16_max(p)) + 1;
@@ -259,6 +263,13 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     g2.Cy = WS(uint16_t, y);
     g2.ldc = H;
 
+    if (stream) {
+        g1.part = g2.part = WS(float, part);
+        g1.cnt = WS(int32_t, cnt1);
+        g2.cnt = g1.zero_cnt = WS(int32_t, cnt2);
+        g1.zero_n = (int)stream_items(false, (int)H, tiles16_max(p)) + 1;
+    }
+
     if ((rc = prof_mark(4, st))) return rc;
     if (!fp4) {
         g1.A = WS(uint8_t, xq);
@@ -266,13 +277,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g1.Cs = WS(float, acts);
         g1.e_lo = 0;
         g1.e_hi = (int)E + (shared_rows ? 1 : 0);
-        if (stream) {
-            g1.part = g2.part = WS(float, part);
-            g1.cnt = WS(int32_t, cnt1);
-            g2.cnt = g1.zero_cnt = WS(int32_t, cnt2);
-            g1.zero_n = (int)stream_items(false, (int)H, tiles16_max(p)) + 1;
-        }
-        rc = stream ? launch_gemm_stream(g1, true, routed_tiles + shared_tiles, rows_all, st)
+        rc = stream ? launch_gemm_stream(g1, true, false, stream_tiles, rows_all, st)
              : wide ? launch_gemm_wide(g1, true, routed_tiles + shared_tiles, st)
                     : launch_gemm(g1, true, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
@@ -280,7 +285,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g2.As = WS(float, acts);
         g2.e_lo = 0;
         g2.e_hi = g1.e_hi;
-        rc = stream ? launch_gemm_stream(g2, false, routed_tiles + shared_tiles, rows_all, st)
+        rc = stream ? launch_gemm_stream(g2, false, false, stream_tiles, rows_all, st)
              : wide ? launch_gemm_wide(g2, false, routed_tiles + shared_tiles, st)
                     : launch_gemm(g2, false, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
@@ -291,7 +296,8 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         r1.Cs = WS(uint8_t, actms);
         r1.e_lo = 0;
         r1.e_hi = (int)E;
-        rc = launch_gemm(r1, true, true, routed_tiles, st);
+        rc = stream ? launch_gemm_stream(r1, true, true, stream_tiles, rows_all, st)
+                    : launch_gemm(r1, true, true, routed_tiles, st);
         if (rc) return rc;
         if (shared_rows) {
             GemmArgs s1 = g1;
@@ -308,7 +314,8 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         r2.As = WS(uint8_t, actms);
         r2.e_lo = 0;
         r2.e_hi = (int)E;
-        rc = launch_gemm(r2, false, true, routed_tiles, st);
+        rc = stream ? launch_gemm_stream(r2, false, true, stream_tiles, rows_all, st)
+                    : launch_gemm(r2, false, true, routed_tiles, st);
         if (rc) return rc;
         if (shared_rows) {
             GemmArgs s2 = g2;

@@ -38,14 +38,15 @@ int launch_gemm(const GemmArgs &a, bool gateup, bool fp4, int grid_y, hipStream_
 // a.tile_tab the tile table for that height.
 int wide_tile_rows();
 int launch_gemm_wide(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st);
-// Persistent decode GEMMs (moe_gemm_stream.hip), FP8, a.bm 16 or 32.  tiles_max
-// bounds the tile count of the launch's range of the tile table, rows_max the
-// positions of a.row_token; a.cnt holds 1 + items counters, zero on entry.
+// Persistent stream-K GEMMs (moe_gemm_stream.hip): FP8 with a.bm 16 or 32,
+// MXFP4 with a.bm 16, 32 or 64.  tiles_max bounds the tile count of the
+// launch's range of the tile table, rows_max the positions; a.cnt holds one
+// counter per item, zero on entry.
 int stream_blocks();
-bool stream_fits(int bm, int64_t tiles_max, int64_t rows_max);
+bool stream_fits(int bm, bool fp4, int64_t tiles_max, int64_t rows_max);
 int64_t stream_items(bool gateup, int N, int64_t tiles_max);
 size_t stream_part_bytes(int64_t items_max, int K, int bm);
-int launch_gemm_stream(const GemmArgs &a, bool gateup, int tiles_max, int64_t rows_max, hipStream_t st);
+int launch_gemm_stream(const GemmArgs &a, bool gateup, bool fp4, int tiles_max, int64_t rows_max, hipStream_t st);
 int launch_combine(const uint16_t *y, const int32_t *inv, const float *w, int64_t T, int64_t k,
                    int64_t H, int64_t shared_base, int has_shared, void *out, int out_dtype,
                    hipStream_t st);

@@ -1,5 +1,6 @@
-// moe_gemm_stream.hip -- persistent grouped FP8 block-scaled expert GEMMs for
-// decode-sized tiles (16 or 32 rows of one expert), gfx950.
+// moe_gemm_stream.hip -- persistent grouped expert GEMMs on gfx950: FP8
+// block-scaled experts on 16- or 32-row tiles (decode) and MXFP4 experts on
+// 16- to 64-row tiles.
 //
 // Nearest reference code: gemm_silu_and_mul_kernel (xstar_cpp/src/ops/mlp.cu:52-200)
 // and gemm_kernel (xstar_cpp/src/ops/gemm.cu:41-210); numerics as the FP8 tiles of
@@ -37,31 +38,50 @@ namespace {
 
 constexpr int kNW = 4;                 // waves per block
 constexpr int kNT = 64 * kNW;
-constexpr int kNST = 4;                // ring stages
 constexpr int kTrash = 1024;           // LDS target of padding DMAs
-constexpr int kMaxItems = 40;          // item descriptors a block can hold
 
-template <int BM>
+// FP8: e4m3 weights with 128x128 f32 block scales, 1x128 FP8 activations, K
+// steps of 128 (the products are folded with the scales in VALU).  MXFP4:
+// e2m1 weights and MXFP8 activations with e8m0 scales per 32 K, applied by the
+// MFMA; K steps of 256, so a weight row is read as whole 128-byte lines.
+template <int BM, bool FP4>
 struct SCfg {
     static constexpr int MI = BM / 16;             // 16-token subtiles (every wave holds all of them)
     static constexpr int NJ = 4;                   // 16-column subtiles per wave (64 weight rows)
-    static constexpr int A_BYTES = BM * 128;
+    static constexpr int KSTEP = FP4 ? 256 : 128;
+    static constexpr int NST = FP4 ? 3 : 4;    // ring stages (MXFP4: the scale buffers of a pair of steps are
+                                               // rewritten 2 steps ahead, which 2 buffers allow)
+    static constexpr int MAXIT = FP4 && BM == 64 ? 30 : 40;          // item descriptors a block can hold
+    static constexpr int AROW = FP4 ? 256 : 128;                      // activation bytes per row and step
+    static constexpr int A_BYTES = BM * AROW;
     static constexpr int B_BYTES = 256 * 128;
-    static constexpr int SA_OFF = A_BYTES + B_BYTES;   // 64 activation row scales (f32)
-    static constexpr int SB_OFF = SA_OFF + 256;        // 2 weight block scales (+ padding)
-    static constexpr int STAGE = SB_OFF + 256;
-    static constexpr int A_INSTR = A_BYTES / 1024;     // wave-wide 1 KB DMAs for A (<= kNW)
+    // FP8: 64 row scales and 2 block scales ride in each stage.  MXFP4: the
+    // e8m0 scales (8 per row and step) are fetched 16 bytes per row for each
+    // pair of steps into a separate double buffer (4-byte gathers from 320
+    // rows every step outnumbered all operand requests to the L2).
+    static constexpr int SA_BYTES = FP4 ? 0 : 256;
+    static constexpr int SB_BYTES = FP4 ? 0 : 256;
+    static constexpr int SA_OFF = A_BYTES + B_BYTES;
+    static constexpr int SB_OFF = SA_OFF + SA_BYTES;
+    static constexpr int STAGE = SB_OFF + SB_BYTES;
+    static constexpr int A_INSTR = A_BYTES / 1024;     // wave-wide 1 KB DMAs for A
+    static constexpr int NA = A_INSTR > kNW ? A_INSTR / kNW : 1;   // per wave (padding ones target the trash)
     static constexpr int NB = B_BYTES / 1024 / kNW;    // weight DMAs per wave
-    static constexpr int PER_STAGE = 1 + NB + 1;       // loads per wave per stage
-    static constexpr int RED_OFF = kNST * STAGE + kTrash;
-    static constexpr int META_OFF = RED_OFF + 4 * 4 * BM;
-    static constexpr int RTOK_OFF = META_OFF + 16 * kMaxItems;
-    static constexpr int SMEM = RTOK_OFF + 4 * BM * kMaxItems;
-    static_assert(A_INSTR >= 1 && A_INSTR <= kNW && BM <= 64, "tile rows");
+    static constexpr int NS = FP4 ? 2 : 1;             // scale DMAs per wave
+    static constexpr int PER_STAGE = NA + NB + NS;     // loads per wave per stage
+    static constexpr int SC_OFF = NST * STAGE + kTrash;    // MXFP4 scale buffers [2][256 + 64 rows][16 B]
+    static constexpr int SC_BUF = FP4 ? 320 * 16 : 0;
+    static constexpr int RED_OFF = SC_OFF + 2 * SC_BUF;
+    static constexpr int META_OFF = RED_OFF + (FP4 ? 0 : 16 * BM);
+    static constexpr int RTOK_OFF = META_OFF + 16 * MAXIT;
+    static constexpr int SMEM = RTOK_OFF + 2 * BM * MAXIT;   // row tokens as 16-bit (T < 65536)
+    static_assert(A_INSTR >= 1 && (A_INSTR <= kNW || A_INSTR % kNW == 0) && BM <= 64, "tile rows");
+    static_assert(SMEM <= 160 * 1024, "LDS");
     static_assert(SMEM <= 160 * 1024, "LDS");
 };
 
-__device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }
+__device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }     // 128-byte rows
+__device__ __forceinline__ int swz16(int r, int c) { return c ^ (r & 15); }         // 256-byte rows
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p)
 {
@@ -74,7 +94,8 @@ __device__ __forceinline__ v8i cat(v4i a, v4i b) { return v8i{a[0], a[1], a[2], 
 // M0 carries the wave-uniform LDS base; it is written only here.
 __device__ __forceinline__ void dma16_v(const void *g, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
 }
 __device__ __forceinline__ void dma16_s(const uint8_t *sbase, uint32_t voff, uint32_t lds)
 {
@@ -86,7 +107,8 @@ __device__ __forceinline__ void dma16_s_nt(const uint8_t *sbase, uint32_t voff, 
 }
 __device__ __forceinline__ void dma4_v(const void *g, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
 }
 // A pointer the compiler cannot prove wave-uniform (it was read from LDS) made
 // scalar, for the saddr form of the DMAs.
@@ -114,20 +136,21 @@ __device__ uint64_t g_stream_trace[2][2048][6];
 // Number of 256-row weight slabs per tile.
 __host__ __device__ __forceinline__ int slabs_of(bool gateup, int N) { return gateup ? N / 128 : (N + 255) / 256; }
 
-template <int BM, bool GATEUP>
+template <int BM, bool GATEUP, bool FP4>
 __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
 {
-    using C = SCfg<BM>;
+    using C = SCfg<BM, FP4>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int last_flag;
     float *red = reinterpret_cast<float *>(smem + C::RED_OFF);      // [4][BM]
-    int4 *meta = reinterpret_cast<int4 *>(smem + C::META_OFF);      // [kMaxItems]
-    int *rtok = reinterpret_cast<int *>(smem + C::RTOK_OFF);        // [kMaxItems][BM]
+    int4 *meta = reinterpret_cast<int4 *>(smem + C::META_OFF);      // [MAXIT]
+    uint16_t *rtok = reinterpret_cast<uint16_t *>(smem + C::RTOK_OFF);   // [MAXIT][BM]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, g = lane >> 4;
-    const int KB = a.K / 128;
+    const int KB = a.K / C::KSTEP;       // K steps per item
+    const int KB128 = a.K / 128;         // FP8 scale blocks along K
     XS_TRACE(0);
 
     // Counters of the launch that follows (the down GEMM after gate_up).
@@ -149,7 +172,7 @@ __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
     if (b >= G) return;
     const int s0 = (int)((int64_t)b * W / G), s1 = (int)((int64_t)(b + 1) * W / G);
     const int it0 = s0 / KB, it1 = (s1 - 1) / KB;
-    const int nit = it1 - it0 + 1;   // <= kMaxItems (grid sized by the host)
+    const int nit = it1 - it0 + 1;   // <= MAXIT (grid sized by the host)
 
     // ---- item descriptors: {expert, first position, rows, slab | multi-tile << 30} ----
     // Items run expert by expert, then slab, then tile (tab .w: tile index in
@@ -168,17 +191,19 @@ __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
     for (int q = tid; q < nit * BM; q += kNT) {
         const int4 m = meta[q / BM];
         const int p = m.y + min(q % BM, m.z - 1);
-        rtok[q] = a.row_token ? a.row_token[p] : p;
+        rtok[q] = (uint16_t)(a.row_token ? a.row_token[p] : p);
     }
     __syncthreads();
 
     XS_TRACE(1);
     // ---- issue side: DMA sources of the item being loaded ----
-    const uint32_t ring = lds_addr(smem), trash = lds_addr(smem + kNST * C::STAGE);
+    const uint32_t ring = lds_addr(smem), trash = lds_addr(smem + C::NST * C::STAGE);
+    const uint32_t sc_base = lds_addr(smem + C::SC_OFF);
     const int Nrows = GATEUP ? 2 * a.N : a.N;
     int cur = -1;
-    const uint8_t *gA = nullptr;        // this lane's activation chunk (64-bit: T x K may exceed 4 GB)
-    const uint8_t *gS = nullptr;        // this lane's row-scale / block-scale word
+    const uint8_t *gA[C::NA];           // this lane's activation chunks (64-bit: T x K may exceed 4 GB)
+    const uint8_t *gS = nullptr;        // this lane's row-scale / block-scale word (FP8), row-scale word (MXFP4)
+    const uint8_t *gS2 = nullptr;       // MXFP4: this lane's weight-scale word
     const uint8_t *bW = nullptr;        // wave-uniform weight base of the item
     uint32_t oW[C::NB];                 // this lane's weight chunk offsets in the expert
     bool w_nt = false;
@@ -189,33 +214,39 @@ __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
         const bool shared = e == a.E;
         const int n0 = slab * (GATEUP ? 128 : 256);
         w_nt = (m.w >> 30) == 0;
-        bW = uniform_ptr(shared ? a.Bsh : a.B + (size_t)e * Nrows * a.K);
-        {
-            const int p = 64 * wave + lane, r = p >> 3;
-            const int row = wave < C::A_INSTR ? r : 0;
-            gA = a.A + (size_t)rtok[li * BM + row] * a.K + swz8(r, p & 7) * 16;
+        bW = uniform_ptr(shared ? a.Bsh : a.B + (size_t)e * Nrows * (FP4 ? a.K / 2 : a.K));
+#pragma unroll
+        for (int u = 0; u < C::NA; ++u) {
+            const int q = wave + kNW * u, p = 64 * q + lane;
+            const int r = FP4 ? p >> 4 : p >> 3, c = FP4 ? swz16(r, p & 15) : swz8(r, p & 7);
+            gA[u] = a.A + (size_t)rtok[li * BM + (q < C::A_INSTR ? r : 0)] * a.K + c * 16;
         }
+        // weight row of slab row vr (gate_up: 16-row gate / up subtiles interleaved)
+        auto brow_of = [&](int vr) -> int {
+            if (GATEUP) {
+                const int sub = vr >> 4, w = vr & 15, n = n0 + (sub >> 1) * 16 + w;
+                return (sub & 1) ? a.N + n : n;
+            }
+            return min(n0 + vr, a.N - 1);
+        };
 #pragma unroll
         for (int u = 0; u < C::NB; ++u) {
             const int p = 64 * (wave + kNW * u) + lane;
             const int vr = p >> 3;
-            int brow;
-            if (GATEUP) {
-                const int sub = vr >> 4, w = vr & 15, n = n0 + (sub >> 1) * 16 + w;
-                brow = (sub & 1) ? a.N + n : n;
-            } else {
-                brow = min(n0 + vr, a.N - 1);
-            }
-            oW[u] = (uint32_t)brow * (uint32_t)a.K + (uint32_t)(swz8(vr, p & 7) * 16);
+            oW[u] = (uint32_t)brow_of(vr) * (uint32_t)(FP4 ? a.K / 2 : a.K) + (uint32_t)(swz8(vr, p & 7) * 16);
         }
-        if (wave == 0) {          // activation row scales, row = lane (clamped)
-            gS = reinterpret_cast<const uint8_t *>(a.As) + (size_t)rtok[li * BM + min(lane, BM - 1)] * KB * 4;
+        if (FP4)                  // weight scales (e8m0 per 32 K) of slab row 64 * wave + lane
+            gS2 = reinterpret_cast<const uint8_t *>(a.Bs) + ((size_t)e * Nrows + brow_of(64 * wave + lane)) * (a.K / 32);
+        if (FP4) {                // activation row scales (e8m0 per 32 K), row = lane (clamped)
+            gS = reinterpret_cast<const uint8_t *>(a.As) + (size_t)rtok[li * BM + min(lane, BM - 1)] * (a.K / 32);
+        } else if (wave == 0) {   // activation row scales, row = lane (clamped)
+            gS = reinterpret_cast<const uint8_t *>(a.As) + (size_t)rtok[li * BM + min(lane, BM - 1)] * KB128 * 4;
         } else {                  // wave 1: block scales of the slab's two 128-row blocks
-            const float *Bsf = shared ? a.Bssh : reinterpret_cast<const float *>(a.Bs) + (size_t)e * (Nrows / 128) * KB;
+            const float *Bsf = shared ? a.Bssh : reinterpret_cast<const float *>(a.Bs) + (size_t)e * (Nrows / 128) * KB128;
             int nb;
             if (GATEUP) nb = (lane == 1 ? a.N + n0 : n0) / 128;
             else nb = min(n0 / 128 + (lane == 1 ? 1 : 0), a.N / 128 - 1);
-            gS = reinterpret_cast<const uint8_t *>(Bsf + (size_t)nb * KB);
+            gS = reinterpret_cast<const uint8_t *>(Bsf + (size_t)nb * KB128);
         }
     };
     // Issue side position: item li_i, step kb_i (advanced one step per issue).
@@ -228,8 +259,12 @@ __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
             setup(li_i);
             cur = li_i;
         }
-        const uint32_t st = __builtin_amdgcn_readfirstlane(ring + (uint32_t)((s & (kNST - 1)) * C::STAGE));
-        dma16_v(gA + (size_t)kb_i * 128, wave < C::A_INSTR ? st + 1024 * wave : trash);
+        const uint32_t st = __builtin_amdgcn_readfirstlane(ring + (uint32_t)((s % C::NST) * C::STAGE));
+#pragma unroll
+        for (int u = 0; u < C::NA; ++u) {
+            const int q = wave + kNW * u;
+            dma16_v(gA[u] + (size_t)kb_i * C::AROW, q < C::A_INSTR ? st + 1024 * q : trash);
+        }
         const uint8_t *wb = uniform_ptr(bW + (size_t)kb_i * 128);
         const uint32_t d0 = __builtin_amdgcn_readfirstlane(st + C::A_BYTES + (uint32_t)(wave * 1024));
         if (w_nt) {
@@ -239,7 +274,19 @@ __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
 #pragma unroll
             for (int u = 0; u < C::NB; ++u) dma16_s(wb, oW[u], d0 + (uint32_t)(u * kNW * 1024));
         }
-        dma4_v(gS + (size_t)kb_i * 4, wave == 0 ? st + C::SA_OFF : (wave == 1 ? st + C::SB_OFF : trash));
+        if (FP4) {
+            // the scales of steps 2p, 2p+1 (16 bytes per row) land in buffer p % 2
+            // with step 2p's loads (or with the block's first step); otherwise
+            // the same number of loads goes to the trash
+            const int gs = s0 + n_issued;
+            const bool load = n_issued < n_steps && ((gs & 1) == 0 || n_issued == 0);
+            const uint32_t sc = __builtin_amdgcn_readfirstlane(sc_base + (uint32_t)(((gs >> 1) & 1) * C::SC_BUF));
+            const int kp = kb_i & ~1;
+            dma16_v(gS2 + (size_t)kp * 8, load ? sc + 1024 * wave : trash);
+            dma16_v(gS + (size_t)kp * 8, load && wave == 0 ? sc + 4096 : trash);
+        } else {
+            dma4_v(gS + (size_t)kb_i * 4, wave == 0 ? st + C::SA_OFF : (wave == 1 ? st + C::SB_OFF : trash));
+        }
         if (++n_issued < n_steps && ++kb_i == KB) {
             kb_i = 0;
             ++li_i;
@@ -251,7 +298,40 @@ __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
         const int4 m = meta[li];
         const int pos0 = m.y, rows = m.z, slab = m.w & 0x3fffffff;
         const int wn = wave;
-        if (GATEUP) {
+        if (GATEUP && FP4) {
+            // MXFP8 1x32 requant: a 32-column block is the wave's two act column
+            // subtiles, so the block amax stays within the wave
+            const int n0 = slab * 128;
+            uint8_t *Cs8 = reinterpret_cast<uint8_t *>(a.Cs);
+#pragma unroll
+            for (int i = 0; i < C::MI; ++i) {
+                const int r = 16 * i + l16;
+                float act[2][4];
+                float mx = 0.f;
+#pragma unroll
+                for (int p = 0; p < 2; ++p)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float gt = acc[i][2 * p][v], up = acc[i][2 * p + 1][v];
+                        act[p][v] = gt * fast_sigmoid(gt) * up;
+                        mx = fmaxf(mx, __builtin_fabsf(act[p][v]));
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 16, WAVE));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+                const int se = mx_exponent(mx, 8);
+                if (r < rows) {
+#pragma unroll
+                    for (int p = 0; p < 2; ++p) {
+                        float q[4];
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) q[v] = fminf(fmaxf(__builtin_ldexpf(act[p][v], -se), -448.f), 448.f);
+                        *reinterpret_cast<uint32_t *>(a.Cq + (size_t)(pos0 + r) * a.N + n0 + (2 * wn + p) * 16 + 4 * g) =
+                            e4m3_pack2_hw(q[0], q[1]) | (e4m3_pack2_hw(q[2], q[3]) << 16);
+                    }
+                    if (g == 0) Cs8[(size_t)(pos0 + r) * (a.N / 32) + (n0 + 32 * wn) / 32] = (uint8_t)(se + 127);
+                }
+            }
+        } else if (GATEUP) {
             const int n0 = slab * 128;
             float act[C::MI][2][4];
 #pragma unroll
@@ -373,13 +453,13 @@ __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
     const bool last_split = s1 < (it1 + 1) * KB || s0 > it1 * KB;
 
 #pragma unroll
-    for (int j = 0; j < kNST - 1; ++j) issue(s0 + j);
+    for (int j = 0; j < C::NST - 1; ++j) issue(s0 + j);
 
     int li = 0, kb = s0 % KB;                        // compute side position
     for (int s = s0; s < s1; ++s) {
-        wait_vm<(kNST - 2) * C::PER_STAGE>();    // this wave's loads of step s landed
-        __syncthreads();                          // ... and every wave's; stage (s-1) % kNST is free
-        issue(s + kNST - 1);
+        wait_vm<(C::NST - 2) * C::PER_STAGE>();  // this wave's loads of step s landed
+        __syncthreads();                          // ... and every wave's; stage (s-1) % NST is free
+        issue(s + C::NST - 1);
         if (s == s0) XS_TRACE(2);
         if (s == s0 || kb == 0) {
 #pragma unroll
@@ -387,41 +467,74 @@ __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
 #pragma unroll
                 for (int j = 0; j < C::NJ; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
         }
-        const uint8_t *sA = smem + (s & (kNST - 1)) * C::STAGE;
+        const uint8_t *sA = smem + (s % C::NST) * C::STAGE;
         const uint8_t *sW = sA + C::A_BYTES;
-        const float *sS = reinterpret_cast<const float *>(sA + C::SA_OFF);
-        const float *sBk = reinterpret_cast<const float *>(sA + C::SB_OFF);
-        const float sb0 = GATEUP ? sBk[0] : sBk[wave >> 1];
-        const float sb1 = GATEUP ? sBk[1] : sb0;
-        // Operand layout of v_mfma_f32_16x16x128_f8f6f4: lane 16g + r holds row r
-        // with K bytes [16g, 16g+16) and [64+16g, 64+16g+16): LDS chunks g, g+4.
+        // Operand layout of v_mfma_*_16x16x128_f8f6f4: an FP8 operand's lane
+        // 16g + r holds row r with K bytes [16g, 16g+16) and [64+16g, 64+16g+16)
+        // (LDS chunks g, g+4 of a 128-wide slice); an FP4 operand's lane holds K
+        // elements [32g, 32g+32), chunk g of the slice's 64 bytes, and the e8m0
+        // scale of (row r, 32-wide block b) comes from lane 16b + r.
         // Weights are operand A, tokens operand B: lane 16g + r of the result
         // holds token r and weight rows 4g..4g+3 of the subtile.
-        v8i xf[C::MI];
-        float c0[C::MI], c1[C::MI];
+        if (FP4) {
+            // scale buffer of step s: rows of 16 bytes = [step parity][slice][4 x 32-K block]
+            const uint32_t *scw = reinterpret_cast<const uint32_t *>(smem + C::SC_OFF + ((s >> 1) & 1) * C::SC_BUF);
+            const int hw = (s & 1) * 2;
 #pragma unroll
-        for (int i = 0; i < C::MI; ++i) {
-            const int r = 16 * i + l16;
-            const uint8_t *rp = sA + r * 128;
-            xf[i] = cat(*reinterpret_cast<const v4i *>(rp + swz8(r, g) * 16),
-                        *reinterpret_cast<const v4i *>(rp + swz8(r, g + 4) * 16));
-            const float sx = sS[r];
-            c0[i] = sx * sb0;
-            c1[i] = sx * sb1;
-        }
+            for (int u = 0; u < 2; ++u) {      // two 128-wide slices per step
+                v8i xf[C::MI];
+                int sx[C::MI];
 #pragma unroll
-        for (int j = 0; j < C::NJ; ++j) {
-            const int vr = 64 * wave + 16 * j + l16;
-            const uint8_t *rp = sW + vr * 128;
-            const v8i wf = cat(*reinterpret_cast<const v4i *>(rp + swz8(vr, g) * 16),
-                               *reinterpret_cast<const v4i *>(rp + swz8(vr, g + 4) * 16));
+                for (int i = 0; i < C::MI; ++i) {
+                    const int r = 16 * i + l16;
+                    const uint8_t *rp = sA + r * 256;
+                    xf[i] = cat(*reinterpret_cast<const v4i *>(rp + swz16(r, 8 * u + g) * 16),
+                                *reinterpret_cast<const v4i *>(rp + swz16(r, 8 * u + g + 4) * 16));
+                    sx[i] = (int)((scw[4 * (256 + r) + hw + u] >> (8 * g)) & 0xffu);
+                }
+#pragma unroll
+                for (int j = 0; j < C::NJ; ++j) {
+                    const int vr = 64 * wave + 16 * j + l16;
+                    const v4i b4 = *reinterpret_cast<const v4i *>(sW + vr * 128 + swz8(vr, 4 * u + g) * 16);
+                    const v8i wf = v8i{b4[0], b4[1], b4[2], b4[3], 0, 0, 0, 0};
+                    const int sw = (int)((scw[4 * vr + hw + u] >> (8 * g)) & 0xffu);
+#pragma unroll
+                    for (int i = 0; i < C::MI; ++i)
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf[i], acc[i][j], 4, 0, 0, sw, 0,
+                                                                                    sx[i]);
+                }
+            }
+        } else {
+            const float *sS = reinterpret_cast<const float *>(sA + C::SA_OFF);
+            const float *sBk = reinterpret_cast<const float *>(sA + C::SB_OFF);
+            const float sb0 = GATEUP ? sBk[0] : sBk[wave >> 1];
+            const float sb1 = GATEUP ? sBk[1] : sb0;
+            v8i xf[C::MI];
+            float c0[C::MI], c1[C::MI];
 #pragma unroll
             for (int i = 0; i < C::MI; ++i) {
-                const v4f pr = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf, xf[i], v4f{0.f, 0.f, 0.f, 0.f},
-                                                                               0, 0, 0, 0, 0, 0);
-                const float c = (GATEUP && (j & 1)) ? c1[i] : c0[i];
+                const int r = 16 * i + l16;
+                const uint8_t *rp = sA + r * 128;
+                xf[i] = cat(*reinterpret_cast<const v4i *>(rp + swz8(r, g) * 16),
+                            *reinterpret_cast<const v4i *>(rp + swz8(r, g + 4) * 16));
+                const float sx = sS[r];
+                c0[i] = sx * sb0;
+                c1[i] = sx * sb1;
+            }
 #pragma unroll
-                for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(pr[v], c, acc[i][j][v]);
+            for (int j = 0; j < C::NJ; ++j) {
+                const int vr = 64 * wave + 16 * j + l16;
+                const uint8_t *rp = sW + vr * 128;
+                const v8i wf = cat(*reinterpret_cast<const v4i *>(rp + swz8(vr, g) * 16),
+                                   *reinterpret_cast<const v4i *>(rp + swz8(vr, g + 4) * 16));
+#pragma unroll
+                for (int i = 0; i < C::MI; ++i) {
+                    const v4f pr = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        wf, xf[i], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
+                    const float c = (GATEUP && (j & 1)) ? c1[i] : c0[i];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(pr[v], c, acc[i][j][v]);
+                }
             }
         }
         if (kb == KB - 1 || s == s1 - 1) {            // end of this block's part of the item
@@ -462,17 +575,25 @@ int cu_count()
     return g_cus;
 }
 
-template <int BM, bool GATEUP>
-int launch_stream_one(const GemmArgs &a, int grid, hipStream_t st)
+// Blocks: one per CU, more when a block would hold more than MAXIT items.
+int stream_grid(int64_t items_max, int maxit)
 {
-    using C = SCfg<BM>;
-    auto fn = moe_gemm_stream_kernel<BM, GATEUP>;
+    const int64_t g = cu_count();
+    const int64_t need = (items_max + maxit - 3) / (maxit - 2);   // items per block <= maxit
+    return (int)(g > need ? g : need);
+}
+
+template <int BM, bool GATEUP, bool FP4>
+int launch_stream_one(const GemmArgs &a, int64_t items_max, hipStream_t st)
+{
+    using C = SCfg<BM, FP4>;
+    auto fn = moe_gemm_stream_kernel<BM, GATEUP, FP4>;
     static bool attr_set = false;
     if (!attr_set) {
         XS_HIP(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, C::SMEM));
         attr_set = true;
     }
-    fn<<<dim3((unsigned)grid), dim3(kNT), C::SMEM, st>>>(a);
+    fn<<<dim3((unsigned)stream_grid(items_max, C::MAXIT)), dim3(kNT), C::SMEM, st>>>(a);
     XS_LAUNCH_CHECK();
     return XS_OK;
 }
@@ -481,38 +602,42 @@ int launch_stream_one(const GemmArgs &a, int grid, hipStream_t st)
 
 int stream_blocks() { return cu_count(); }
 
-static int stream_grid(int64_t items_max)
+// (MXFP4 also needs K % 512 == 0 for both GEMMs: the scale pairs of steps
+// must not straddle an item.)
+bool stream_fits(int bm, bool fp4, int64_t tiles_max, int64_t rows_max)
 {
-    int64_t g = cu_count();
-    const int64_t need = (items_max + kMaxItems - 3) / (kMaxItems - 2);   // items per block <= kMaxItems
-    return (int)(g > need ? g : need);
+    const bool bm_ok = fp4 ? (bm == 16 || bm == 32 || bm == 64) : (bm == 16 || bm == 32);
+    return bm_ok && tiles_max < 32768 && rows_max < 65536;   // row tokens are kept as 16-bit in LDS
 }
-
-bool stream_fits(int bm, int64_t tiles_max, int64_t) { return (bm == 16 || bm == 32) && tiles_max < 32768; }
 
 int64_t stream_items(bool gateup, int N, int64_t tiles_max) { return tiles_max * slabs_of(gateup, N); }
 
 size_t stream_part_bytes(int64_t items_max, int, int bm)
 {
     // two partial tiles per block (its first and last item may be split)
-    return (size_t)2 * stream_grid(items_max) * kNT * (bm / 16) * 4 * 16;
+    return (size_t)2 * stream_grid(items_max, 30) * kNT * (bm / 16) * 4 * 16;
 }
 
-int launch_gemm_stream(const GemmArgs &a, bool gateup, int tiles_max, int64_t, hipStream_t st)
+int launch_gemm_stream(const GemmArgs &a, bool gateup, bool fp4, int tiles_max, int64_t rows_max, hipStream_t st)
 {
-    XS_REQUIRE(a.K % 128 == 0 && a.K >= 128 && a.tile_tab && a.offsets && a.part && a.cnt,
+    XS_REQUIRE(a.K % (fp4 ? 512 : 128) == 0 && a.K >= 128 && a.tile_tab && a.offsets && a.part && a.cnt,
                "stream GEMM: bad arguments");
     XS_REQUIRE(a.N % 128 == 0, "shape mismatch: N must be a multiple of 128");
     XS_REQUIRE((int64_t)(gateup ? 2 * a.N : a.N) * a.K < ((int64_t)1 << 32), "expert weights exceed 4 GB");
     if (tiles_max <= 0) return XS_OK;
-    XS_REQUIRE(stream_items(gateup, a.N, tiles_max) * (a.K / 128) < ((int64_t)1 << 31) && tiles_max < 32768,
-               "stream GEMM: too many tiles");
-    const int grid = stream_grid(stream_items(gateup, a.N, tiles_max));
-    switch (a.bm) {
-    case 16: return gateup ? launch_stream_one<16, true>(a, grid, st) : launch_stream_one<16, false>(a, grid, st);
-    case 32: return gateup ? launch_stream_one<32, true>(a, grid, st) : launch_stream_one<32, false>(a, grid, st);
-    default: return set_error(XS_ERR_INVALID, "stream GEMM: unsupported tile rows %d", a.bm);
+    const int64_t items = stream_items(gateup, a.N, tiles_max);
+    XS_REQUIRE(items * (a.K / 128) < ((int64_t)1 << 31) && stream_fits(a.bm, fp4, tiles_max, rows_max),
+               "stream GEMM: launch exceeds the kernel's tables");
+#define XS_S(BMV, FP)                                                                                   \
+    return gateup ? launch_stream_one<BMV, true, FP>(a, items, st) : launch_stream_one<BMV, false, FP>(a, items, st)
+    if (fp4) {
+        if (a.bm == 16) XS_S(16, true);
+        if (a.bm == 32) XS_S(32, true);
+        XS_S(64, true);
     }
+    if (a.bm == 16) XS_S(16, false);
+    XS_S(32, false);
+#undef XS_S
 }
 
 }  // namespace xs
