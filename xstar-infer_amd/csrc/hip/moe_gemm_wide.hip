@@ -14,9 +14,12 @@
 //     slab (gate_up: 128 gate + the matching 128 up rows; down: 256 rows of W2);
 //   * both operand tiles move global -> LDS by DMA (global_load_lds_dwordx4,
 //     8 lanes per 128-byte row, so every load instruction is fully coalesced)
-//     into two rings (activations 2 deep, weights 3 deep: first-touch weight
-//     reads from HBM have the longer latency); 16-byte chunks are
-//     XOR-swizzled per row so the MFMA fragment reads are bank-conflict free;
+//     into two rings: tiles of up to 128 rows keep activations 2 deep and
+//     weights 3 deep (their weights stream from HBM, the longer latency),
+//     taller tiles 3 and 2 (their weights are shared with the expert's other
+//     tiles through L2, and the gathered activation rows wait longest);
+//     16-byte chunks are XOR-swizzled per row so the MFMA fragment reads are
+//     bank-conflict free;
 //   * 8 waves as 2 (tokens) x 4 (weight columns): a wave owns 64 weight rows
 //     (gate_up: 32 gate + the matching 32 up) and the 16-token subtiles of its
 //     parity, so a partially filled tile still splits evenly over both halves;
@@ -39,7 +42,7 @@ constexpr int kNT = 64 * kNW;        // threads
 constexpr int kRing = 148 * 1024;    // LDS bytes of the operand ring
 constexpr int kTrash = 1024;         // LDS target of padding DMAs
 
-template <int BM>
+template <int BM, bool DEEP_A>
 struct WCfg {
     static constexpr int NS16 = BM / 16;                   // 16-token subtiles per tile
     static constexpr int MI = NS16 / 2;                    // per wave row
@@ -47,11 +50,13 @@ struct WCfg {
     static constexpr int W_BYTES = 256 * 128;              // weight rows of one K step
     static constexpr int S_BYTES = BM * 4;                 // activation row scales
     static constexpr int AS_BYTES = A_BYTES + S_BYTES;     // activation ring stage
-    // Two rings: activations (+ row scales) NAR deep, weights NWR deep, so the
-    // LDS left over by whole stages buys one more step of prefetch for one
-    // operand (prefetch distances NAR-1 and NWR-1 steps).
-    static constexpr int NAR = 2;
-    static constexpr int NWR = 3;
+    // Two rings: activations (+ row scales) NAR deep, weights NWR deep (prefetch
+    // distances NAR-1 and NWR-1 steps).  Tiles of more than 128 rows (experts
+    // with several tiles, whose weight slabs the tiles share through L2) wait on
+    // their activation rows: 3 + 2 stages.  Shorter tiles stream their weights
+    // from HBM: 2 + 3 stages.
+    static constexpr int NAR = DEEP_A ? 3 : 2;
+    static constexpr int NWR = DEEP_A ? 2 : 3;
     static constexpr int DA = NAR - 1, DW = NWR - 1;
     static constexpr int NA = BM / 8 / kNW;                // 1 KB activation DMAs per wave and step
     static constexpr int NB = 256 / 8 / kNW;               // 1 KB weight DMAs per wave and step
@@ -99,10 +104,20 @@ __device__ __forceinline__ void wait_vm()
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int BM, bool GATEUP, bool FULL>
+#ifdef XS_WIDE_TRACE
+// Development builds only: per-block phase timestamps (100 MHz wall clock).
+__device__ uint64_t g_wide_trace[2][16384][6];
+#define XS_WTRACE(ev) \
+    if (threadIdx.x == 0 && blockIdx.x + gridDim.x * blockIdx.y < 16384) \
+        g_wide_trace[GATEUP ? 1 : 0][blockIdx.x + gridDim.x * blockIdx.y][ev] = wall_clock64()
+#else
+#define XS_WTRACE(ev)
+#endif
+
+template <int BM, bool GATEUP, bool FULL, bool DEEP_A>
 __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int rows, int slab, uint8_t *smem)
 {
-    using C = WCfg<BM>;
+    using C = WCfg<BM, DEEP_A>;
     const int KB = a.K / 128;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -206,6 +221,7 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
     __syncthreads();   // sB visible
 #pragma unroll
     for (int j = -C::PRO; j < 0; ++j) issue(j);
+    XS_WTRACE(1);
 
     const int sbi = GATEUP ? 0 : (wn >> 1);   // down: the wave's 128-row scale block
     for (int kb = 0; kb < KB; ++kb) {
@@ -270,6 +286,7 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
         }
     }
     wait_vm<0>();      // the clamped DMAs past the last step land before the block ends
+    XS_WTRACE(2);
 
     // ------------------------------------------------------------ epilogue
     // acc[i][j][v]: token row 16 (wm + 2 i) + r16; A-tile j row 4 g + v.
@@ -339,10 +356,19 @@ __global__ __launch_bounds__(kNT) void moe_gemm_wide_kernel(GemmArgs a)
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int4 *tab = reinterpret_cast<const int4 *>(a.tile_tab);   // shared + routed tiles
     if ((int)blockIdx.y >= tab[0].x) return;
+    XS_WTRACE(0);
     const int4 d = tab[1 + blockIdx.y];   // {expert, first position, rows}
     const int slab = (int)blockIdx.x;
-    if (d.z >= BM) run_tile<BM, GATEUP, true>(a, d.x, d.y, BM, slab, smem);
-    else run_tile<BM, GATEUP, false>(a, d.x, d.y, d.z, slab, smem);
+    if (d.z >= BM) run_tile<BM, GATEUP, true, true>(a, d.x, d.y, BM, slab, smem);
+    else if (d.z > 128) run_tile<BM, GATEUP, false, true>(a, d.x, d.y, d.z, slab, smem);
+    else run_tile<BM, GATEUP, false, false>(a, d.x, d.y, d.z, slab, smem);
+    XS_WTRACE(3);
+#ifdef XS_WIDE_TRACE
+    if (threadIdx.x == 0 && blockIdx.x + gridDim.x * blockIdx.y < 16384) {
+        g_wide_trace[GATEUP ? 1 : 0][blockIdx.x + gridDim.x * blockIdx.y][4] = (uint64_t)d.z;
+        g_wide_trace[GATEUP ? 1 : 0][blockIdx.x + gridDim.x * blockIdx.y][5] = (uint64_t)d.x;
+    }
+#endif
 }
 
 template <int BM, bool GATEUP>
@@ -379,3 +405,10 @@ int launch_gemm_wide(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
 }
 
 }  // namespace xs
+
+#ifdef XS_WIDE_TRACE
+extern "C" int xs_wide_trace_read(void *dst)
+{
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(xs::g_wide_trace), sizeof(xs::g_wide_trace)) == hipSuccess ? 0 : 1;
+}
+#endif

@@ -268,6 +268,46 @@ __device__ __forceinline__ Cand wave_best(Cand c)
     return c;
 }
 
+// 64-bit rank of a routing candidate: larger rank = better.  The key's bits
+// are mapped to an unsigned order (-0 is folded into +0 first, as the float
+// comparison treats them equal); the low word is ~expert, so equal keys rank
+// the lower expert index higher.
+__device__ __forceinline__ uint64_t route_rank(float key, int e)
+{
+    const uint32_t u = __builtin_bit_cast(uint32_t, key + 0.0f);
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v)
+{
+    const int lo = __builtin_amdgcn_update_dpp((int)(uint32_t)v, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp((int)(uint32_t)(v >> 32), (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+// Wave-wide maximum (uniform result): DPP within each row of 16 lanes
+// (quad xor 1, quad xor 2, half-row mirror, row mirror), then the four row
+// results through readlane.  No LDS round trips.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
+{
+    uint64_t o;
+    o = dpp_u64<0xB1>(v);  v = o > v ? o : v;    // quad_perm [1,0,3,2]
+    o = dpp_u64<0x4E>(v);  v = o > v ? o : v;    // quad_perm [2,3,0,1]
+    o = dpp_u64<0x141>(v); v = o > v ? o : v;    // row_half_mirror
+    o = dpp_u64<0x140>(v); v = o > v ? o : v;    // row_mirror
+    uint64_t r = 0;
+#pragma unroll
+    for (int row = 0; row < 4; ++row) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * row);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 16 * row);
+        const uint64_t x = ((uint64_t)hi << 32) | lo;
+        r = x > r ? x : r;
+    }
+    return r;
+}
+
 // One wave per token.  Lane l holds experts l + 64*i, i < NV.
 template <int NV>
 __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ logits,
@@ -344,43 +384,39 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ lo
             if (ok[i]) ok[i] = (keep >> (e / gs)) & 1ull;
         }
     }
-    int sel_e[16];
-    float sel_s[16];
+    // top-k: k rounds of a wave arg-max over 64-bit ranks (order-preserving
+    // key bits, then the complement of the expert index: ties go to the lower
+    // index, as in the reference's comparison); empty candidates rank 0
+    uint64_t rk[NV];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        if (j < k) {
-        Cand c;
-        c.e = -1;
-        c.key = 0.0f;
-        c.s = 0.0f;
+    for (int i = 0; i < NV; ++i) rk[i] = ok[i] ? route_rank(key[i], lane + 64 * i) : 0ull;
+    // lane j keeps pick j; the weight denominator is summed in pick order
+    int my_e = -1;
+    float my_s = 0.0f, denom = 0.0f;
+#pragma unroll 1
+    for (int j = 0; j < k; ++j) {
+        uint64_t b = rk[0];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            Cand d;
-            d.e = ok[i] ? lane + 64 * i : -1;
-            d.key = key[i];
-            d.s = s[i];
-            if (better(d, c)) c = d;
-        }
-        c = wave_best(c);
-        sel_e[j] = c.e;
-        sel_s[j] = c.s;
+        for (int i = 1; i < NV; ++i) b = rk[i] > b ? rk[i] : b;
+        b = wave_max_u64(b);
+        const int e = b ? (int)(0xffffffffu - (uint32_t)b) : -1;
+        // the winner's score, from its lane
+        float sv = 0.0f;
 #pragma unroll
         for (int i = 0; i < NV; ++i)
-            if (lane + 64 * i == c.e) ok[i] = false;
-        }
+            if ((e >> 6) == i) sv = s[i];
+        sv = e >= 0 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), e & 63)) : 0.0f;
+        denom = __fadd_rn(denom, sv);
+        if (lane == j) { my_e = e; my_s = sv; }
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            if (lane + 64 * i == e) rk[i] = 0ull;
     }
-    float denom = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-        if (j < k) denom = __fadd_rn(denom, sel_s[j]);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        if (j < k && lane == j) {
-            float wv = renorm ? __fmul_rn(__fdiv_rn(sel_s[j], denom), scaling) : __fmul_rn(sel_s[j], scaling);
-            idx[(size_t)t * k + j] = sel_e[j];
-            wout[(size_t)t * k + j] = wv;
-            if (mask) atomicOr(&mask[(size_t)sel_e[j] * mask_words + (t >> 5)], 1u << (t & 31));
-        }
+    if (lane < k) {
+        const float wv = renorm ? __fmul_rn(__fdiv_rn(my_s, denom), scaling) : __fmul_rn(my_s, scaling);
+        idx[(size_t)t * k + lane] = my_e;
+        wout[(size_t)t * k + lane] = wv;
+        if (mask && my_e >= 0) atomicOr(&mask[(size_t)my_e * mask_words + (t >> 5)], 1u << (t & 31));
     }
 }
 
