@@ -34,6 +34,8 @@
 //     permute builds, so a block starts with one load instead of a search.
 #include "moe_gemm.hpp"
 
+#include <cstdlib>
+
 namespace xs {
 namespace {
 
@@ -355,10 +357,30 @@ __global__ __launch_bounds__(kNT) void moe_gemm_wide_kernel(GemmArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int4 *tab = reinterpret_cast<const int4 *>(a.tile_tab);   // shared + routed tiles
-    if ((int)blockIdx.y >= tab[0].x) return;
+    const int tiles = tab[0].x;
+    int tile, slab;
+    if (a.xcd_order) {
+        // 1-D grid.  Blocks go round-robin to the 8 XCDs (linear id L to XCD
+        // L % 8), each with its own L2.  The work is cut into groups of 8
+        // tiles x 4 slabs (the 32 blocks an XCD runs at once): a group's tiles
+        // share each weight slab and its slabs share each tile's activation
+        // rows inside one L2, which per K step and XCD reads 8 x 24 KB of
+        // activations and 4 x 32 KB of weights (grid order: 16 tiles x 2
+        // slabs, 384 + 64 KB).  XCD x takes groups x, x + 8, ... in order.
+        const int gx = GATEUP ? a.N / 128 : a.N / 256, nq = gx / 4;
+        const int L = (int)blockIdx.x, j = L >> 3;
+        const int sg = (L & 7) + 8 * (j >> 5), i = j & 31;
+        const int g = sg / nq, q = sg - g * nq;
+        tile = 8 * g + (i >> 2);
+        slab = 4 * q + (i & 3);
+        if (tile >= tiles) return;
+    } else {
+        tile = (int)blockIdx.y;
+        slab = (int)blockIdx.x;
+        if (tile >= tiles) return;
+    }
     XS_WTRACE(0);
-    const int4 d = tab[1 + blockIdx.y];   // {expert, first position, rows}
-    const int slab = (int)blockIdx.x;
+    const int4 d = tab[1 + tile];   // {expert, first position, rows}
     if (d.z >= BM) run_tile<BM, GATEUP, true, true>(a, d.x, d.y, BM, slab, smem);
     else if (d.z > 128) run_tile<BM, GATEUP, false, true>(a, d.x, d.y, d.z, slab, smem);
     else run_tile<BM, GATEUP, false, false>(a, d.x, d.y, d.z, slab, smem);
@@ -384,7 +406,12 @@ int launch_wide(const GemmArgs &a, int grid_y, hipStream_t st)
         attr_set = true;
     }
     const int grid_x = GATEUP ? a.N / 128 : a.N / 256;
-    fn<<<dim3((unsigned)grid_x, (unsigned)grid_y), dim3(kNT), smem, st>>>(a);
+    if (a.xcd_order) {
+        const int64_t groups = (grid_y + 7) / 8 * (grid_x / 4);      // 8-tile x 4-slab groups
+        fn<<<dim3((unsigned)((groups + 7) / 8 * 256)), dim3(kNT), smem, st>>>(a);
+    } else {
+        fn<<<dim3((unsigned)grid_x, (unsigned)grid_y), dim3(kNT), smem, st>>>(a);
+    }
     XS_LAUNCH_CHECK();
     return XS_OK;
 }
@@ -401,7 +428,11 @@ int launch_gemm_wide(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
     if (a.bm != wide_tile_rows()) return set_error(XS_ERR_INVALID, "wide GEMM needs %d-row tiles", wide_tile_rows());
     if (a.K % 128 || (gateup ? a.N % 128 : a.N % 256) || !a.tile_tab)
         return set_error(XS_ERR_UNSUPPORTED, "wide GEMM shape K=%d N=%d", a.K, a.N);
-    return gateup ? launch_wide<kWideBM, true>(a, grid_y, st) : launch_wide<kWideBM, false>(a, grid_y, st);
+    GemmArgs b = a;
+    const char *ord = getenv("XS_WIDE_ORDER");
+    // XS_WIDE_ORDER=0: one block per (slab, tile) in grid order (measurements)
+    b.xcd_order = !(ord && ord[0] == '0') && (gateup ? a.N / 128 : a.N / 256) % 4 == 0;
+    return gateup ? launch_wide<kWideBM, true>(b, grid_y, st) : launch_wide<kWideBM, false>(b, grid_y, st);
 }
 
 }  // namespace xs
