@@ -310,7 +310,14 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
             m = fmaxf(m, __shfl_xor(m, 32, WAVE));
             if (g == 0) red[wn * BM + 16 * (wm + 2 * i) + r16] = m;
         }
-        __syncthreads();
+        __syncthreads();   // every wave is past its loop: the ring is free for staging
+        // The FP8 tile is staged in the ring (rows padded to 144 B: a wave's
+        // 16-row x 4-lane writes hit 64 distinct banks) and stored as whole
+        // 128-byte rows; an instruction that scatters 4 bytes over 16 rows
+        // moves about a quarter of the bytes per clock of a row-contiguous one.
+        constexpr int QS = 144;
+        static_assert(BM * QS <= kRing, "staging tile");
+        uint8_t *qs = smem;
         float *Cs = reinterpret_cast<float *>(a.Cs);
         const int nsc = a.N / 128;
 #pragma unroll
@@ -320,34 +327,50 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
 #pragma unroll
             for (int w = 0; w < 4; ++w) amax = fmaxf(amax, red[w * BM + row]);
             const float inv = amax == 0.f ? 0.f : __fdiv_rn(448.0f, amax);
-            if (row < rows) {
-                const size_t pos = (size_t)(pos0 + row);
 #pragma unroll
-                for (int jj = 0; jj < 2; ++jj) {
-                    float x[4];
+            for (int jj = 0; jj < 2; ++jj) {
+                float x[4];
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) x[v] = fminf(fmaxf(act[i][jj][v] * inv, -448.f), 448.f);
-                    *reinterpret_cast<uint32_t *>(a.Cq + pos * a.N + n0 + 32 * wn + 16 * jj + 4 * g) =
-                        e4m3_pack2_hw(x[0], x[1]) | (e4m3_pack2_hw(x[2], x[3]) << 16);
-                }
-                if (wn == 0 && g == 0) Cs[pos * nsc + n0 / 128] = amax == 0.f ? 1.0f : __fdiv_rn(amax, 448.0f);
+                for (int v = 0; v < 4; ++v) x[v] = fminf(fmaxf(act[i][jj][v] * inv, -448.f), 448.f);
+                *reinterpret_cast<uint32_t *>(qs + row * QS + 32 * wn + 16 * jj + 4 * g) =
+                    e4m3_pack2_hw(x[0], x[1]) | (e4m3_pack2_hw(x[2], x[3]) << 16);
             }
+            if (wn == 0 && g == 0 && row < rows) Cs[(size_t)(pos0 + row) * nsc + n0 / 128] = amax == 0.f ? 1.0f : __fdiv_rn(amax, 448.0f);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int pass = 0; pass < BM / 64; ++pass) {
+            const int row = 64 * pass + (tid >> 3), c = tid & 7;
+            if (row < rows)
+                *reinterpret_cast<v4i *>(a.Cq + (size_t)(pos0 + row) * a.N + n0 + 16 * c) =
+                    *reinterpret_cast<const v4i *>(qs + row * QS + 16 * c);
         }
     } else {
-        // output column n0 + 64 wn + 16 j + 4 g + v
+        // output column n0 + 64 wn + 16 j + 4 g + v.  The bf16 tile is staged in
+        // the ring (rows padded to 528 B: a half-wave's 16-row x 2-lane 8-byte
+        // writes hit distinct banks) and stored as whole 512-byte rows.
+        constexpr int YS = 528;
+        static_assert(BM * YS <= kRing, "staging tile");
+        uint8_t *ys = smem;
+        __syncthreads();   // every wave is past its loop: the ring is free for staging
 #pragma unroll
         for (int i = 0; i < C::MI; ++i) {
             const int row = 16 * (wm + 2 * i) + r16;
-            if (row < rows) {
-                uint16_t *dst = a.Cy + (size_t)(pos0 + row) * a.ldc + n0 + 64 * wn + 4 * g;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    v2i pk;
-                    pk[0] = (int)((uint32_t)bf16_from_f32(acc[i][j][0]) | ((uint32_t)bf16_from_f32(acc[i][j][1]) << 16));
-                    pk[1] = (int)((uint32_t)bf16_from_f32(acc[i][j][2]) | ((uint32_t)bf16_from_f32(acc[i][j][3]) << 16));
-                    *reinterpret_cast<v2i *>(dst + 16 * j) = pk;
-                }
+            for (int j = 0; j < 4; ++j) {
+                v2i pk;
+                pk[0] = (int)((uint32_t)bf16_from_f32(acc[i][j][0]) | ((uint32_t)bf16_from_f32(acc[i][j][1]) << 16));
+                pk[1] = (int)((uint32_t)bf16_from_f32(acc[i][j][2]) | ((uint32_t)bf16_from_f32(acc[i][j][3]) << 16));
+                *reinterpret_cast<v2i *>(ys + row * YS + 2 * (64 * wn + 16 * j + 4 * g)) = pk;
             }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int pass = 0; pass < BM / 16; ++pass) {
+            const int row = 16 * pass + (tid >> 5), c = tid & 31;
+            if (row < rows)
+                *reinterpret_cast<v4i *>(a.Cy + (size_t)(pos0 + row) * a.ldc + n0 + 8 * c) =
+                    *reinterpret_cast<const v4i *>(ys + row * YS + 16 * c);
         }
     }
 }
