@@ -134,6 +134,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="prefill only, no extra configs")
     ap.add_argument("--sections", default="prefill,decode,gemm,fp4",
                     help="comma list of prefill,decode,gemm,fp4 (the JSON line needs prefill)")
+    ap.add_argument("--decode-tokens", default="1,16,64,256",
+                    help="comma list of decode batch sizes (configs[3])")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=8)
     a = ap.parse_args()
@@ -231,7 +233,7 @@ def decode(a, X, torch):
     from moe_synth import synth_layer, layer_from, expert_bytes
     dec = {}
     gd = synth_layer(256, H, I, E, K_TOP, seed=1, bias_std=0.0)
-    for Td in (1, 16, 64, 256):
+    for Td in (int(t) for t in a.decode_tokens.split(",")):
         L = layer_from(gd)
         xd = gd["x"][:Td].contiguous()
         msd, st = time_forward(L, xd, max(a.steps, 50), a.warmup, profile=True)

@@ -33,6 +33,8 @@
 //     single-tile experts stream their weights with the non-temporal hint).
 #include "moe_gemm.hpp"
 
+#include <cstdlib>
+
 namespace xs {
 namespace {
 
@@ -168,24 +170,55 @@ __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
     else if (a.e_hi <= a.E) lo = h.y;     // routed experts only
     const int gx = slabs_of(GATEUP, a.N);
     const int W = (hi - lo) * gx * KB;
-    const int G = W < (int)gridDim.x ? W : (int)gridDim.x, b = blockIdx.x;
-    if (b >= G) return;
-    const int s0 = (int)((int64_t)b * W / G), s1 = (int)((int64_t)(b + 1) * W / G);
-    const int it0 = s0 / KB, it1 = (s1 - 1) / KB;
+    const int G = W < (int)gridDim.x ? W : (int)gridDim.x;
+    // Grouped partition (set by the host for MXFP4): whole items only.  Logical
+    // block b = 16 g + s (gx = 16 slabs) takes slab s of the tile run
+    // [g ntl / NG, (g+1) ntl / NG), and the gx blocks of a group sit on one XCD
+    // (blocks go round-robin to the 8 XCDs; logical neighbours are 8 block ids
+    // apart), so at any moment the group's CUs read one tile's activation rows
+    // together through their L2 instead of each re-reading them from memory,
+    // item after item, behind the weight stream.
+    const int ntl = hi - lo, NG = G / gx;
+    const bool grouped = a.xcd_order && G == (int)gridDim.x && (G & 7) == 0 && ((G >> 3) % gx) == 0 &&
+                         ntl >= NG && (ntl + NG - 1) / NG <= C::MAXIT;
+    int b = (int)blockIdx.x, s0, s1, it0, it1, gsl = 0, gt0 = 0;
+    if (grouped) {
+        b = ((int)blockIdx.x & 7) * (G >> 3) + ((int)blockIdx.x >> 3);
+        const int grp = b / gx;
+        gsl = b - grp * gx;
+        gt0 = (int)((int64_t)grp * ntl / NG);
+        const int n = (int)((int64_t)(grp + 1) * ntl / NG) - gt0;   // >= 1 (ntl >= NG)
+        it0 = gt0 * gx + gsl * n;
+        it1 = it0 + n - 1;
+        s0 = it0 * KB;
+        s1 = (it1 + 1) * KB;
+    } else {
+        if (b >= G) return;
+        s0 = (int)((int64_t)b * W / G);
+        s1 = (int)((int64_t)(b + 1) * W / G);
+        it0 = s0 / KB;
+        it1 = (s1 - 1) / KB;
+    }
     const int nit = it1 - it0 + 1;   // <= MAXIT (grid sized by the host)
 
     // ---- item descriptors: {expert, first position, rows, slab | multi-tile << 30} ----
     // Items run expert by expert, then slab, then tile (tab .w: tile index in
-    // the expert's group | tiles in the group << 16).
+    // the expert's group | tiles in the group << 16); grouped: this block's
+    // tile run at slab gsl.
     if (tid < nit) {
-        const int it = it0 + tid;
-        const int tm = lo + it / gx;                 // a tile of the item's expert group
-        const int4 d = tab[1 + tm];
-        const int t = d.w & 0xffff, nt = d.w >> 16, t0 = tm - t;
-        const int local = it - (t0 - lo) * gx;
-        const int slab = local / nt, tile = t0 + local % nt;
-        const int4 dd = tile == tm ? d : tab[1 + tile];
-        meta[tid] = int4{d.x, dd.y, min(dd.z, BM), slab | (nt > 1 ? (1 << 30) : 0)};
+        if (grouped) {
+            const int4 d = tab[1 + lo + gt0 + tid];
+            meta[tid] = int4{d.x, d.y, min(d.z, BM), gsl | ((d.w >> 16) > 1 ? (1 << 30) : 0)};
+        } else {
+            const int it = it0 + tid;
+            const int tm = lo + it / gx;                 // a tile of the item's expert group
+            const int4 d = tab[1 + tm];
+            const int t = d.w & 0xffff, nt = d.w >> 16, t0 = tm - t;
+            const int local = it - (t0 - lo) * gx;
+            const int slab = local / nt, tile = t0 + local % nt;
+            const int4 dd = tile == tm ? d : tab[1 + tile];
+            meta[tid] = int4{d.x, dd.y, min(dd.z, BM), slab | (nt > 1 ? (1 << 30) : 0)};
+        }
     }
     __syncthreads();
     for (int q = tid; q < nit * BM; q += kNT) {
@@ -628,8 +661,11 @@ int launch_gemm_stream(const GemmArgs &a, bool gateup, bool fp4, int tiles_max, 
     const int64_t items = stream_items(gateup, a.N, tiles_max);
     XS_REQUIRE(items * (a.K / 128) < ((int64_t)1 << 31) && stream_fits(a.bm, fp4, tiles_max, rows_max),
                "stream GEMM: launch exceeds the kernel's tables");
+    GemmArgs b = a;
+    const char *grp = getenv("XS_STREAM_GROUPED");   // 0: stream-K partition for MXFP4 too (measurements)
+    b.xcd_order = fp4 && !(grp && grp[0] == '0');
 #define XS_S(BMV, FP)                                                                                   \
-    return gateup ? launch_stream_one<BMV, true, FP>(a, items, st) : launch_stream_one<BMV, false, FP>(a, items, st)
+    return gateup ? launch_stream_one<BMV, true, FP>(b, items, st) : launch_stream_one<BMV, false, FP>(b, items, st)
     if (fp4) {
         if (a.bm == 16) XS_S(16, true);
         if (a.bm == 32) XS_S(32, true);
