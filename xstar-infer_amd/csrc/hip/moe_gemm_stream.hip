@@ -171,7 +171,8 @@ __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
     const int gx = slabs_of(GATEUP, a.N);
     const int W = (hi - lo) * gx * KB;
     const int G = W < (int)gridDim.x ? W : (int)gridDim.x;
-    // Grouped partition (set by the host for MXFP4): whole items only.  Logical
+    // Grouped partition (the default; stream-K below when the tiles do not
+    // fill the groups or a block would hold more than MAXIT items): whole items only.  Logical
     // block b = 16 g + s (gx = 16 slabs) takes slab s of the tile run
     // [g ntl / NG, (g+1) ntl / NG), and the gx blocks of a group sit on one XCD
     // (blocks go round-robin to the 8 XCDs; logical neighbours are 8 block ids
@@ -662,8 +663,8 @@ int launch_gemm_stream(const GemmArgs &a, bool gateup, bool fp4, int tiles_max, 
     XS_REQUIRE(items * (a.K / 128) < ((int64_t)1 << 31) && stream_fits(a.bm, fp4, tiles_max, rows_max),
                "stream GEMM: launch exceeds the kernel's tables");
     GemmArgs b = a;
-    const char *grp = getenv("XS_STREAM_GROUPED");   // 0: stream-K partition for MXFP4 too (measurements)
-    b.xcd_order = fp4 && !(grp && grp[0] == '0');
+    const char *grp = getenv("XS_STREAM_GROUPED");   // 0: stream-K partition (measurements)
+    b.xcd_order = !(grp && grp[0] == '0');
 #define XS_S(BMV, FP)                                                                                   \
     return gateup ? launch_stream_one<BMV, true, FP>(b, items, st) : launch_stream_one<BMV, false, FP>(b, items, st)
     if (fp4) {
