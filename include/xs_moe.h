@@ -181,7 +181,8 @@ size_t xs_moe_workspace_size(const xs_moe_params *p);
 
 /* Router -> top-k -> permute (+ activation quant) -> grouped gate_up GEMM with
  * SwiGLU and FP8 re-quant -> grouped down GEMM -> weighted combine (+ shared).
- * Stream-ordered, no host synchronisation inside. */
+ * Stream-ordered, no host synchronisation inside.  T = 0 returns XS_OK after
+ * validating the params; its tensor pointers may then be null. */
 int xs_moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *workspace,
                    size_t workspace_bytes, void *stream);
 

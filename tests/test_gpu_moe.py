@@ -167,3 +167,51 @@ def test_moe_prefill_full_size_properties():
     assert max_abs_rel(got, r["out_f32"]) <= TOL
     # sum of the routed weights per token is 1 (renormalised)
     assert np.allclose(d["topk_w"].sum(1), 1.0, rtol=1e-5)
+
+
+def _golden_mlp_case(E, k, shared):
+    """The reference's own mlp() test vectors (tests/golden/ref_vectors.npz,
+    written by the compiled reference) as an MoE layer: every routed expert and
+    the shared expert carry the same FP8-quantized [gate; up] and down weights,
+    and a zero router ties every expert (top-k takes the lowest indices with
+    renormalised weights 1/k)."""
+    import os
+    r = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz"))
+    x, w13, w2 = r["mlp_x"], r["mlp_w13"], r["mlp_w2"]
+    T, H = x.shape
+    I = w2.shape[1]
+    q13, s13 = oracle.quant_weight_fp8_block(w13[None])
+    q2, s2 = oracle.quant_weight_fp8_block(w2[None])
+    c = dict(T=T, H=H, I=I, E=E, k=k, bias=None, x=x, router_w=np.zeros((E, H), np.float32),
+             w13=np.repeat(q13, E, 0), s13=np.repeat(s13, E, 0), w2=np.repeat(q2, E, 0),
+             s2=np.repeat(s2, E, 0), fp4=False,
+             shared=(q13[0], s13[0], q2[0], s2[0]) if shared else None)
+    return c
+
+
+def test_moe_reduces_to_reference_mlp_closed_forms():
+    """E = 1, top-1, no shared expert: the layer is mlp(x) (checked against the
+    oracle, which test_oracle pins to the reference mlp() golden).  E = 4
+    identical experts, top-2, plus the same shared expert: the combine sums
+    y + y/2 + y/2 of bit-identical expert rows, which is exactly 2 y in f32 and
+    in the output cast, so the output is twice the E = 1 output bit for bit."""
+    c1 = _golden_mlp_case(1, 1, False)
+    g1 = to_device(c1)
+    _run_and_check(c1, g1, router_exact=True)
+    y1 = layer_for(c1, g1, router_exact=True).forward(g1["x"]).cpu().numpy()
+    c4 = _golden_mlp_case(4, 2, True)
+    g4 = to_device(c4)
+    _run_and_check(c4, g4, router_exact=True)
+    y4 = layer_for(c4, g4, router_exact=True).forward(g4["x"]).cpu().numpy()
+    assert np.array_equal(y4, 2 * y1)
+
+
+def test_moe_empty_input():
+    """T = 0: the layer returns an empty output and launches nothing."""
+    c = make_case(4, 256, 128, 8, 2, seed=5)
+    g = to_device(c)
+    layer = layer_for(c, g)
+    x0 = g["x"][:0]
+    out = layer.forward(x0)
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (0, 256)

@@ -153,6 +153,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
 {
     int rc = check_params(p);
     if (rc) return rc;
+    if (p->T == 0) return XS_OK;   // empty input: nothing is read or written (its tensors may be null)
     XS_REQUIRE(t && t->x && t->router_w && t->w13 && t->w13_scale && t->w2 && t->w2_scale && t->out,
                "null pointer");
     XS_REQUIRE(!p->has_shared || (t->shared_w13 && t->shared_w13_scale && t->shared_w2 && t->shared_w2_scale),
