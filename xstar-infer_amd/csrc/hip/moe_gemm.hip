@@ -72,10 +72,12 @@ __device__ __forceinline__ uint32_t lds_off(const void *p)
 // The LDS base goes through M0 and must be wave-uniform.
 // M0 is written only inside these statements; compiled kernels here use M0 for
 // nothing else.
+// Wait state inside the asm (the compiler's hazard checks do not look into an
+// asm string): an LDS DMA that reads M0 needs one after the SALU write of M0.
 __device__ __forceinline__ void dma16(const void *g, uint32_t lds)
 {
     const uint32_t s = __builtin_amdgcn_readfirstlane(lds);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(s) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(s) : "memory");
 }
 // The same with the non-temporal hint: weights streamed once (decode tiles)
 // should not displace reused lines, and the hint raises HBM streaming
@@ -84,12 +86,12 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds)
 __device__ __forceinline__ void dma16_nt(const void *g, uint32_t lds)
 {
     const uint32_t s = __builtin_amdgcn_readfirstlane(lds);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "s"(s) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "s"(s) : "memory");
 }
 __device__ __forceinline__ void dma4(const void *g, uint32_t lds)
 {
     const uint32_t s = __builtin_amdgcn_readfirstlane(lds);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(s) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(s) : "memory");
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt()

@@ -87,18 +87,23 @@ __device__ __forceinline__ v8i cat(v4i a, v4i b) { return v8i{a[0], a[1], a[2], 
 // Wave-wide DMA global -> LDS: lane i's 16 (4) bytes, read from sbase + voff,
 // land at lds + 16 i (4 i).  M0 carries the wave-uniform LDS base; it is
 // written only here.
+// Wait states inside the asm (the compiler's hazard checks do not look into
+// an asm string): an LDS DMA that reads M0 needs one after the SALU write of
+// M0, and a VMEM instruction reading an SGPR that a VALU instruction wrote
+// (v_readfirstlane of the base) needs five, hence s_nop 4 where the base is a
+// scalar operand and s_nop 0 where the address is a VGPR.
 __device__ __forceinline__ void dma16(const uint8_t *sbase, uint32_t voff, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 // Non-temporal variant for weights read by a single tile (streamed once).
 __device__ __forceinline__ void dma16_nt(const uint8_t *sbase, uint32_t voff, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4(const uint8_t *sbase, uint32_t voff, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 template <int N>
 __device__ __forceinline__ void wait_vm()

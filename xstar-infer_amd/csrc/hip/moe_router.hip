@@ -144,9 +144,11 @@ __device__ __forceinline__ uint32_t rt_lds(const void *p)
 }
 // Wave-wide DMA global -> LDS: lane i's 16 bytes land at lds + 16 i.  M0 carries
 // the wave-uniform LDS base; it is written only here.
+// Wait state inside the asm (the compiler's hazard checks do not look into an
+// asm string): an LDS DMA that reads M0 needs one after the SALU write of M0.
 __device__ __forceinline__ void rt_dma16(const void *g, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
                  : "memory");
 }
 template <int N>
