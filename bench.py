@@ -132,8 +132,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="prefill only, no extra configs")
-    ap.add_argument("--sections", default="prefill,decode,gemm,fp4",
-                    help="comma list of prefill,decode,gemm,fp4 (the JSON line needs prefill)")
+    ap.add_argument("--sections", default="prefill,decode,gemm,fp4,norm",
+                    help="comma list of prefill,decode,gemm,fp4,norm (the JSON line needs prefill)")
     ap.add_argument("--decode-tokens", default="1,16,64,256",
                     help="comma list of decode batch sizes (configs[3])")
     ap.add_argument("--no-cpu", action="store_true")
@@ -163,6 +163,8 @@ def main():
         res["gemm_fp8_512x4096x4096"] = single_gemm(a, X, torch)
     if "fp4" in sections:
         res["fp4_2048"] = fp4_layer(a, X, torch)
+    if "norm" in sections:
+        res["rmsnorm_8192x7168"] = norm_legs(a, X, torch)
     print(json.dumps(res))
     return 0
 
@@ -284,6 +286,66 @@ def fp4_layer(a, X, torch):
             "hbm_gbs_weights": by4 / (ms4 * 1e-3) / 1e9, "stage_ms": st4}
 
 
+
+def norm_legs(a, X, torch):
+    """RMSNorm at the prefill activation shape (8192 x 7168 bf16): alone, fused
+    with the FP8 1x128 quant of its output, the separate quant for comparison,
+    and the MoE layer with the pre-norm against the layer without it."""
+    from moe_synth import synth_layer, layer_from
+    T = 8192
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    x = torch.randn((T, H), generator=gen, device="cuda").to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(H, generator=gen, device="cuda")).to(torch.bfloat16)
+    y = torch.empty_like(x)
+    q = torch.empty((T, H), dtype=torch.uint8, device="cuda")
+    s = torch.empty((T, H // 128), dtype=torch.float32, device="cuda")
+    st = X._stream()
+    L = X.lib()
+
+    def norm(quant):
+        X.check(L.xs_rmsnorm(X._ptr(x), X._ptr(w), X.XS_BF16, T, H, 1e-6, X._ptr(y),
+                             X._ptr(q) if quant else None, X._ptr(s) if quant else None, st))
+
+    def quant_only():
+        X.check(L.xs_quant_act_fp8(X._ptr(y), X.XS_BF16, T, H, X._ptr(q), X._ptr(s), st))
+
+    def timed(fn, n=50):
+        for _ in range(a.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    out = {}
+    b_norm = 2 * T * H * 2 + 2 * H
+    b_fused = b_norm + T * H + 4 * T * (H // 128)
+    b_quant = 2 * T * H + T * H + 4 * T * (H // 128)
+    for name, fn, by in (("rmsnorm", lambda: norm(False), b_norm), ("rmsnorm_fp8", lambda: norm(True), b_fused),
+                         ("quant_act_fp8", quant_only, b_quant)):
+        ms = timed(fn)
+        out[name] = {"ms": ms, "bytes": by, "gbs": by / (ms * 1e-3) / 1e9,
+                     "frac_hbm_peak": by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+    del x, y, q, s
+    # the MoE layer with and without the pre-norm (prefill and a decode batch)
+    g = synth_layer(T, H, I, E, K_TOP, seed=0, zipf=1.1)
+    for Tn in (T, 16):
+        xn = g["x"][:Tn].contiguous()
+        base = layer_from(g)
+        ms0, _ = time_forward(base, xn, a.steps, a.warmup)
+        del base
+        pre = layer_from(g, norm_weight=w, norm_eps=1e-6)
+        ms1, st1 = time_forward(pre, xn, a.steps, a.warmup, profile=True)
+        del pre
+        out[f"moe_T{Tn}"] = {"ms_without_norm": ms0, "ms_with_prenorm": ms1, "act_quant_stage_ms": st1["act_quant"]}
+    del g
+    torch.cuda.empty_cache()
+    return out
 
 
 if __name__ == "__main__":

@@ -108,6 +108,20 @@ int xs_quant_act_fp8(const void *x, int dtype, int64_t rows, int64_t cols, uint8
 int xs_quant_act_mxfp8(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q,
                        uint8_t *s, void *stream);
 
+/* RMSNorm, optionally fused with the FP8 1x128 activation quantization of its
+ * output.  Replaces rmsnorm(x, weight, eps) (xstar_cpp/include/ops/rmsnorm.h,
+ * xstar_cpp/src/ops/rmsnorm.cpp:6-81; device launcher rmsnorm_launch,
+ * xstar_cpp/src/ops/rmsnorm.cu:57-81) and, with q/s, the rmsnorm -> activation
+ * quant pair ahead of the MoE layer (xstar_cpp/src/ops/transformer_block.cpp:353).
+ * x, y [rows, hidden] and weight [hidden] of `dtype` (XS_F32 or XS_BF16).
+ * y = x * inv * weight with inv = 1 / sqrt(mean(x^2) + eps) in f32 (correctly
+ * rounded sqrt and divisions); bf16 rounds x * inv to bf16 before the weight
+ * multiply, as the reference CPU path does (rmsnorm.cpp:72).  q [rows, hidden]
+ * e4m3 and s [rows, hidden/128] f32 (both NULL, or both set with
+ * hidden % 128 == 0) receive xs_quant_act_fp8(y). */
+int xs_rmsnorm(const void *x, const void *weight, int dtype, int64_t rows, int64_t hidden, float eps,
+               void *y, uint8_t *q, float *s, void *stream);
+
 /* Weight quantization for loading dense checkpoints (no reference counterpart;
  * the reference loads F32/BF16 only, xstar_cpp/src/weight_io.cpp:122-127).
  * FP8 128x128 blocks: w [batch, n, k] -> q [batch, n, k], s [batch, n/128, k/128] f32,
@@ -149,6 +163,8 @@ typedef struct {
     int routed_format;    /* XS_FP8_E4M3 (128x128 f32 scales) or XS_FP4_E2M1X2 (MXFP4) */
     int has_shared;       /* 1: shared expert weights present (FP8 128x128) */
     int router_exact;     /* 1: bit-exact sequential f32 router logits */
+    int has_norm;         /* 1: RMSNorm x with norm_weight first (the block's pre-norm) */
+    float norm_eps;       /* RMSNorm epsilon when has_norm */
 } xs_moe_params;
 
 typedef struct {
@@ -174,13 +190,19 @@ typedef struct {
     int32_t *offsets;          /* [E+1] */
     int32_t *perm;             /* [T*k] */
     int32_t *inv;              /* [T*k] */
+    /* RMSNorm weight [H] x_dtype when has_norm (else ignored) */
+    const void *norm_weight;
 } xs_moe_tensors;
 
 /* Device workspace the forward needs for these params (bytes, 256-aligned). */
 size_t xs_moe_workspace_size(const xs_moe_params *p);
 
-/* Router -> top-k -> permute (+ activation quant) -> grouped gate_up GEMM with
- * SwiGLU and FP8 re-quant -> grouped down GEMM -> weighted combine (+ shared).
+/* [RMSNorm] + activation quant -> router -> top-k -> permute -> grouped gate_up
+ * GEMM with SwiGLU and FP8 re-quant -> grouped down GEMM -> weighted combine
+ * (+ shared).  With has_norm the layer computes moe(rmsnorm(x, norm_weight,
+ * norm_eps)) (xstar_cpp/src/ops/transformer_block.cpp:353 with the MoE in place
+ * of mlp()): one kernel writes the normalized rows the router reads and their
+ * FP8 quantization the expert GEMMs read (xs_rmsnorm semantics).
  * Stream-ordered, no host synchronisation inside.  T = 0 returns XS_OK after
  * validating the params; its tensor pointers may then be null. */
 int xs_moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *workspace,
@@ -190,8 +212,8 @@ int xs_moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *worksp
  * Per-stage timing hook (no reference counterpart; the reference times ops with
  * torch.cuda.Event around whole calls, bench/bench_splitkv.py:86-105).  While
  * enabled, xs_moe_forward records a HIP event at each stage boundary on its
- * stream (router logits, route, activation quant, permute, gate_up GEMM, down
- * GEMM, combine).  xs_moe_profile_read waits for the recorded forwards, writes
+ * stream (activation quant with the optional RMSNorm, router logits, route,
+ * permute, gate_up GEMM, down GEMM, combine).  xs_moe_profile_read waits for the recorded forwards, writes
  * the summed milliseconds of up to 7 stages and the number of forwards, and
  * clears the record.  Process-wide state: not for concurrent callers.
  * ------------------------------------------------------------------------- */

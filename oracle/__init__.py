@@ -60,6 +60,7 @@ def lib():
         L.xo_quant_weight_fp8_block.argtypes = [P, I64, I64, P, P]
         L.xo_quant_weight_mxfp4.argtypes = [P, I64, I64, P, P]
         L.xo_router_logits.argtypes = [P, P, C.c_int, I64, I64, I64, P]
+        L.xo_rmsnorm.argtypes = [P, P, C.c_int, I64, I64, C.c_float, P]
         L.xo_route.argtypes = [P, P, I64, I64, I64, I64, I64, C.c_int, C.c_float, P, P]
         L.xo_permute.argtypes = [P, I64, I64, I64, P, P, P, P]
         L.xo_moe_forward.argtypes = [P, P, P]
@@ -127,6 +128,21 @@ def quant_act_fp8(x: np.ndarray):
     s = np.empty((rows, cols // 128), np.float32)
     lib().xo_quant_act_fp8(_p(x), rows, cols, _p(q), _p(s))
     return q, s
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float, bf16: bool = False) -> np.ndarray:
+    """RMSNorm over the last axis (xo_rmsnorm; rmsnorm.cpp:27-73).  bf16=True:
+    x and w are bf16 bit patterns (uint16) and so is the result; else f32."""
+    dt = np.uint16 if bf16 else np.float32
+    x = np.ascontiguousarray(x, dtype=dt)
+    w = np.ascontiguousarray(w, dtype=dt)
+    hidden = x.shape[-1]
+    assert w.shape == (hidden,)
+    rows = x.size // hidden if hidden else 0
+    y = np.empty_like(x)
+    if rows:
+        lib().xo_rmsnorm(_p(x), _p(w), int(bf16), rows, hidden, float(eps), _p(y))
+    return y
 
 
 def quant_act_mxfp8(x: np.ndarray):

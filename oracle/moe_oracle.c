@@ -237,6 +237,30 @@ static inline float ld(const void *p, int is_bf16, int64_t i)
     return is_bf16 ? xo_f32_from_bf16(((const uint16_t *)p)[i]) : ((const float *)p)[i];
 }
 
+/* ------------------------------------------------------------------ RMSNorm */
+
+/* xstar_cpp/src/ops/rmsnorm.cpp:29-50 (f32) and :52-75 (bf16). */
+void xo_rmsnorm(const void *x, const void *w, int is_bf16, int64_t rows, int64_t hidden, float eps, void *y)
+{
+    for (int64_t r = 0; r < rows; ++r) {
+        float sum = 0.0f;
+        for (int64_t j = 0; j < hidden; ++j) {
+            float v = ld(x, is_bf16, r * hidden + j);
+            sum += v * v;
+        }
+        float inv = 1.0f / sqrtf(sum / (float)hidden + eps);
+        for (int64_t j = 0; j < hidden; ++j) {
+            float v = ld(x, is_bf16, r * hidden + j), g = ld(w, is_bf16, j);
+            if (is_bf16) {
+                float n = xo_f32_from_bf16(xo_bf16_from_f32(v * inv));
+                ((uint16_t *)y)[r * hidden + j] = xo_bf16_from_f32(n * g);
+            } else {
+                ((float *)y)[r * hidden + j] = v * inv * g;
+            }
+        }
+    }
+}
+
 /* gemm.h:57-83 (transB = true): for each row i, temp[j] += s * B[kk + j*ldb]
  * over kk ascending -- per output a sequential k-sum of separately rounded
  * products.  Evaluated here as a contiguous dot product per (i, j): same

@@ -62,6 +62,15 @@ void xo_quant_weight_fp8_block(const float *w, int64_t n, int64_t k, uint8_t *q,
  * s [n, k/32] e8m0 bytes. */
 void xo_quant_weight_mxfp4(const float *w, int64_t n, int64_t k, uint8_t *q, uint8_t *s);
 
+/* ---------------- RMSNorm ---------------- */
+/* y = x * inv_rms * w per row of `hidden` values, following the reference CPU
+ * path xstar_cpp/src/ops/rmsnorm.cpp:27-73: sum of squares in f32 over the row
+ * in order (product rounded, then sum rounded), inv_rms = 1 / sqrt(sum/hidden + eps)
+ * with IEEE sqrt and division; f32: y = (x * inv_rms) * w; bf16:
+ * y = bf16(f32(bf16(x * inv_rms)) * w).  x, w, y are f32 (is_bf16 = 0) or bf16
+ * bits (is_bf16 = 1). */
+void xo_rmsnorm(const void *x, const void *w, int is_bf16, int64_t rows, int64_t hidden, float eps, void *y);
+
 /* ---------------- router ---------------- */
 /* logits[t, e] = sum_kk x[t,kk] * Wr[e,kk] in gemm_cpu order (sequential kk,
  * separate multiply then add, f32).  x/Wr are f32 (is_bf16 = 0) or bf16 bits

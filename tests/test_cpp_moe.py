@@ -120,3 +120,32 @@ def test_cpp_moe_matches_capi_and_oracle():
     assert np.array_equal(cpp_to_torch(xstar_cpp.to_cpu(idx), (40, 4)).numpy(), r["idx"])
     counts, offsets, perm, inv = xstar_cpp.moe_permute(idx, 16)
     assert np.array_equal(cpp_to_torch(xstar_cpp.to_cpu(perm), (160,)).numpy(), r["perm"])
+
+
+# ------------------------------------------------------------------ rmsnorm
+def test_rmsnorm_validation_messages():
+    """Checks and messages of xstar_cpp/src/ops/rmsnorm.cpp:9-16, raised before
+    any device work; CPU tensors are an unsupported device (no CPU compute)."""
+    x = torch_to_cpp(torch.randn(4, 32))
+    w = torch_to_cpp(torch.randn(32))
+    wb = torch_to_cpp(torch.randn(32).to(torch.bfloat16))
+    with pytest.raises(RuntimeError, match="x and weight must have the same dtype"):
+        xstar_cpp.rmsnorm(x, wb, 1e-5)
+    with pytest.raises(RuntimeError, match="rank >= 1 and weight 1D"):
+        xstar_cpp.rmsnorm(x, torch_to_cpp(torch.randn(2, 16)), 1e-5)
+    with pytest.raises(RuntimeError, match="shape mismatch"):
+        xstar_cpp.rmsnorm(x, torch_to_cpp(torch.randn(31)), 1e-5)
+    with pytest.raises(RuntimeError, match="unsupported device"):
+        xstar_cpp.rmsnorm(x, w, 1e-5)
+    with pytest.raises(RuntimeError, match="shape mismatch"):
+        xstar_cpp.rmsnorm_quant_fp8(torch_to_cpp(torch.randn(4, 96)), torch_to_cpp(torch.randn(96)), 1e-5)
+
+
+def test_moe_norm_weight_validation():
+    x, wr, (w13, s13, w2, s2) = _weights()
+    with pytest.raises(RuntimeError, match="dtype mismatch"):
+        xstar_cpp.moe(torch_to_cpp(x), torch_to_cpp(wr), None, w13, s13, w2, s2, top_k=2,
+                      norm_weight=torch_to_cpp(torch.ones(256)))
+    with pytest.raises(RuntimeError, match="shape mismatch"):
+        xstar_cpp.moe(torch_to_cpp(x), torch_to_cpp(wr), None, w13, s13, w2, s2, top_k=2,
+                      norm_weight=torch_to_cpp(torch.ones(128).to(torch.bfloat16)))

@@ -27,6 +27,7 @@ def _bf16_dev(a_u16):
 def _cases_act(rng):
     x = rng.standard_normal((37, 512)).astype(np.float32)
     x[3, :128] = 0.0                       # all-zero group
+    x[4, 384:] = -0.0                      # all-zero group of negative zeros (FP8: code 0)
     x[5, 128:256] *= 1e4                   # large
     x[6, 256:384] *= 1e-30                 # tiny (subnormal after scaling)
     x[7, 0] = 3.0e38                       # near f32 max

@@ -375,3 +375,92 @@ def test_quant_path_fp4_vs_torch():
             ref[t] += float(r["w"][t, j]) * (a2 @ d2[e].T).numpy()[0]
     err = np.abs(r["out_f32"] - ref).max() / np.abs(ref).max()
     assert err < 2e-3, err
+
+
+# ------------------------------------------------------------------ RMSNorm
+def _torch_rmsnorm_layer(x, w, eps, ieee=True):
+    """The reference's Python layer (xstar/layers/rmsnorm.py:44-58): f32
+    statistics, normalise in f32, cast back, multiply by the weight in the
+    input dtype.  ieee=True writes its rsqrt as 1 / sqrt, the form of the C++
+    CPU path (rmsnorm.cpp:44,67)."""
+    import torch
+    xf = x.to(torch.float32)
+    ms = xf.pow(2).mean(-1, keepdim=True) + eps
+    rms = 1.0 / torch.sqrt(ms) if ieee else torch.rsqrt(ms)
+    return w * (xf * rms).to(x.dtype)
+
+
+def _bits(t):
+    import torch
+    return t.view(torch.int16).numpy().view(np.uint16) if t.dtype == torch.bfloat16 else t.numpy()
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("shape,eps", [((4, 32), 1e-5), ((3, 1024), 1e-6), ((5, 2048), 1e-5), ((2, 1), 1e-5)])
+def test_rmsnorm_bitexact_on_exact_sums(bf16, shape, eps):
+    """x on a 1/8 grid in [-1, 1]: every square and partial sum is exact in f32,
+    so torch's reduction order cannot matter and the reference layer's steps
+    (mean, + eps, sqrt, divide, normalise, cast, weight) give the oracle's bits.
+    Pins eps inside the sqrt, the division by hidden, (x * inv) * w in f32 and
+    the two bf16 roundings."""
+    import torch
+    g = torch.Generator().manual_seed(shape[-1])
+    dt = torch.bfloat16 if bf16 else torch.float32
+    x = (torch.randint(-8, 9, shape, generator=g).float() / 8).to(dt)
+    w = torch.randn(shape[-1], generator=g).to(dt)
+    ref = _torch_rmsnorm_layer(x, w, eps)
+    got = oracle.rmsnorm(_bits(x), _bits(w), eps, bf16=bf16)
+    assert np.array_equal(got, _bits(ref))
+
+
+def test_rmsnorm_bf16_double_rounding_is_visible():
+    """The bf16 path rounds x * inv to bf16 before the weight multiply
+    (rmsnorm.cpp:72).  Find inputs where one rounding of x * inv * w gives
+    another bf16 value and check the oracle keeps the two roundings."""
+    import torch
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randint(-8, 9, (64, 32), generator=g).float() / 8).to(torch.bfloat16)
+    w = torch.randn(32, generator=g).to(torch.bfloat16)
+    xf = x.float()
+    inv = 1.0 / torch.sqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5)
+    single = (xf * inv * w.float()).to(torch.bfloat16)
+    double = _torch_rmsnorm_layer(x, w, 1e-5)
+    assert not torch.equal(single, double)
+    got = oracle.rmsnorm(_bits(x), _bits(w), 1e-5, bf16=True)
+    assert np.array_equal(got, _bits(double))
+
+
+@pytest.mark.parametrize("bf16,shape,rtol,atol", [(False, (4, 32), 0, 1e-6), (False, (16,), 0, 1e-6),
+                                                  (False, (4, 1024), 0, 1e-4), (True, (4, 32), 0, 1e-2),
+                                                  (True, (8, 7168), 1e-2, 1e-2)])
+def test_rmsnorm_vs_reference_layer(bf16, shape, rtol, atol):
+    """randn inputs against the reference layer as written (torch.rsqrt), to the
+    tolerances of tests/ops/test_cpp_rmsnorm.py:30,51,140 and
+    tests/ops/test_cpp_cuda_rmsnorm.py:111-116."""
+    import torch
+    g = torch.Generator().manual_seed(11)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    x = torch.randn(shape, generator=g).to(dt)
+    w = torch.randn(shape[-1], generator=g).to(dt)
+    ref = _torch_rmsnorm_layer(x, w, 1e-5, ieee=False).float().numpy()
+    got = oracle.rmsnorm(_bits(x), _bits(w), 1e-5, bf16=bf16)
+    got = oracle.f32_from_bf16(got) if bf16 else got
+    assert np.allclose(got, ref, rtol=rtol, atol=atol)
+
+
+def test_rmsnorm_closed_forms():
+    """Zero rows give exact zeros (eps keeps them finite,
+    tests/ops/test_cpp_rmsnorm.py:76-95); hidden = 1 gives x / sqrt(x^2 + eps) * w;
+    a constant row c gives c / sqrt(c^2 + eps) * w."""
+    z = oracle.rmsnorm(np.zeros((4, 32), np.float32), np.ones(32, np.float32), 1e-5)
+    assert np.array_equal(z, np.zeros((4, 32), np.float32))
+    x = np.array([[3.0], [-0.5], [1e-3], [0.0]], np.float32)
+    w = np.array([1.5], np.float32)
+    h1 = oracle.rmsnorm(x, w, 1e-5)
+    ref = x.astype(np.float64) / np.sqrt(x.astype(np.float64) ** 2 + np.float64(np.float32(1e-5))) * 1.5
+    assert np.allclose(h1, ref, rtol=3e-7, atol=0)
+    c = np.full((1, 256), 0.75, np.float32)
+    wc = np.linspace(-2, 2, 256, dtype=np.float32)
+    yc = oracle.rmsnorm(c, wc, 1e-6)
+    ref = 0.75 / math.sqrt(0.5625 + float(np.float32(1e-6))) * wc.astype(np.float64)
+    assert np.allclose(yc[0], ref, rtol=3e-7, atol=1e-12)

@@ -15,7 +15,7 @@ namespace xs {
 static size_t al(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // ---- optional per-stage timing (xs_moe_profile_*) ----
-// Stage boundaries: 0 logits | 1 route | 2 act quant | 3 permute | 4 gate_up |
+// Stage boundaries: 0 act quant (+ RMSNorm) | 1 logits | 2 route | 3 permute | 4 gate_up |
 // 5 down | 6 combine | 7 end.  One set of 8 events per forward, up to kProfMax
 // forwards between two reads.
 static constexpr int kStages = 7, kProfMax = 512;
@@ -39,7 +39,7 @@ static int prof_mark(int stage, hipStream_t st)
 
 struct WsLayout {
     size_t logits, idx, w, mask, wordprefix, counts, offsets, perm, inv, row_token, tiles, tiletab, part, cnt1, cnt2;
-    size_t xq, xs, xmq, xms, actq, acts, actms, y;
+    size_t xn, xq, xs, xmq, xms, actq, acts, actms, y;
     size_t total;
 };
 
@@ -112,6 +112,7 @@ static WsLayout layout(const xs_moe_params *p)
         take(L.cnt1, st ? 4 * (size_t)(n1 + 1) : 0);
         take(L.cnt2, st ? 4 * (size_t)(n2 + 1) : 0);
     }
+    take(L.xn, p->has_norm ? T * H * (p->x_dtype == XS_BF16 ? 2 : 4) : 0);
     take(L.xq, T * H);
     take(L.xs, 4 * T * (H / 128));
     take(L.xmq, fp4 ? T * H : 0);
@@ -136,6 +137,7 @@ static int check_params(const xs_moe_params *p)
     XS_REQUIRE(p->routed_format == XS_FP8_E4M3 || p->routed_format == XS_FP4_E2M1X2,
                "unsupported routed expert format");
     XS_REQUIRE(p->T * p->top_k + p->T < ((int64_t)1 << 31), "too many rows");
+    XS_REQUIRE(p->has_norm == 0 || p->has_norm == 1, "has_norm must be 0 or 1");
     XS_REQUIRE(p->routed_format != XS_FP4_E2M1X2 || p->I % 256 == 0,
                "shape mismatch: MXFP4 experts need I to be a multiple of 256");
     if (p->n_group > 1) {
@@ -156,6 +158,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     if (p->T == 0) return XS_OK;   // empty input: nothing is read or written (its tensors may be null)
     XS_REQUIRE(t && t->x && t->router_w && t->w13 && t->w13_scale && t->w2 && t->w2_scale && t->out,
                "null pointer");
+    XS_REQUIRE(!p->has_norm || t->norm_weight, "null norm weight");
     XS_REQUIRE(!p->has_shared || (t->shared_w13 && t->shared_w13_scale && t->shared_w2 && t->shared_w2_scale),
                "null shared expert pointer");
     const WsLayout L = layout(p);
@@ -178,26 +181,35 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     int32_t *tiles = WS(int32_t, tiles);
     const int Wd = mask_words_for(T);
 
-    // 1. router: logits -> top-k + per-expert token masks
+    // 1. activation quantization (once per token, gathered by the GEMMs),
+    //    with the optional RMSNorm fused in front of it
     if ((rc = prof_mark(0, st))) return rc;
-    const int nsplit = router_logits_splits(T, H, p->router_exact, p->x_dtype);
-    rc = launch_router_logits(t->x, t->router_w, p->x_dtype, T, E, H, p->router_exact, logits, nsplit, st, mask,
-                              (int64_t)Wd * E);
-    if (rc) return rc;
-    if ((rc = prof_mark(1, st))) return rc;
-    rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
-                      p->routed_scaling, idx, w, mask, Wd, nsplit, t->logits, st);
-    if (rc) return rc;
-    // 2. activation quantization (once per token, gathered by the GEMMs)
-    if ((rc = prof_mark(2, st))) return rc;
-    if (!fp4 || p->has_shared) {
-        rc = launch_quant_act(t->x, p->x_dtype, T, H, WS(uint8_t, xq), WS(float, xs), 0, st);
+    const void *xin = t->x;
+    const bool fp8_act = !fp4 || p->has_shared;
+    if (p->has_norm) {
+        void *xn = WS(void, xn);
+        rc = launch_rmsnorm(t->x, t->norm_weight, p->x_dtype, T, H, p->norm_eps, xn,
+                            fp8_act ? WS(uint8_t, xq) : nullptr, fp8_act ? WS(float, xs) : nullptr, st);
+        if (rc) return rc;
+        xin = xn;
+    } else if (fp8_act) {
+        rc = launch_quant_act(xin, p->x_dtype, T, H, WS(uint8_t, xq), WS(float, xs), 0, st);
         if (rc) return rc;
     }
     if (fp4) {
-        rc = launch_quant_act(t->x, p->x_dtype, T, H, WS(uint8_t, xmq), WS(uint8_t, xms), 1, st);
+        rc = launch_quant_act(xin, p->x_dtype, T, H, WS(uint8_t, xmq), WS(uint8_t, xms), 1, st);
         if (rc) return rc;
     }
+    // 2. router: logits -> top-k + per-expert token masks
+    if ((rc = prof_mark(1, st))) return rc;
+    const int nsplit = router_logits_splits(T, H, p->router_exact, p->x_dtype);
+    rc = launch_router_logits(xin, t->router_w, p->x_dtype, T, E, H, p->router_exact, logits, nsplit, st, mask,
+                              (int64_t)Wd * E);
+    if (rc) return rc;
+    if ((rc = prof_mark(2, st))) return rc;
+    rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
+                      p->routed_scaling, idx, w, mask, Wd, nsplit, t->logits, st);
+    if (rc) return rc;
     // 3. permute: (expert, token)-sorted positions, tile offsets
     if ((rc = prof_mark(3, st))) return rc;
     const bool wide = use_wide(p);

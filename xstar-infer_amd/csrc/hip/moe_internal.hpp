@@ -44,6 +44,30 @@ __device__ __forceinline__ void store8(float *p, const float *v)
     *reinterpret_cast<v4f *>(p + 4) = v4f{v[4], v[5], v[6], v[7]};
 }
 
+// FP8 1x128 activation quant of 8 consecutive values held by one lane; the
+// 16 lanes of an aligned 16-lane group hold one 128-column group.  amax over
+// the group, inv = 448/amax, q = e4m3_rne(v * inv) (amax == 0: q = 0, scale 1),
+// scale = amax/448 written through `s` by the group's first lane (s != null).
+__device__ __forceinline__ void quant8_fp8(const float *v, uint8_t *__restrict__ q, float *__restrict__ s)
+{
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, WAVE));
+    float inv = amax == 0.0f ? 0.0f : __fdiv_rn(448.0f, amax);
+    // |v * inv| <= 448 (1 + 2^-22): clamped to the e4m3 range, the hardware
+    // RNE converter gives the software encoder's codes (pinned by the GPU tests)
+    float r[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = fminf(fmaxf(__fmul_rn(v[i], inv), -448.0f), 448.0f);
+    uint32_t lo = e4m3_pack2_hw(r[0], r[1]) | (e4m3_pack2_hw(r[2], r[3]) << 16);
+    uint32_t hi = e4m3_pack2_hw(r[4], r[5]) | (e4m3_pack2_hw(r[6], r[7]) << 16);
+    if (amax == 0.0f) lo = hi = 0u;   // an all-zero group is code 0, also where its values are -0
+    *reinterpret_cast<v2i *>(q) = v2i{(int)lo, (int)hi};
+    if (s) *s = amax == 0.0f ? 1.0f : __fdiv_rn(amax, 448.0f);
+}
+
 // ---- launchers (stream-ordered, no synchronisation) ----
 // Number of K slices the bf16 MFMA router uses for T tokens (1 = no split).
 int router_logits_splits(int64_t T, int64_t H, int exact, int dtype);
@@ -60,6 +84,11 @@ int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, i
                  hipStream_t st);
 int launch_quant_act(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, void *s,
                      int mx, hipStream_t st);
+
+// RMSNorm of rows x [rows, hidden] -> y (same dtype); with q/s non-null also the
+// FP8 1x128 quantization of y (hidden % 128 == 0).
+int launch_rmsnorm(const void *x, const void *w, int dtype, int64_t rows, int64_t hidden, float eps, void *y,
+                   uint8_t *q, float *s, hipStream_t st);
 
 // Permute.  Inputs: idx [T, k] and the per-expert token bitmasks built by the
 // route kernel (mask [E+?][mask_words]).  Outputs positions sorted by

@@ -500,21 +500,7 @@ __device__ __forceinline__ void quant_chunk_fp8(const T *__restrict__ xr, int co
 {
     float v[8];
     load8(xr + c8 * 8, v);
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, WAVE));
-    float inv = amax == 0.0f ? 0.0f : __fdiv_rn(448.0f, amax);
-    // |v * inv| <= 448 (1 + 2^-22): clamped to the e4m3 range, the hardware
-    // RNE converter gives the software encoder's codes (pinned by the GPU tests)
-    float q[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) q[i] = fminf(fmaxf(__fmul_rn(v[i], inv), -448.0f), 448.0f);
-    const uint32_t lo = e4m3_pack2_hw(q[0], q[1]) | (e4m3_pack2_hw(q[2], q[3]) << 16);
-    const uint32_t hi = e4m3_pack2_hw(q[4], q[5]) | (e4m3_pack2_hw(q[6], q[7]) << 16);
-    *reinterpret_cast<v2i *>(qr + c8 * 8) = v2i{(int)lo, (int)hi};
-    if ((c8 & 15) == 0) sr[c8 / 16] = amax == 0.0f ? 1.0f : __fdiv_rn(amax, 448.0f);
+    quant8_fp8(v, qr + c8 * 8, (c8 & 15) == 0 ? sr + c8 / 16 : nullptr);
 }
 
 // Each thread owns 8 consecutive columns (rows are whole multiples of 16

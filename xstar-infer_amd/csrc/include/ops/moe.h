@@ -21,6 +21,9 @@
  *                    or [E, H, I/2] Float4E2M1x2 with w2_scale [E, H, I/32] Float8E8M0
  *   shared_*         one FP8 expert (2-D shapes of the above) or all nullptr
  *   top_k, n_group, topk_group, renormalize, routed_scaling: routing options
+ *   norm_weight      [H] dtype of x, or nullptr: the layer computes
+ *                    moe(rmsnorm(x, norm_weight, norm_eps)) with the norm fused
+ *                    into the activation quantization (ops/rmsnorm.h numerics)
  *   returns          [..., H], dtype of x, device CUDA
  *
  * Numerics: routing bit-exact with the CPU restatement given the logits;
@@ -38,7 +41,8 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
            const Tensor *shared_w13, const Tensor *shared_w13_scale,
            const Tensor *shared_w2, const Tensor *shared_w2_scale,
            std::int64_t top_k, std::int64_t n_group = 1, std::int64_t topk_group = 1,
-           bool renormalize = true, float routed_scaling = 1.0f, bool router_exact = false);
+           bool renormalize = true, float routed_scaling = 1.0f, bool router_exact = false,
+           const Tensor *norm_weight = nullptr, float norm_eps = 1e-6f);
 
 /** Router logits x . router_w^T in f32 ([T, E]); exact: bit-identical to
  * gemm_cpu's sequential accumulation (xstar_cpp/include/ops/gemm.h:57-83). */

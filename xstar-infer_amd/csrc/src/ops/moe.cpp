@@ -33,12 +33,14 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
            const Tensor *shared_w13, const Tensor *shared_w13_scale,
            const Tensor *shared_w2, const Tensor *shared_w2_scale,
            std::int64_t top_k, std::int64_t n_group, std::int64_t topk_group,
-           bool renormalize, float routed_scaling, bool router_exact)
+           bool renormalize, float routed_scaling, bool router_exact,
+           const Tensor *norm_weight, float norm_eps)
 {
     // ---- dtype ----
     if (!is_act(x.dtype())) throw std::runtime_error("unsupported dtype");
     if (router_w.dtype() != x.dtype()) throw std::runtime_error("dtype mismatch");
     if (router_bias && router_bias->dtype() != DType::Float32) throw std::runtime_error("dtype mismatch");
+    if (norm_weight && norm_weight->dtype() != x.dtype()) throw std::runtime_error("dtype mismatch");
     const bool fp4 = w13.dtype() == DType::Float4E2M1x2;
     const DType wq = fp4 ? DType::Float4E2M1x2 : DType::Float8E4M3;
     const DType ws = fp4 ? DType::Float8E8M0 : DType::Float32;
@@ -55,7 +57,7 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
     // ---- rank ----
     if (x.shape().size() < 1 || router_w.shape().size() != 2 || w13.shape().size() != 3 ||
         w2.shape().size() != 3 || w13_scale.shape().size() != 3 || w2_scale.shape().size() != 3 ||
-        (router_bias && router_bias->shape().size() != 1))
+        (router_bias && router_bias->shape().size() != 1) || (norm_weight && norm_weight->shape().size() != 1))
         throw std::runtime_error("rank mismatch");
     if (has_shared && (shared_w13->shape().size() != 2 || shared_w2->shape().size() != 2 ||
                        shared_w13_scale->shape().size() != 2 || shared_w2_scale->shape().size() != 2))
@@ -69,7 +71,8 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
         return s == std::vector<std::int64_t>(v);
     };
     bool ok = router_w.shape()[1] == H && eq(w13.shape(), {E, 2 * I, hk}) && eq(w2.shape(), {E, H, fp4 ? I / 2 : I}) &&
-              (!router_bias || router_bias->shape()[0] == E) && H % 256 == 0 && I % 128 == 0;
+              (!router_bias || router_bias->shape()[0] == E) && (!norm_weight || norm_weight->shape()[0] == H) &&
+              H % 256 == 0 && I % 128 == 0;
     if (ok) {
         if (fp4) ok = eq(w13_scale.shape(), {E, 2 * I, H / 32}) && eq(w2_scale.shape(), {E, H, I / 32});
         else ok = eq(w13_scale.shape(), {E, 2 * I / 128, H / 128}) && eq(w2_scale.shape(), {E, H / 128, I / 128});
@@ -81,6 +84,7 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
     // ---- device ----
     for (const Tensor *t : {&router_w, &w13, &w13_scale, &w2, &w2_scale}) same_device(x, *t);
     if (router_bias) same_device(x, *router_bias);
+    if (norm_weight) same_device(x, *norm_weight);
     if (has_shared)
         for (const Tensor *t : {shared_w13, shared_w13_scale, shared_w2, shared_w2_scale}) same_device(x, *t);
     require_cuda(x);
@@ -100,6 +104,8 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
     p.routed_format = fp4 ? XS_FP4_E2M1X2 : XS_FP8_E4M3;
     p.has_shared = has_shared ? 1 : 0;
     p.router_exact = router_exact ? 1 : 0;
+    p.has_norm = norm_weight ? 1 : 0;
+    p.norm_eps = norm_eps;
     std::size_t wsb = xs_moe_workspace_size(&p);
     if (wsb == 0) throw std::runtime_error("shape mismatch");
     Tensor wsp({static_cast<std::int64_t>(wsb)}, DType::UInt8, Device::CUDA);
@@ -118,6 +124,7 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
         t.shared_w2_scale = static_cast<const float *>(shared_w2_scale->data());
     }
     t.out = out.data();
+    t.norm_weight = norm_weight ? norm_weight->data() : nullptr;
     xs_check(xs_moe_forward(&p, &t, wsp.data(), wsb, nullptr));
     sync();
     return out;

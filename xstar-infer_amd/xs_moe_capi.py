@@ -24,14 +24,15 @@ class MoeParams(C.Structure):
     _fields_ = [("T", I64), ("H", I64), ("I", I64), ("E", I64), ("top_k", I64),
                 ("n_group", I64), ("topk_group", I64), ("renormalize", C.c_int),
                 ("routed_scaling", C.c_float), ("x_dtype", C.c_int), ("routed_format", C.c_int),
-                ("has_shared", C.c_int), ("router_exact", C.c_int)]
+                ("has_shared", C.c_int), ("router_exact", C.c_int),
+                ("has_norm", C.c_int), ("norm_eps", C.c_float)]
 
 
 class MoeTensors(C.Structure):
     _fields_ = [(n, P) for n in (
         "x", "router_w", "router_bias", "w13", "w13_scale", "w2", "w2_scale",
         "shared_w13", "shared_w13_scale", "shared_w2", "shared_w2_scale", "out",
-        "logits", "topk_idx", "topk_w", "counts", "offsets", "perm", "inv")]
+        "logits", "topk_idx", "topk_w", "counts", "offsets", "perm", "inv", "norm_weight")]
 
 
 EXPORTS = {
@@ -50,6 +51,7 @@ EXPORTS = {
     "xs_moe_permute": (C.c_int, [P, I64, I64, I64, P, P, P, P, P, C.c_size_t, P]),
     "xs_quant_act_fp8": (C.c_int, [P, C.c_int, I64, I64, P, P, P]),
     "xs_quant_act_mxfp8": (C.c_int, [P, C.c_int, I64, I64, P, P, P]),
+    "xs_rmsnorm": (C.c_int, [P, P, C.c_int, I64, I64, C.c_float, P, P, P, P]),
     "xs_quant_weight_fp8_block": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P]),
     "xs_quant_weight_mxfp4": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P]),
     "xs_gemm_fp8_blockscale_workspace_size": (C.c_size_t, [I64, I64]),
@@ -60,7 +62,7 @@ EXPORTS = {
     "xs_moe_profile_read": (C.c_int, [P, C.c_int, P]),
 }
 
-STAGES = ("router_logits", "route", "act_quant", "permute", "gemm_gate_up", "gemm_down", "combine")
+STAGES = ("act_quant", "router_logits", "route", "permute", "gemm_gate_up", "gemm_down", "combine")
 
 
 def profile_enable(on=True):
@@ -178,6 +180,22 @@ def quant_act_mxfp8(x):
     return q, s
 
 
+def rmsnorm(x, weight, eps, quant=False):
+    """RMSNorm over the last axis -> y (dtype of x); quant=True also returns the
+    FP8 1x128 quantization of y as (y, q uint8, s f32 [rows, H/128])."""
+    import torch
+    hidden = x.shape[-1]
+    rows = x.numel() // hidden if hidden else 0
+    y = torch.empty_like(x)
+    q = s = None
+    if quant:
+        q = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+        s = torch.empty((*x.shape[:-1], hidden // 128), dtype=torch.float32, device=x.device)
+    check(lib().xs_rmsnorm(_ptr(x), _ptr(weight), _dtype_code(x), rows, hidden, float(eps), _ptr(y),
+                           _ptr(q), _ptr(s), _stream()))
+    return (y, q, s) if quant else y
+
+
 def quant_weight_fp8_block(w):
     """w [..., n, k] (bf16/f32, CUDA) -> (q uint8 [..., n, k], s f32 [..., n/128, k/128])."""
     import torch
@@ -222,8 +240,10 @@ class MoeLayer:
 
     def __init__(self, router_w, w13, w13_scale, w2, w2_scale, top_k, router_bias=None,
                  shared=None, routed_format=XS_FP8_E4M3, n_group=1, topk_group=1,
-                 renormalize=True, routed_scaling=1.0, router_exact=False):
+                 renormalize=True, routed_scaling=1.0, router_exact=False, norm_weight=None,
+                 norm_eps=1e-6):
         self.router_w, self.router_bias = router_w, router_bias
+        self.norm_weight, self.norm_eps = norm_weight, norm_eps
         self.w13, self.w13_scale, self.w2, self.w2_scale = _u8(w13), w13_scale, _u8(w2), w2_scale
         self.shared = None if shared is None else (_u8(shared[0]), shared[1], _u8(shared[2]), shared[3])
         self.top_k, self.routed_format = top_k, routed_format
@@ -236,7 +256,8 @@ class MoeLayer:
     def params(self, T, x_dtype):
         return MoeParams(T, self.H, self.I, self.E, self.top_k, self.n_group, self.topk_group,
                          int(self.renormalize), float(self.routed_scaling), x_dtype,
-                         self.routed_format, int(self.shared is not None), int(self.router_exact))
+                         self.routed_format, int(self.shared is not None), int(self.router_exact),
+                         int(self.norm_weight is not None), float(self.norm_eps))
 
     def workspace(self, T, x_dtype, device):
         import torch
@@ -264,6 +285,7 @@ class MoeLayer:
                        _ptr(self.w13_scale), _ptr(self.w2), _ptr(self.w2_scale), _ptr(sh[0]),
                        _ptr(sh[1]), _ptr(sh[2]), _ptr(sh[3]), _ptr(out),
                        *[_ptr(d.get(n)) for n in ("logits", "topk_idx", "topk_w", "counts",
-                                                 "offsets", "perm", "inv")])
+                                                 "offsets", "perm", "inv")],
+                       _ptr(self.norm_weight))
         check(lib().xs_moe_forward(C.byref(p), C.byref(t), _ptr(ws), ws.numel(), _stream()))
         return out
