@@ -10,6 +10,7 @@ from __future__ import annotations
 import argparse
 import glob
 import os
+import re
 import subprocess
 import sys
 import sysconfig
@@ -38,13 +39,36 @@ def _run(cmd):
     subprocess.run(cmd, check=True)
 
 
+def _scratch_users(remarks: str):
+    """Kernels whose resource-usage remarks report scratch (register spills)."""
+    bad, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            bad.append((name, int(m.group(1))))
+    return bad
+
+
 def build_hip() -> str:
     os.makedirs(OUT, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(HERE, "csrc", "hip", "*.hip")))
     out = os.path.join(OUT, "libxs_moe.so")
     tmp = out + ".tmp"
-    _run([HIPCC, *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc", "hip"),
-          *srcs, "-o", tmp, "-Wl,-soname,libxs_moe.so"])
+    cmd = [HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-I", os.path.join(ROOT, "include"),
+           "-I", os.path.join(HERE, "csrc", "hip"), *srcs, "-o", tmp, "-Wl,-soname,libxs_moe.so"]
+    print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if r.returncode != 0:
+        print("\n".join(l for l in r.stdout.splitlines() if "remark:" not in l), flush=True)
+        raise subprocess.CalledProcessError(r.returncode, cmd)
+    # every kernel keeps its state in registers: a spill to scratch fails the build
+    bad = _scratch_users(r.stdout)
+    if bad:
+        os.remove(tmp)
+        raise RuntimeError("kernels spill to scratch: " + ", ".join(f"{n} ({b} B/lane)" for n, b in bad))
     os.replace(tmp, out)
     return out
 
