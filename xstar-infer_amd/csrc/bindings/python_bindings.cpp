@@ -12,7 +12,9 @@
 #include <vector>
 
 #include "ops/moe.h"
+#include "ops/moe_weights.h"
 #include "ops/rmsnorm.h"
+#include "weight_io.h"
 #include "tensor.h"
 
 namespace py = pybind11;
@@ -82,6 +84,16 @@ py::tuple pair_py(Tensor &t)
     return py::make_tuple(std::move(std::get<0>(r)), std::move(std::get<1>(r)));
 }
 
+// An optional tensor member as a Python attribute: the Tensor (kept alive by
+// its owner) or None.
+template <std::optional<Tensor> MoeLayerWeights::*F>
+py::object opt_member(py::object self)
+{
+    auto &w = self.cast<MoeLayerWeights &>();
+    if (!(w.*F)) return py::none();
+    return py::cast(&*(w.*F), py::return_value_policy::reference_internal, self);
+}
+
 PYBIND11_MODULE(xstar_cpp, m)
 {
     m.doc() = "Xstar MoE operator on MI355X (gfx950): Tensor runtime + MoE ops";
@@ -120,6 +132,34 @@ PYBIND11_MODULE(xstar_cpp, m)
           py::arg("router_exact") = false, py::arg("norm_weight") = py::none(), py::arg("norm_eps") = 1e-6f);
     m.def("rmsnorm", &rmsnorm, py::arg("x"), py::arg("weight"), py::arg("eps"));
     m.def("rmsnorm_quant_fp8", &rmsnorm_quant_fp8_py, py::arg("x"), py::arg("weight"), py::arg("eps"));
+    // safetensors reading (the reference's names and signatures, bindings/python_bindings.cpp:412-424,519-522)
+    py::class_<MMapFile>(m, "MMapFile")
+        .def(py::init<const std::string &>(), py::arg("path"))
+        .def("addr", [](const MMapFile &f) { return reinterpret_cast<std::uintptr_t>(f.addr()); })
+        .def("size", &MMapFile::size);
+    py::class_<TensorMeta>(m, "TensorMeta")
+        .def_readonly("offset", &TensorMeta::offset)
+        .def_readonly("shape", &TensorMeta::shape)
+        .def_readonly("dtype", &TensorMeta::dtype);
+    m.def("make_weight_view", &make_weight_view, py::arg("mf"), py::arg("offset"), py::arg("shape"), py::arg("dtype"),
+          py::keep_alive<0, 1>());
+    m.def("parse_safetensors_header", &parse_safetensors_header, py::arg("mf"));
+    py::class_<MoeLayerWeights>(m, "MoeLayerWeights")
+        .def_readonly("E", &MoeLayerWeights::E)
+        .def_readonly("H", &MoeLayerWeights::H)
+        .def_readonly("I", &MoeLayerWeights::I)
+        .def_property_readonly("router_w", &opt_member<&MoeLayerWeights::router_w>)
+        .def_property_readonly("router_bias", &opt_member<&MoeLayerWeights::router_bias>)
+        .def_property_readonly("w13", &opt_member<&MoeLayerWeights::w13>)
+        .def_property_readonly("w13_scale", &opt_member<&MoeLayerWeights::w13_scale>)
+        .def_property_readonly("w2", &opt_member<&MoeLayerWeights::w2>)
+        .def_property_readonly("w2_scale", &opt_member<&MoeLayerWeights::w2_scale>)
+        .def_property_readonly("shared_w13", &opt_member<&MoeLayerWeights::shared_w13>)
+        .def_property_readonly("shared_w13_scale", &opt_member<&MoeLayerWeights::shared_w13_scale>)
+        .def_property_readonly("shared_w2", &opt_member<&MoeLayerWeights::shared_w2>)
+        .def_property_readonly("shared_w2_scale", &opt_member<&MoeLayerWeights::shared_w2_scale>);
+    m.def("load_moe_layer", &load_moe_layer, py::arg("paths"), py::arg("prefix"), py::arg("device") = Device::CUDA);
+
     m.def("moe_router_logits", &moe_router_logits, py::arg("x"), py::arg("router_w"), py::arg("exact") = false);
     m.def("moe_route", &moe_route_py, py::arg("logits"), py::arg("bias"), py::arg("top_k"),
           py::arg("n_group") = 1, py::arg("topk_group") = 1, py::arg("renormalize") = true,
