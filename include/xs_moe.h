@@ -192,6 +192,10 @@ typedef struct {
     int32_t *inv;              /* [T*k] */
     /* RMSNorm weight [H] x_dtype when has_norm (else ignored) */
     const void *norm_weight;
+    /* optional [T, H] x_dtype added to the output before its one rounding
+     * (the block's residual, xstar_cpp/src/ops/transformer_block.cpp:75,353:
+     * add(h, mlp(rmsnorm(h)))); may equal out (in place); NULL = none */
+    const void *residual;
 } xs_moe_tensors;
 
 /* Device workspace the forward needs for these params (bytes, 256-aligned). */
@@ -202,7 +206,9 @@ size_t xs_moe_workspace_size(const xs_moe_params *p);
  * (+ shared).  With has_norm the layer computes moe(rmsnorm(x, norm_weight,
  * norm_eps)) (xstar_cpp/src/ops/transformer_block.cpp:353 with the MoE in place
  * of mlp()): one kernel writes the normalized rows the router reads and their
- * FP8 quantization the expert GEMMs read (xs_rmsnorm semantics).
+ * FP8 quantization the expert GEMMs read (xs_rmsnorm semantics).  With a
+ * residual the combine adds it in f32 before the one cast, so has_norm plus
+ * residual = x computes the block's whole FFN half, x + moe(rmsnorm(x)).
  * Stream-ordered, no host synchronisation inside.  T = 0 returns XS_OK after
  * validating the params; its tensor pointers may then be null. */
 int xs_moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *workspace,

@@ -196,3 +196,83 @@ def test_moe_prenorm_equals_norm_then_moe(T, fp4, shared):
     assert np.abs(cn["x"].astype(np.int32) - rn.astype(np.int32)).max() <= 2
     r = oracle_forward(cn, logits_in=logits.cpu().numpy())
     assert max_abs_rel(out_n.float().cpu().numpy(), r["out_f32"]) <= 2e-2
+
+
+# ------------------------------------------------- residual / block FFN half
+def _f32_copy(c):
+    """The same case with x and router_w as f32 (the bf16 values widened)."""
+    cf = dict(c)
+    cf["x"] = oracle.f32_from_bf16(c["x"])
+    cf["router_w"] = oracle.f32_from_bf16(c["router_w"])
+    return cf
+
+
+@pytest.mark.parametrize("T,shared", [(64, True), (300, False)])
+def test_moe_residual_is_added_before_the_one_rounding(T, shared):
+    """f32 layer: out(residual=h) == h + out() in f32, bit for bit (also in place).
+    bf16 layer: out(residual=h) == bf16(f32(h) + out_f32), the f32 layer's output
+    being the combine's f32 sum (exact routers on both sides)."""
+    from moe_cases import make_case, to_device, layer_for
+    H, I, E, k = 512, 256, 16, 4
+    c = make_case(T, H, I, E, k, seed=7 + T, shared=shared)
+    cf = _f32_copy(c)
+    gf = to_device(cf)
+    print(f"moe residual T={T} shared={shared}", flush=True)
+    Lf = layer_for(cf, gf, router_exact=True)
+    base = Lf.forward(gf["x"])
+    h = torch.randn((T, H), generator=torch.Generator(device="cuda").manual_seed(T), device="cuda")
+    withr = Lf.forward(gf["x"], residual=h)
+    inplace = h.clone()
+    Lf.forward(gf["x"], out=inplace, residual=inplace)
+    torch.cuda.synchronize()
+    ref = h.cpu().numpy() + base.cpu().numpy()
+    assert np.array_equal(withr.cpu().numpy(), ref)
+    assert np.array_equal(inplace.cpu().numpy(), ref)
+    g = to_device(c)
+    hb = h.to(torch.bfloat16)
+    outb = layer_for(c, g, router_exact=True).forward(g["x"], residual=hb)
+    torch.cuda.synchronize()
+    want = oracle.bf16_from_f32(oracle.f32_from_bf16(_host(hb)) + base.cpu().numpy())
+    assert np.array_equal(_host(outb), want)
+
+
+def test_moe_block_ffn_from_a_checkpoint(tmp_path):
+    """xstar_cpp.moe_block_ffn(h, ln2_w, eps, load_moe_layer(...)) equals the
+    layer with pre-norm and residual through the C ABI, bit for bit, and the
+    unfused h + moe(rmsnorm(h)) within two bf16 codes of the output."""
+    import xstar_cpp
+    from safetensors.torch import save_file
+    from bridge import torch_to_cpp, cpp_to_torch
+    from moe_cases import make_case, to_device, layer_for
+    from test_gpu_weights import _checkpoint
+    import xs_moe_capi as X
+    T, H, I, E, k = 96, 512, 256, 16, 4
+    c = make_case(T, H, I, E, k, seed=5)
+    p = str(tmp_path / "l.safetensors")
+    save_file(_checkpoint(c, "blk.mlp"), p)
+    w = xstar_cpp.load_moe_layer([p], "blk.mlp")
+    ln = oracle.bf16_from_f32((1 + 0.1 * np.random.default_rng(1).standard_normal(H)).astype(np.float32))
+    print("moe_block_ffn", flush=True)
+    ht = xstar_cpp.to_cuda(torch_to_cpp(_t_bf16(c["x"])))
+    out = xstar_cpp.moe_block_ffn(ht, xstar_cpp.to_cuda(torch_to_cpp(_t_bf16(ln))), 1e-6, w, top_k=k)
+    got = cpp_to_torch(xstar_cpp.to_cpu(out), (T, H))
+    g = to_device(c)
+    lnd = _dev(ln)
+    fused = layer_for(c, g, norm_weight=lnd, norm_eps=1e-6).forward(g["x"], residual=g["x"])
+    moe_out = layer_for(c, g).forward(X.rmsnorm(g["x"], lnd, 1e-6))
+    unfused = g["x"].float() + moe_out.float()
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), fused.cpu().view(torch.int16))
+    # the unfused path rounds the MoE output to bf16 before the add: the two
+    # differ by at most half an ulp of that output plus one rounding of the sum
+    # each (value-based: where h + moe cancels, the first term dominates)
+    def ulp(v):
+        return np.exp2(np.floor(np.log2(np.maximum(np.abs(v), 1e-30))) - 7)
+    a = fused.float().cpu().numpy()
+    b = unfused.to(torch.bfloat16).float().cpu().numpy()
+    m = moe_out.float().cpu().numpy()
+    assert np.all(np.abs(a - b) <= ulp(np.maximum(np.abs(a), np.abs(b))) + ulp(m) / 2)
+
+
+def _t_bf16(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).view(torch.bfloat16)

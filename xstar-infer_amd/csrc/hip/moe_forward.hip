@@ -159,6 +159,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     XS_REQUIRE(t && t->x && t->router_w && t->w13 && t->w13_scale && t->w2 && t->w2_scale && t->out,
                "null pointer");
     XS_REQUIRE(!p->has_norm || t->norm_weight, "null norm weight");
+    XS_REQUIRE(t->residual == nullptr || ((uintptr_t)t->residual & 15) == 0, "misaligned residual");
     XS_REQUIRE(!p->has_shared || (t->shared_w13 && t->shared_w13_scale && t->shared_w2 && t->shared_w2_scale),
                "null shared expert pointer");
     const WsLayout L = layout(p);
@@ -341,7 +342,8 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     }
     // 5. weighted combine (+ shared), one cast to the output dtype
     if ((rc = prof_mark(6, st))) return rc;
-    rc = launch_combine(WS(uint16_t, y), inv, w, T, k, H, S, shared_rows ? 1 : 0, t->out, p->x_dtype, st);
+    rc = launch_combine(WS(uint16_t, y), inv, w, T, k, H, S, shared_rows ? 1 : 0, t->out, p->x_dtype, st,
+                        t->residual);
     if (rc) return rc;
     if ((rc = prof_mark(7, st))) return rc;
 

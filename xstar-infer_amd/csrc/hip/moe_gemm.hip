@@ -524,7 +524,8 @@ int launch_gemm(const GemmArgs &a, bool gateup, bool fp4, int grid_y, hipStream_
 }
 
 // --------------------------------------------------------------- combine
-// out[t] = y_shared[t] + sum_j w[t,j] * y[inv[t*k+j]]  (f32, slot order, one cast)
+// out[t] = [residual[t] +] y_shared[t] + sum_j w[t,j] * y[inv[t*k+j]]
+// (f32, slot order, residual added last, one cast)
 // One block per token, one pass over the row when H <= 8 * blockDim (the
 // launch picks blockDim = H / 8 up to 512), so all k + 1 row loads of a thread
 // are in flight together.
@@ -545,7 +546,7 @@ __global__ __launch_bounds__(512) void combine_kernel(const uint16_t *__restrict
                                                       const int32_t *__restrict__ inv,
                                                       const float *__restrict__ w, int k, int H,
                                                       int64_t shared_base, int has_shared,
-                                                      OutT *__restrict__ out)
+                                                      const OutT *residual, OutT *out)
 {
     const int t = blockIdx.x;
     int pos[16];
@@ -571,22 +572,30 @@ __global__ __launch_bounds__(512) void combine_kernel(const uint16_t *__restrict
                 for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(wt[j], v[i]));
             }
         }
+        if (residual) {   // the block's residual add, before the one rounding (out may alias residual)
+            float r[8];
+            load8(residual + (size_t)t * H + c, r);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(r[i], acc[i]);
+        }
         store8(out + (size_t)t * H + c, acc);
     }
 }
 
 int launch_combine(const uint16_t *y, const int32_t *inv, const float *w, int64_t T, int64_t k,
                    int64_t H, int64_t shared_base, int has_shared, void *out, int out_dtype,
-                   hipStream_t st)
+                   hipStream_t st, const void *residual)
 {
     if (T == 0) return XS_OK;
     const int nt = (int)(H / 8 < 64 ? 64 : (H / 8 > 512 ? 512 : (H / 8 + 63) / 64 * 64));
     if (out_dtype == XS_BF16)
         combine_kernel<uint16_t><<<dim3((unsigned)T), dim3(nt), 0, st>>>(y, inv, w, (int)k, (int)H, shared_base,
-                                                                         has_shared, (uint16_t *)out);
+                                                                         has_shared, (const uint16_t *)residual,
+                                                                         (uint16_t *)out);
     else
         combine_kernel<float><<<dim3((unsigned)T), dim3(nt), 0, st>>>(y, inv, w, (int)k, (int)H, shared_base,
-                                                                      has_shared, (float *)out);
+                                                                      has_shared, (const float *)residual,
+                                                                      (float *)out);
     XS_LAUNCH_CHECK();
     return XS_OK;
 }

@@ -50,6 +50,6 @@ size_t stream_part_bytes(int64_t items_max, int K, int bm);
 int launch_gemm_stream(const GemmArgs &a, bool gateup, bool fp4, int tiles_max, int64_t rows_max, hipStream_t st);
 int launch_combine(const uint16_t *y, const int32_t *inv, const float *w, int64_t T, int64_t k,
                    int64_t H, int64_t shared_base, int has_shared, void *out, int out_dtype,
-                   hipStream_t st);
+                   hipStream_t st, const void *residual = nullptr);
 
 }  // namespace xs

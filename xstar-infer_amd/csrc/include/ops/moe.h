@@ -2,6 +2,7 @@
 #include <cstdint>
 #include <tuple>
 
+#include "ops/moe_weights.h"
 #include "tensor.h"
 
 /**
@@ -21,6 +22,8 @@
  *                    or [E, H, I/2] Float4E2M1x2 with w2_scale [E, H, I/32] Float8E8M0
  *   shared_*         one FP8 expert (2-D shapes of the above) or all nullptr
  *   top_k, n_group, topk_group, renormalize, routed_scaling: routing options
+ *   residual         [..., H] dtype of x, or nullptr: added to the output (in f32,
+ *                    before its one rounding)
  *   norm_weight      [H] dtype of x, or nullptr: the layer computes
  *                    moe(rmsnorm(x, norm_weight, norm_eps)) with the norm fused
  *                    into the activation quantization (ops/rmsnorm.h numerics)
@@ -42,7 +45,19 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
            const Tensor *shared_w2, const Tensor *shared_w2_scale,
            std::int64_t top_k, std::int64_t n_group = 1, std::int64_t topk_group = 1,
            bool renormalize = true, float routed_scaling = 1.0f, bool router_exact = false,
-           const Tensor *norm_weight = nullptr, float norm_eps = 1e-6f);
+           const Tensor *norm_weight = nullptr, float norm_eps = 1e-6f, const Tensor *residual = nullptr);
+
+/**
+ * The FFN half of a MoE transformer block in one call: h + moe(rmsnorm(h, ln2_w, eps)),
+ * the line `add(attention_x, mlp(rmsnorm(attention_x, ln2_w, eps), gate_up_w, down_w))`
+ * of xstar_cpp/src/ops/transformer_block.cpp:75,353 with the MoE in place of mlp().
+ * The norm is fused into the activation quantization and the residual into the
+ * combine (added in f32 before the output's one rounding).  `w` comes from
+ * load_moe_layer (ops/moe_weights.h).  Same checks and messages as moe().
+ */
+Tensor moe_block_ffn(const Tensor &h, const Tensor &ln2_w, float eps, const MoeLayerWeights &w, std::int64_t top_k,
+                     std::int64_t n_group = 1, std::int64_t topk_group = 1, bool renormalize = true,
+                     float routed_scaling = 1.0f, bool router_exact = false);
 
 /** Router logits x . router_w^T in f32 ([T, E]); exact: bit-identical to
  * gemm_cpu's sequential accumulation (xstar_cpp/include/ops/gemm.h:57-83). */

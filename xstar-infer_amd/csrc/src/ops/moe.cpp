@@ -34,13 +34,14 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
            const Tensor *shared_w2, const Tensor *shared_w2_scale,
            std::int64_t top_k, std::int64_t n_group, std::int64_t topk_group,
            bool renormalize, float routed_scaling, bool router_exact,
-           const Tensor *norm_weight, float norm_eps)
+           const Tensor *norm_weight, float norm_eps, const Tensor *residual)
 {
     // ---- dtype ----
     if (!is_act(x.dtype())) throw std::runtime_error("unsupported dtype");
     if (router_w.dtype() != x.dtype()) throw std::runtime_error("dtype mismatch");
     if (router_bias && router_bias->dtype() != DType::Float32) throw std::runtime_error("dtype mismatch");
     if (norm_weight && norm_weight->dtype() != x.dtype()) throw std::runtime_error("dtype mismatch");
+    if (residual && residual->dtype() != x.dtype()) throw std::runtime_error("dtype mismatch");
     const bool fp4 = w13.dtype() == DType::Float4E2M1x2;
     const DType wq = fp4 ? DType::Float4E2M1x2 : DType::Float8E4M3;
     const DType ws = fp4 ? DType::Float8E8M0 : DType::Float32;
@@ -72,6 +73,7 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
     };
     bool ok = router_w.shape()[1] == H && eq(w13.shape(), {E, 2 * I, hk}) && eq(w2.shape(), {E, H, fp4 ? I / 2 : I}) &&
               (!router_bias || router_bias->shape()[0] == E) && (!norm_weight || norm_weight->shape()[0] == H) &&
+              (!residual || residual->shape() == x.shape()) &&
               H % 256 == 0 && I % 128 == 0;
     if (ok) {
         if (fp4) ok = eq(w13_scale.shape(), {E, 2 * I, H / 32}) && eq(w2_scale.shape(), {E, H, I / 32});
@@ -85,6 +87,7 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
     for (const Tensor *t : {&router_w, &w13, &w13_scale, &w2, &w2_scale}) same_device(x, *t);
     if (router_bias) same_device(x, *router_bias);
     if (norm_weight) same_device(x, *norm_weight);
+    if (residual) same_device(x, *residual);
     if (has_shared)
         for (const Tensor *t : {shared_w13, shared_w13_scale, shared_w2, shared_w2_scale}) same_device(x, *t);
     require_cuda(x);
@@ -125,9 +128,21 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
     }
     t.out = out.data();
     t.norm_weight = norm_weight ? norm_weight->data() : nullptr;
+    t.residual = residual ? residual->data() : nullptr;
     xs_check(xs_moe_forward(&p, &t, wsp.data(), wsb, nullptr));
     sync();
     return out;
+}
+
+Tensor moe_block_ffn(const Tensor &h, const Tensor &ln2_w, float eps, const MoeLayerWeights &w, std::int64_t top_k,
+                     std::int64_t n_group, std::int64_t topk_group, bool renormalize, float routed_scaling,
+                     bool router_exact)
+{
+    if (!w.router_w || !w.w13 || !w.w13_scale || !w.w2 || !w.w2_scale) throw std::runtime_error("shape mismatch");
+    auto p = [](const std::optional<Tensor> &t) { return t ? &*t : nullptr; };
+    return moe(h, *w.router_w, p(w.router_bias), *w.w13, *w.w13_scale, *w.w2, *w.w2_scale, p(w.shared_w13),
+               p(w.shared_w13_scale), p(w.shared_w2), p(w.shared_w2_scale), top_k, n_group, topk_group, renormalize,
+               routed_scaling, router_exact, &ln2_w, eps, &h);
 }
 
 Tensor moe_router_logits(const Tensor &x, const Tensor &router_w, bool exact)
