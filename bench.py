@@ -132,8 +132,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="prefill only, no extra configs")
-    ap.add_argument("--sections", default="prefill,decode,gemm,fp4,norm",
-                    help="comma list of prefill,decode,gemm,fp4,norm (the JSON line needs prefill)")
+    ap.add_argument("--sections", default="prefill,decode,gemm,fp4,norm,block",
+                    help="comma list of prefill,decode,gemm,fp4,norm,block (the JSON line needs prefill)")
     ap.add_argument("--decode-tokens", default="1,16,64,256",
                     help="comma list of decode batch sizes (configs[3])")
     ap.add_argument("--no-cpu", action="store_true")
@@ -163,8 +163,8 @@ def main():
         res["gemm_fp8_512x4096x4096"] = single_gemm(a, X, torch)
     if "fp4" in sections:
         res["fp4_2048"] = fp4_layer(a, X, torch)
-    if "norm" in sections:
-        res["rmsnorm_8192x4096"] = norm_legs(a, X, torch)
+    if "norm" in sections or "block" in sections:
+        res["rmsnorm_8192x4096"] = norm_legs(a, X, torch, kernels="norm" in sections, block="block" in sections)
     print(json.dumps(res))
     return 0
 
@@ -287,7 +287,7 @@ def fp4_layer(a, X, torch):
 
 
 
-def norm_legs(a, X, torch):
+def norm_legs(a, X, torch, kernels=True, block=True):
     """RMSNorm at the prefill activation shape (8192 x 4096 bf16): alone, fused
     with the FP8 1x128 quant of its output, the separate quant for comparison,
     and the MoE layer with the pre-norm against the layer without it."""
@@ -326,12 +326,16 @@ def norm_legs(a, X, torch):
     b_norm = 2 * T * H * 2 + 2 * H
     b_fused = b_norm + T * H + 4 * T * (H // 128)
     b_quant = 2 * T * H + T * H + 4 * T * (H // 128)
-    for name, fn, by in (("rmsnorm", lambda: norm(False), b_norm), ("rmsnorm_fp8", lambda: norm(True), b_fused),
-                         ("quant_act_fp8", quant_only, b_quant)):
+    legs = (("rmsnorm", lambda: norm(False), b_norm), ("rmsnorm_fp8", lambda: norm(True), b_fused),
+            ("quant_act_fp8", quant_only, b_quant))
+    for name, fn, by in legs if kernels else ():
         ms = timed(fn)
         out[name] = {"ms": ms, "bytes": by, "gbs": by / (ms * 1e-3) / 1e9,
                      "frac_hbm_peak": by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
     del x, y, q, s
+    if not block:
+        torch.cuda.empty_cache()
+        return out
     # the MoE layer with and without the pre-norm (prefill and a decode batch)
     g = synth_layer(T, H, I, E, K_TOP, seed=0, zipf=1.1)
     for Tn in (T, 16):
