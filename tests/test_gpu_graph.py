@@ -1,0 +1,54 @@
+"""The MoE forward under HIP graph capture (torch.cuda.CUDAGraph): every replay
+equals the eager output bit for bit, with the program's own eager forwards and
+synchronisations between the replays.  The forward records no memset (its
+persistent-GEMM counters are cleared by the permute kernel), so a captured
+graph replays the same work each time."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import xs_moe_capi  # noqa: F401  (fails loudly when the library is missing)
+
+
+@pytest.mark.parametrize("T,stream,norm", [(16, "1", False), (16, "0", True), (200, "1", True), (64, "0", False)])
+def test_graph_replays_equal_eager(monkeypatch, T, stream, norm):
+    from moe_cases import make_case, to_device, layer_for
+    monkeypatch.setenv("XS_MOE_STREAM", stream)
+    H, I, E, k = 512, 256, 16, 4
+    c = make_case(max(T, 40), H, I, E, k, seed=T)
+    g = to_device(c)
+    kw = {}
+    if norm:
+        kw = dict(norm_weight=torch.ones(H, dtype=torch.bfloat16, device="cuda"), norm_eps=1e-6)
+    L = layer_for(c, g, **kw)
+    x = g["x"][:T].contiguous()
+    other = g["x"][T // 2:T // 2 + 7].contiguous()
+    print(f"graph T={T} XS_MOE_STREAM={stream} norm={norm}", flush=True)
+    eager = L.forward(x).clone()
+    out = torch.empty_like(eager)
+    res = x.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):   # warm-up on the capture stream (workspace allocated here)
+        L.forward(x, out=out, residual=res if norm else None)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        L.forward(x, out=out, residual=res if norm else None)
+    want = L.forward(x, residual=res).clone() if norm else eager
+    for rep in range(4):
+        out.zero_()
+        L.forward(other)            # eager work between replays, same workspace
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {rep}"
