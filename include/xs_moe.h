@@ -9,7 +9,11 @@
  * the reference (xstar_cpp/include/cuda/cuda_check.h:23-31).
  *
  * All device pointers must be device-resident (hipMalloc'd or torch CUDA
- * tensors).  Compute entry points enqueue work on `stream` and return without
+ * tensors).  Activations, outputs and weights are moved with 16-byte vector
+ * loads and stores: their base pointers must be 16-byte aligned (f32 scales 4,
+ * FP8 codes written by the quantizers 8); a misaligned pointer is rejected
+ * with XS_ERR_INVALID ("misaligned operand ...").  xs_rmsnorm without its FP8
+ * output accepts any alignment (it falls back to a scalar kernel).  Compute entry points enqueue work on `stream` and return without
  * synchronising; callers that need results on the host synchronise the stream
  * (the C++ Tensor ops do, matching the reference's synchronous launchers,
  * xstar_cpp/src/ops/gemm.cu:238-239).

@@ -44,3 +44,11 @@ def test_argument_validation_without_gpu():
     assert rc == 1 and b"null" in L.xs_last_error()
     rc = L.xs_quant_act_fp8(ctypes.c_void_p(16), X.XS_BF16, 4, 100, ctypes.c_void_p(16), ctypes.c_void_p(16), None)
     assert rc == 1 and b"128" in L.xs_last_error()
+    rc = L.xs_quant_act_fp8(ctypes.c_void_p(18), X.XS_BF16, 4, 128, ctypes.c_void_p(16), ctypes.c_void_p(16), None)
+    assert rc == 1 and b"misaligned" in L.xs_last_error()
+    rc = L.xs_rmsnorm(ctypes.c_void_p(16), ctypes.c_void_p(16), X.XS_BF16, 4, 128, 1e-6, ctypes.c_void_p(18),
+                      ctypes.c_void_p(16), ctypes.c_void_p(16), None)
+    assert rc == 1 and b"misaligned" in L.xs_last_error()
+    rc = L.xs_rmsnorm(ctypes.c_void_p(16), ctypes.c_void_p(16), X.XS_BF16, 4, 96, 1e-6, ctypes.c_void_p(16),
+                      ctypes.c_void_p(16), ctypes.c_void_p(16), None)
+    assert rc == 1 and b"hidden % 128" in L.xs_last_error()

@@ -159,7 +159,13 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     XS_REQUIRE(t && t->x && t->router_w && t->w13 && t->w13_scale && t->w2 && t->w2_scale && t->out,
                "null pointer");
     XS_REQUIRE(!p->has_norm || t->norm_weight, "null norm weight");
-    XS_REQUIRE(t->residual == nullptr || ((uintptr_t)t->residual & 15) == 0, "misaligned residual");
+    XS_REQUIRE(((uintptr_t)t->x & 15) == 0 && ((uintptr_t)t->out & 15) == 0 &&
+                   ((uintptr_t)t->residual & 15) == 0,
+               "misaligned operand: x, out and residual need 16-byte alignment");
+    XS_REQUIRE(((uintptr_t)t->w13 & 15) == 0 && ((uintptr_t)t->w2 & 15) == 0 &&
+                   ((uintptr_t)t->shared_w13 & 15) == 0 && ((uintptr_t)t->shared_w2 & 15) == 0 &&
+                   ((uintptr_t)t->router_w & 15) == 0,
+               "misaligned operand: weights need 16-byte alignment");
     XS_REQUIRE(!p->has_shared || (t->shared_w13 && t->shared_w13_scale && t->shared_w2 && t->shared_w2_scale),
                "null shared expert pointer");
     const WsLayout L = layout(p);
@@ -438,6 +444,9 @@ int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int
                            int64_t K, void *C, void *workspace, size_t workspace_bytes, void *stream)
 {
     XS_REQUIRE(A && B && Bs && C, "null pointer");
+    XS_REQUIRE(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && ((uintptr_t)C & 15) == 0 &&
+                   ((uintptr_t)Bs & 3) == 0,
+               "misaligned operand: A, B and C need 16-byte, Bs 4-byte alignment");
     XS_REQUIRE(M >= 0 && M < (1 << 24) && N >= 128 && N % 128 == 0 && K >= 128 && K % 128 == 0,
                "shape mismatch: N and K must be multiples of 128");
     size_t o_s, o_meta;

@@ -671,6 +671,8 @@ int xs_quant_act_fp8(const void *x, int dtype, int64_t rows, int64_t cols, uint8
     XS_REQUIRE(x && q && s, "null pointer");
     XS_REQUIRE(dtype == XS_F32 || dtype == XS_BF16, "unsupported dtype");
     XS_REQUIRE(rows >= 0 && cols > 0 && cols % 128 == 0, "cols must be a multiple of 128");
+    XS_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 7) == 0 && ((uintptr_t)s & 3) == 0,
+               "misaligned operand: x needs 16-byte, q 8-byte, s 4-byte alignment");
     return launch_quant_act(x, dtype, rows, cols, q, s, 0, (hipStream_t)stream);
 }
 
@@ -680,6 +682,8 @@ int xs_quant_act_mxfp8(const void *x, int dtype, int64_t rows, int64_t cols, uin
     XS_REQUIRE(x && q && s, "null pointer");
     XS_REQUIRE(dtype == XS_F32 || dtype == XS_BF16, "unsupported dtype");
     XS_REQUIRE(rows >= 0 && cols > 0 && cols % 32 == 0, "cols must be a multiple of 32");
+    XS_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 7) == 0,
+               "misaligned operand: x needs 16-byte, q 8-byte alignment");
     return launch_quant_act(x, dtype, rows, cols, q, s, 1, (hipStream_t)stream);
 }
 

@@ -211,6 +211,7 @@ extern "C" int xs_rmsnorm(const void *x, const void *weight, int dtype, int64_t 
     XS_REQUIRE(rows * hidden < ((int64_t)1 << 40), "too many elements");
     if (rows == 0) return XS_OK;
     XS_REQUIRE(x && weight && y, "null pointer");
-    XS_REQUIRE(q == nullptr || (((uintptr_t)q & 7) == 0 && ((uintptr_t)s & 3) == 0), "misaligned FP8 output");
+    XS_REQUIRE(q == nullptr || (((uintptr_t)q & 7) == 0 && ((uintptr_t)s & 3) == 0 && ((uintptr_t)y & 15) == 0),
+               "misaligned operand: with the FP8 output, y needs 16-byte, q 8-byte, s 4-byte alignment");
     return launch_rmsnorm(x, weight, dtype, rows, hidden, eps, y, q, s, (hipStream_t)stream);
 }
