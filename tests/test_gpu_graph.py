@@ -2,7 +2,8 @@
 equals the eager output bit for bit, with the program's own eager forwards and
 synchronisations between the replays.  The forward records no memset (its
 persistent-GEMM counters are cleared by the permute kernel), so a captured
-graph replays the same work each time."""
+graph replays the same work each time.  Also: the activation quant folded
+into the decode router launch equals the separate quant pass."""
 import numpy as np
 import pytest
 
@@ -52,3 +53,21 @@ def test_graph_replays_equal_eager(monkeypatch, T, stream, norm):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), want.view(torch.int16)), f"replay {rep}"
+
+
+@pytest.mark.parametrize("T", [1, 16, 100, 256])
+def test_router_folded_quant_equals_separate_quant(monkeypatch, T):
+    """Decode batches quantize the activations inside the router launch; the
+    layer output equals the one with the separate quant pass, bit for bit."""
+    from moe_cases import make_case, to_device, layer_for
+    H, I, E, k = 1024, 256, 32, 4
+    c = make_case(T, H, I, E, k, seed=100 + T)
+    g = to_device(c)
+    L = layer_for(c, g)
+    print(f"fold quant T={T}", flush=True)
+    monkeypatch.setenv("XS_FOLD_QUANT", "1")
+    a = L.forward(g["x"]).clone()
+    monkeypatch.setenv("XS_FOLD_QUANT", "0")
+    b = L.forward(g["x"]).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))

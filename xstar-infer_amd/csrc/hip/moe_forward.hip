@@ -65,6 +65,13 @@ static bool use_wide(const xs_moe_params *p)
 // The routed (FP8: and shared) GEMMs may run the persistent kernels
 // (moe_gemm_stream.hip) when the tall-tile FP8 kernels are not used:
 // 0 never, 1 by size, 2 always.  XS_MOE_STREAM=0|1 forces (benchmarks, tests).
+// An on/off switch from the environment, read per call (tests switch it).
+static bool getenv_flag(const char *name, bool dflt)
+{
+    const char *v = getenv(name);
+    return v ? v[0] != '0' : dflt;
+}
+
 static int use_stream(const xs_moe_params *p)
 {
     if (p->routed_format == XS_FP8_E4M3 && use_wide(p)) return 0;
@@ -199,7 +206,11 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
                             fp8_act ? WS(uint8_t, xq) : nullptr, fp8_act ? WS(float, xs) : nullptr, st);
         if (rc) return rc;
         xin = xn;
-    } else if (fp8_act) {
+    }
+    // small batches: the decode router writes the FP8 activations in its own launch
+    const bool fold_quant = !p->has_norm && fp8_act && router_quantizes(T, p->router_exact, p->x_dtype) &&
+                            getenv_flag("XS_FOLD_QUANT", true);
+    if (!p->has_norm && fp8_act && !fold_quant) {
         rc = launch_quant_act(xin, p->x_dtype, T, H, WS(uint8_t, xq), WS(float, xs), 0, st);
         if (rc) return rc;
     }
@@ -211,7 +222,8 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     if ((rc = prof_mark(1, st))) return rc;
     const int nsplit = router_logits_splits(T, H, p->router_exact, p->x_dtype);
     rc = launch_router_logits(xin, t->router_w, p->x_dtype, T, E, H, p->router_exact, logits, nsplit, st, mask,
-                              (int64_t)Wd * E);
+                              (int64_t)Wd * E, fold_quant ? WS(uint8_t, xq) : nullptr,
+                              fold_quant ? WS(float, xs) : nullptr);
     if (rc) return rc;
     if ((rc = prof_mark(2, st))) return rc;
     rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,

@@ -73,9 +73,13 @@ __device__ __forceinline__ void quant8_fp8(const float *v, uint8_t *__restrict__
 int router_logits_splits(int64_t T, int64_t H, int exact, int dtype);
 // Writes nsplit partial logit slices [nsplit][T][E] (nsplit = 1: the logits).
 // mask_clear (optional): a [mask_words] bitmask zeroed by the same launch.
+// q/qs (optional, decode path only: router_quantizes()): the FP8 1x128
+// quantization of x, written by the same launch.
+bool router_quantizes(int64_t T, int exact, int dtype);
 int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
                          int exact, float *logits, int nsplit, hipStream_t st,
-                         uint32_t *mask_clear = nullptr, int64_t mask_words = 0);
+                         uint32_t *mask_clear = nullptr, int64_t mask_words = 0, uint8_t *q = nullptr,
+                         float *qs = nullptr);
 // Routes on the sum (in slice order) of nsplit partial logit slices; writes the
 // summed logits to logits_out when it is not NULL.
 int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,

@@ -59,6 +59,17 @@ __global__ __launch_bounds__(256) void router_logits_exact_kernel(const T *__res
     if (t < Tn && e < E) logits[(size_t)t * E + e] = acc;
 }
 
+// FP8 1x128 of one 8-column chunk c8 of a row: the 16 lanes of an aligned
+// 16-lane group hold the 16 chunks of one 128-column group.
+template <typename T>
+__device__ __forceinline__ void quant_chunk_fp8(const T *__restrict__ xr, int cols, int c8,
+                                                uint8_t *__restrict__ qr, float *__restrict__ sr)
+{
+    float v[8];
+    load8(xr + c8 * 8, v);
+    quant8_fp8(v, qr + c8 * 8, (c8 & 15) == 0 ? sr + c8 / 16 : nullptr);
+}
+
 // ------------------------------------------------------------- MFMA logits
 // Block = 2 x 2 waves; a wave owns MT x NT subtiles of 16 tokens x 16 experts
 // over one K slice (blockIdx.z; several slices = split-K for few tokens, the
@@ -73,9 +84,21 @@ __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t 
                                                                  const uint16_t *__restrict__ wr,
                                                                  int Tn, int E, int H, int klen,
                                                                  float *__restrict__ part,
-                                                                 uint32_t *__restrict__ mask, int64_t mask_words)
+                                                                 uint32_t *__restrict__ mask, int64_t mask_words,
+                                                                 uint8_t *__restrict__ q, float *__restrict__ qs)
 {
     clear_mask(mask, mask_words);
+    if (q && blockIdx.x == 0) {
+        // the FP8 1x128 activation quant of this block's tokens and K slice
+        // (klen % 128 == 0, so each aligned 16-lane group is one 128-column group)
+        const int per_row = klen / 8, rows = 32 * MT;
+        for (int c = threadIdx.x; c < rows * per_row; c += 256) {
+            const int t = blockIdx.y * rows + c / per_row;
+            if (t < Tn)
+                quant_chunk_fp8(x + (size_t)t * H, H, blockIdx.z * per_row + c % per_row, q + (size_t)t * H,
+                                qs + (size_t)t * (H / 128));
+        }
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int wm = wave >> 1, wn = wave & 1;
@@ -454,10 +477,17 @@ int router_logits_splits(int64_t T, int64_t H, int exact, int dtype)
     return ns;
 }
 
+bool router_quantizes(int64_t T, int exact, int dtype)
+{
+    return !exact && dtype == XS_BF16 && T <= 256;   // the decode (router_logits_mfma_kernel) path
+}
+
 int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
                          int exact, float *logits, int nsplit, hipStream_t st, uint32_t *mask_clear,
-                         int64_t mask_words)
+                         int64_t mask_words, uint8_t *q, float *qs)
 {
+    if (q && !router_quantizes(T, exact, dtype))
+        return set_error(XS_ERR_INVALID, "router: the activation quant is folded into the decode path only");
     if (T == 0) return XS_OK;
     if (exact || dtype == XS_F32) {
         dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16)), block(256);
@@ -485,24 +515,13 @@ int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, in
         dim3 grid((unsigned)((E + 63) / 64), (unsigned)((T + 31) / 32), (unsigned)nsplit), block(256);
         router_logits_mfma_kernel<1, 2><<<grid, block, 0, st>>>((const uint16_t *)x, (const uint16_t *)wr,
                                                                 (int)T, (int)E, (int)H, (int)(H / nsplit), logits,
-                                                                mask_clear, mask_words);
+                                                                mask_clear, mask_words, q, qs);
     }
     XS_LAUNCH_CHECK();
     return XS_OK;
 }
 
 // ---------------------------------------------------- activation quantizers
-// FP8 1x128 of one 8-column chunk c8 of a row: the 16 lanes of an aligned
-// 16-lane group hold the 16 chunks of one 128-column group.
-template <typename T>
-__device__ __forceinline__ void quant_chunk_fp8(const T *__restrict__ xr, int cols, int c8,
-                                                uint8_t *__restrict__ qr, float *__restrict__ sr)
-{
-    float v[8];
-    load8(xr + c8 * 8, v);
-    quant8_fp8(v, qr + c8 * 8, (c8 & 15) == 0 ? sr + c8 / 16 : nullptr);
-}
-
 // Each thread owns 8 consecutive columns (rows are whole multiples of 16
 // threads, so the 16-lane groups stay aligned).
 template <typename T>
