@@ -95,7 +95,11 @@ int xs_moe_route(const float *logits, const float *bias, int64_t T, int64_t E, i
 /* Stable counting sort of the T*k slots (slot = t*k + j) by expert.
  * counts [E], offsets [E+1] (exclusive scan), perm [T*k] (position -> slot),
  * inv [T*k] (slot -> position).  workspace: xs_moe_permute_workspace_size()
- * bytes of device memory. */
+ * bytes of device memory.  Precondition, checked: every idx is in [0, E) and no
+ * row names an expert twice (the router's output always is).  Otherwise the
+ * call returns XS_ERR_INVALID ("idx: expert index outside [0, E)" / "idx:
+ * expert named twice in one row") and the outputs are unspecified.  The check
+ * waits for the stream once, so this stage entry point is synchronous. */
 size_t xs_moe_permute_workspace_size(int64_t T, int64_t E);
 int xs_moe_permute(const int32_t *idx, int64_t T, int64_t E, int64_t k, int32_t *counts,
                    int32_t *offsets, int32_t *perm, int32_t *inv, void *workspace,

@@ -175,6 +175,31 @@ def test_permute_bitexact(T, E, k):
     assert np.array_equal(inv.cpu().numpy(), ri)
 
 
+@pytest.mark.parametrize("case", ["out_of_range", "negative", "duplicate"])
+def test_permute_rejects_invalid_idx(case):
+    """The public permute checks its precondition (experts in [0, E), distinct
+    within a row) and fails with the documented error; a valid call after it
+    still matches the oracle (the error leaves no state behind)."""
+    import xs_moe_capi as X
+    rng = np.random.default_rng(7)
+    T, E, k = 100, 16, 4
+    idx = np.array([rng.permutation(E)[:k] for _ in range(T)], np.int32)
+    bad = idx.copy()
+    if case == "out_of_range":
+        bad[37, 2] = E
+    elif case == "negative":
+        bad[99, 3] = -1
+    else:
+        bad[5, 3] = bad[5, 0]
+    msg = "outside" if case != "duplicate" else "twice"
+    with pytest.raises(X.XsError, match=msg):
+        X.permute(torch.from_numpy(bad).cuda(), E)
+    counts, offsets, perm, inv = X.permute(torch.from_numpy(idx).cuda(), E)
+    rc, ro, rp, ri = oracle.permute(idx, E)
+    assert np.array_equal(counts.cpu().numpy(), rc) and np.array_equal(perm.cpu().numpy(), rp)
+    assert np.array_equal(inv.cpu().numpy(), ri) and np.array_equal(offsets.cpu().numpy(), ro)
+
+
 @pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (40, 256, 384), (1, 128, 128), (2100, 512, 1024)])
 def test_gemm_fp8_blockscale(M, N, K):
     """C = dequant(quant1x128(A)) . dequant(B)^T vs a float64 reference on the

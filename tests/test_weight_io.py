@@ -210,3 +210,23 @@ def test_loader_errors(tmp_path):
     save_file(dense, p)
     with pytest.raises(RuntimeError, match="unsupported device"):   # dense weights are quantized on the GPU
         xstar_cpp.load_moe_layer([p], "m", xstar_cpp.Device.CPU)
+
+
+def test_rejects_byte_count_overflow(tmp_path):
+    """shape product fits 64 bits but times the dtype size wraps to 0; a wrapped
+    count must not pass the data_offsets check."""
+    p = tmp_path / "a"
+    hb = json.dumps({"w": {"dtype": "F32", "shape": [2 ** 31, 2 ** 31], "data_offsets": [0, 0]}}).encode()
+    hb += b" " * ((-len(hb)) % 8)
+    p.write_bytes(struct.pack("<Q", len(hb)) + hb)
+    with pytest.raises(RuntimeError, match="element count overflows"):
+        xstar_cpp.parse_safetensors_header(xstar_cpp.MMapFile(str(p)))
+
+
+def test_weight_view_rejects_byte_count_overflow(tmp_path):
+    p = _raw_file(tmp_path / "a.safetensors", {"w": ("F32", [2], b"\0" * 8)})
+    mf = xstar_cpp.MMapFile(p)
+    with pytest.raises(RuntimeError, match="element count overflows"):
+        xstar_cpp.make_weight_view(mf, 0, [2 ** 62], D.Float32)
+    with pytest.raises(RuntimeError, match="element count overflows"):
+        xstar_cpp.make_weight_view(mf, 0, [2 ** 40, 2 ** 40], D.Float32)

@@ -29,15 +29,22 @@ int launch_mask_clear(uint32_t *mask, int64_t words, hipStream_t st)
     return XS_OK;
 }
 
+// Sets bit t of mask[e] for every slot; flags (bit 0) an expert outside [0, E)
+// and (bit 1) an expert named twice in one row: the second atomicOr of a bit
+// finds it already set, whichever order the atomics run in.
 __global__ void build_mask_kernel(const int32_t *__restrict__ idx, int64_t S, int k, int E,
-                                  uint32_t *__restrict__ mask, int W)
+                                  uint32_t *__restrict__ mask, int W, uint32_t *__restrict__ bad)
 {
     int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= S) return;
     int e = idx[s];
-    if (e < 0 || e >= E) return;
+    if (e < 0 || e >= E) {
+        atomicOr(bad, 1u);
+        return;
+    }
     int t = (int)(s / k);
-    atomicOr(&mask[(size_t)e * W + (t >> 5)], 1u << (t & 31));
+    const uint32_t bit = 1u << (t & 31);
+    if (atomicOr(&mask[(size_t)e * W + (t >> 5)], bit) & bit) atomicOr(bad, 2u);
 }
 
 // Exclusive scan of one int per thread over a 1024-thread block.
@@ -236,7 +243,7 @@ extern "C" {
 size_t xs_moe_permute_workspace_size(int64_t T, int64_t E)
 {
     size_t W = (size_t)mask_words_for(T);
-    return 2 * align256(sizeof(uint32_t) * W * (size_t)E);
+    return 2 * align256(sizeof(uint32_t) * W * (size_t)E) + 256;
 }
 
 int xs_moe_permute(const int32_t *idx, int64_t T, int64_t E, int64_t k, int32_t *counts,
@@ -252,12 +259,21 @@ int xs_moe_permute(const int32_t *idx, int64_t T, int64_t E, int64_t k, int32_t 
     const int W = mask_words_for(T);
     uint32_t *mask = (uint32_t *)workspace;
     int32_t *wordprefix = (int32_t *)((char *)workspace + align256(sizeof(uint32_t) * W * (size_t)E));
+    uint32_t *bad = (uint32_t *)((char *)wordprefix + align256(sizeof(uint32_t) * W * (size_t)E));
     int rc = launch_mask_clear(mask, (int64_t)W * E, st);
     if (rc) return rc;
     if (T * k > 0) {
+        if ((rc = launch_mask_clear(bad, 1, st))) return rc;
         build_mask_kernel<<<dim3((unsigned)((T * k + 255) / 256)), dim3(256), 0, st>>>(
-            idx, T * k, (int)k, (int)E, mask, W);
+            idx, T * k, (int)k, (int)E, mask, W, bad);
         XS_LAUNCH_CHECK();
+        // the caller's idx is checked before anything is placed (this entry
+        // point therefore waits for its stream once)
+        uint32_t flags = 0;
+        XS_HIP(hipMemcpyAsync(&flags, bad, 4, hipMemcpyDeviceToHost, st));
+        XS_HIP(hipStreamSynchronize(st));
+        if (flags & 1u) return set_error(XS_ERR_INVALID, "idx: expert index outside [0, E)");
+        if (flags & 2u) return set_error(XS_ERR_INVALID, "idx: expert named twice in one row");
     }
     PermuteOut o = {};   // caller's offsets has E+1 entries: offsets_ext = 0
     o.counts = counts;

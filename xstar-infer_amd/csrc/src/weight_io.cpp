@@ -3,6 +3,7 @@
 // with the quantized dtypes of FP8 / FP4 checkpoints added.
 #include "weight_io.h"
 
+#include <cstdint>
 #include <cstring>
 #include <stdexcept>
 
@@ -145,8 +146,11 @@ Tensor make_weight_view(MMapFile &mf, std::size_t offset, std::vector<std::int64
     std::size_t numel = 1;
     for (auto d : shape) {
         if (d < 0) throw std::runtime_error("negative dimension");
+        if (d != 0 && numel > SIZE_MAX / static_cast<std::size_t>(d))
+            throw std::runtime_error("element count overflows");
         numel *= static_cast<std::size_t>(d);
     }
+    if (numel > SIZE_MAX / es) throw std::runtime_error("element count overflows");
     const std::size_t nbytes = numel * es;
     if (offset > mf.size() || nbytes > mf.size() - offset) throw std::runtime_error("weight view exceeds mmap region");
     return Tensor(static_cast<const char *>(mf.addr()) + offset, std::move(shape), dtype, Device::CPU);
@@ -213,6 +217,8 @@ std::unordered_map<std::string, TensorMeta> parse_safetensors_header(const MMapF
                 throw std::runtime_error("header inconsistent: element count overflows");
             numel *= static_cast<std::uint64_t>(d);
         }
+        if (numel > UINT64_MAX / dtype_size(dtype))
+            throw std::runtime_error("header inconsistent: element count overflows");
         const std::uint64_t nbytes = numel * dtype_size(dtype);
         if (b1 < b0 || b1 - b0 != nbytes)
             throw std::runtime_error("header inconsistent: data_offsets span " + std::to_string(b1 - b0) +
