@@ -204,6 +204,13 @@ typedef struct {
      * (the block's residual, xstar_cpp/src/ops/transformer_block.cpp:75,353:
      * add(h, mlp(rmsnorm(h)))); may equal out (in place); NULL = none */
     const void *residual;
+    /* optional inspection outputs of the expert stages (NULL = not written),
+     * rows in position order: the routed rows sorted by (expert, token), then
+     * the shared segment's T rows; R = T*k (+ T with the shared expert).
+     * act_q / act_s: FP8 routed format only (ignored for MXFP4). */
+    uint8_t *act_q;            /* [R, I] e4m3: SwiGLU output after its FP8 1x128 re-quant */
+    float *act_s;              /* [R, I/128] f32 scales of act_q */
+    float *y_rows;             /* [R, H] f32: each row's down projection, before the combine */
 } xs_moe_tensors;
 
 /* Device workspace the forward needs for these params (bytes, 256-aligned). */

@@ -53,11 +53,138 @@ def _run_and_check(c, g, router_exact, tol=TOL, rows=None):
     return err
 
 
-def test_moe_c1_tiny_f32():
+# f32 layers.  The whole chain is held to the 2e-2 bound: accumulation order
+# can move one SwiGLU activation across an e4m3 rounding boundary of its FP8
+# re-quantization, and one such flip moves an output by ~5e-3 of its range.
+# The stages around that quantization are held to tight bounds on their own
+# inputs: the combine bit for bit (f32 sum in the fixed order, one cast), and
+# the down projection of the GPU's own act rows to 1e-4 of the float64 product
+# (the FP8 MFMA's own accumulation of a 128-long block measured 4.3e-5 of the
+# output range on C1, median row 1.9e-5: above f32 rounding of a sequential
+# sum, a property of the matrix core).
+TOL_F32 = 1e-4
+
+
+def _check_f32_stages(c, g, d, out):
+    """d: debug outputs of one forward (including act_q, act_s, y_rows)."""
+    T, H, I, E, k = c["T"], c["H"], c["I"], c["E"], c["k"]
+    S = T * k
+    R = S + (T if c["shared"] is not None else 0)
+    y = d["y_rows"]
+    inv = d["inv"].reshape(T, k)
+    # (1) combine: shared row, then the k slots as a + w_j * y_j, each f32-rounded
+    a = y[S:S + T].copy() if c["shared"] is not None else np.zeros((T, H), np.float32)
+    for j in range(k):
+        a = (a + (d["topk_w"][:, j:j + 1] * y[inv[:, j]]).astype(np.float32)).astype(np.float32)
+    got = out.cpu().numpy() if out.dtype == torch.float32 else out.view(torch.int16).cpu().numpy().view(np.uint16)
+    want = a if out.dtype == torch.float32 else oracle.bf16_from_f32(a)
+    assert np.array_equal(got, want)
+    # (2) down projection of the GPU's act rows against float64
+    tab = oracle.e4m3_table().astype(np.float64)
+    act = tab[d["act_q"]] * np.repeat(d["act_s"], 128, 1)
+    expert = np.searchsorted(d["offsets"], np.arange(S), side="right") - 1
+    w2 = {e: oracle.dequant_weight_fp8_block(c["w2"][e], c["s2"][e]).astype(np.float64) for e in np.unique(expert)}
+    yref = np.empty((R, H))
+    for r in range(S):
+        yref[r] = w2[expert[r]] @ act[r]
+    if R > S:
+        sw2 = oracle.dequant_weight_fp8_block(c["shared"][2], c["shared"][3]).astype(np.float64)
+        yref[S:] = act[S:] @ sw2.T
+    err = np.abs(y - yref).max() / np.abs(yref).max()
+    print(f"down rows vs float64: max-abs-rel {err:.3e}, median row {np.median(np.abs(y - yref).max(1)) / np.abs(yref).max():.3e}")
+    assert err <= TOL_F32, err
+    # (3) gate_up + SwiGLU + re-quant: scales to f32 rounding, codes equal but
+    # for rare one-step flips at rounding boundaries
+    x = np.asarray(c["x"], np.float32) if c["x"].dtype != np.uint16 else oracle.f32_from_bf16(c["x"])
+    xq, xs = oracle.quant_act_fp8(x)
+    xd = tab[xq] * np.repeat(xs, 128, 1)
+    tok = np.concatenate([d["perm"] // k, np.arange(R - S)])
+    gu = np.empty((R, 2 * I))
+    for r in range(R):
+        w13 = (oracle.dequant_weight_fp8_block(c["w13"][expert[r]], c["s13"][expert[r]]) if r < S
+               else oracle.dequant_weight_fp8_block(c["shared"][0], c["shared"][1]))
+        gu[r] = w13.astype(np.float64) @ xd[tok[r]]
+    gate, up = gu[:, :I], gu[:, I:]
+    aref = (gate / (1 + np.exp(-gate)) * up).astype(np.float32)
+    qref, sref = oracle.quant_act_fp8(aref)
+    assert np.abs(d["act_s"] / sref - 1).max() <= TOL_F32
+    diff = d["act_q"] != qref
+    print(f"act codes differing from the float64 chain: {diff.mean():.2e}")
+    assert diff.mean() <= 1e-2, diff.mean()   # measured 2e-3 on C1 (MFMA accumulation, as above)
+    da = np.abs(tab[d["act_q"]] - tab[qref])[diff]
+    # one e4m3 step (2^-9 below 2^-6, else at most an eighth of the larger
+    # value) plus the accumulation error, 1e-4 of the group's amax (448 in code
+    # units): a near-cancelling up projection can move a subnormal code by a few
+    big = np.maximum(np.abs(tab[d["act_q"]]), np.abs(tab[qref]))[diff]
+    bad = da > 0.125 * big + 2.0 ** -9 + TOL_F32 * 448
+    if bad.any():
+        gq, rq = tab[d["act_q"]][diff][bad], tab[qref][diff][bad]
+        print("codes off by more than one step (gpu, float64 chain):", list(zip(gq[:8], rq[:8])))
+        print("rows", np.nonzero(diff)[0][bad][:8], "gate/up", gate[diff][bad][:4], up[diff][bad][:4])
+    assert not bad.any()
+    return err
+
+
+@pytest.mark.parametrize("gemm", ["auto", "wide"])
+def test_moe_c1_tiny_f32(gemm, monkeypatch):
     """BASELINE config C1 shape: f32, H=256, I=128, E=8, top-2 + shared, 64
-    tokens, x and weights ~ N(0, 0.02), zero bias."""
+    tokens, x and weights ~ N(0, 0.02), zero bias; on the default GEMMs and on
+    the tall tiles (their down epilogue does the combine): the chain against
+    the oracle, and the stages at f32 bounds."""
+    if gemm == "wide":
+        monkeypatch.setenv("XS_MOE_GEMM", "wide")
     c = make_case(64, 256, 128, 8, 2, seed=11, x_std=0.02, bf16=False, bias_std=0)
-    _run_and_check(c, to_device(c), router_exact=True)
+    g = to_device(c)
+    _run_and_check(c, g, router_exact=True)
+    T, E, k, I, H = 64, 8, 2, 128, 256
+    R = T * k + T
+    dbg = _debug(T, E, k)
+    dbg.update(act_q=torch.empty((R, I), dtype=torch.uint8, device="cuda"),
+               act_s=torch.empty((R, I // 128), dtype=torch.float32, device="cuda"),
+               y_rows=torch.empty((R, H), dtype=torch.float32, device="cuda"))
+    out = layer_for(c, g, router_exact=True).forward(g["x"], debug=dbg)
+    torch.cuda.synchronize()
+    _check_f32_stages(c, g, {n: t.cpu().numpy() for n, t in dbg.items()}, out)
+
+
+@pytest.mark.parametrize("fuse", ["0", "1"])
+def test_moe_f32_stages_bf16_wide(fuse, monkeypatch):
+    """The same stage bounds for a bf16 layer on the tall tiles with multi-tile
+    experts, with the separate combine and with the one fused into the down
+    GEMM's epilogue (either rounds once to bf16)."""
+    monkeypatch.setenv("XS_MOE_GEMM", "wide")
+    monkeypatch.setenv("XS_FUSE_COMBINE", fuse)
+    c = make_case(300, 256, 256, 4, 2, seed=12, zipf=1.1)
+    g = to_device(c)
+    T, E, k, I, H = 300, 4, 2, 256, 256
+    R = T * k + T
+    dbg = _debug(T, E, k)
+    dbg.update(act_q=torch.empty((R, I), dtype=torch.uint8, device="cuda"),
+               act_s=torch.empty((R, I // 128), dtype=torch.float32, device="cuda"),
+               y_rows=torch.empty((R, H), dtype=torch.float32, device="cuda"))
+    out = layer_for(c, g, router_exact=True).forward(g["x"], debug=dbg)
+    torch.cuda.synchronize()
+    _check_f32_stages(c, g, {n: t.cpu().numpy() for n, t in dbg.items()}, out)
+
+
+def _targeted_rows(counts, offsets, perm, k, T, bm):
+    """Tokens whose rows land where tile bugs show: the first and the last rows
+    of the hottest expert (a full tile and its ragged last tile), the first row
+    of its second tile, the last row of the coldest used expert, a single-row
+    expert when there is one, and the shared segment's first and last tokens
+    (the last one sits in a ragged shared tile unless T % bm == 0)."""
+    hot = int(np.argmax(counts))
+    pos = [offsets[hot], offsets[hot] + min(bm, counts[hot]) - 1, offsets[hot + 1] - 1]
+    if counts[hot] > bm:
+        pos.append(offsets[hot] + bm)
+    used = np.flatnonzero(counts > 0)
+    cold = used[np.argmin(counts[used])]
+    pos.append(offsets[cold + 1] - 1)
+    ones = np.flatnonzero(counts == 1)
+    if ones.size:
+        pos.append(offsets[ones[0]])
+    toks = {int(perm[p]) // k for p in pos} | {0, T - 1}
+    return np.array(sorted(toks))
 
 
 @pytest.mark.parametrize("T,H,I,E,k,shared", [
@@ -105,6 +232,36 @@ def test_moe_stream_decode(T, H, I, E, k, zipf, seed, monkeypatch):
     assert max_abs_rel(outs[0], outs[2]) <= 1e-2
 
 
+@pytest.mark.parametrize("bf16", [True, False])
+def test_moe_fused_combine_matches_separate(bf16, monkeypatch):
+    """The tall-tile down GEMM's fused combine (the block that stores a token's
+    last row sums its rows) against the separate combine kernel: the sum order
+    is fixed, so the outputs are identical bit for bit, with and without a
+    residual and with the residual aliasing the output; repeated calls agree
+    (the counters are re-armed every forward)."""
+    monkeypatch.setenv("XS_MOE_GEMM", "wide")
+    c = make_case(700, 1024, 1024, 16, 4, seed=21, zipf=1.1, bf16=bf16)
+    g = to_device(c)
+    layer = layer_for(c, g, router_exact=True)
+    res = torch.randn(700, 1024, device="cuda").to(g["x"].dtype)
+    outs = {}
+    for fuse in ("1", "0"):
+        monkeypatch.setenv("XS_FUSE_COMBINE", fuse)
+        a = layer.forward(g["x"])
+        b = layer.forward(g["x"])
+        r = layer.forward(g["x"], residual=res)
+        inplace = res.clone()
+        layer.forward(g["x"], out=inplace, residual=inplace)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
+        assert torch.equal(r, inplace)
+        outs[fuse] = (a, r)
+    assert torch.equal(outs["1"][0], outs["0"][0])
+    assert torch.equal(outs["1"][1], outs["0"][1])
+    ref = oracle_forward(c)["out_f32"]
+    assert max_abs_rel(outs["1"][0].float().cpu().numpy(), ref) <= TOL
+
+
 def test_moe_group_limited_and_scaling():
     c = make_case(96, 512, 128, 32, 4, seed=3)
     g = to_device(c)
@@ -137,10 +294,52 @@ def test_moe_v4_decode_full_shape(T):
     _run_and_check(c, g, router_exact=False)
 
 
+def test_moe_v4_decode_zero_bias():
+    """C4 as specified: uniform routing with zero router bias, 16 tokens."""
+    c, g = make_case_gpu(16, 4096, 2048, 256, 6, seed=44, bias_std=0)
+    _run_and_check(c, g, router_exact=False)
+
+
 def test_moe_fp4_full_shape():
     """C5 shape (H=4096, I=2048, 256 MXFP4 experts top-6 + FP8 shared) at 32 tokens."""
     c, g = make_case_gpu(32, 4096, 2048, 256, 6, seed=7, fp4=True)
     _run_and_check(c, g, router_exact=False)
+
+
+def _full_size_check(c, g, T, E, k, bm, exact=False):
+    """Routing, counts, offsets, permutation and inverse bit-exact against the
+    oracle (on the GPU logits, or from x with the exact router); the targeted
+    rows' outputs against the oracle run on those tokens."""
+    layer = layer_for(c, g, router_exact=exact)
+    dbg = _debug(T, E, k)
+    out = layer.forward(g["x"], debug=dbg)
+    torch.cuda.synchronize()
+    d = {n: t.cpu().numpy() for n, t in dbg.items()}
+    logits = d["logits"] if not exact else oracle.router_logits(c["x"], c["router_w"])
+    if exact:
+        assert np.array_equal(d["logits"], logits)
+    ridx, rw = oracle.route(logits, c["bias"], k)
+    assert np.array_equal(d["topk_idx"], ridx) and np.array_equal(d["topk_w"], rw)
+    rc, ro, rp, ri = oracle.permute(ridx, E)
+    assert np.array_equal(d["counts"], rc) and np.array_equal(d["offsets"], ro[:E + 1])
+    assert np.array_equal(d["perm"], rp) and np.array_equal(d["inv"], ri)
+    rows = _targeted_rows(rc, ro, rp, k, T, bm)
+    r = oracle_forward(c, logits_in=np.ascontiguousarray(logits[rows]), rows=rows)
+    got = out.float().cpu().numpy()[rows]
+    err = max_abs_rel(got, r["out_f32"])
+    print(f"T={T} rows={rows.tolist()} max-abs-rel={err:.3e}")
+    assert err <= TOL, err
+    return d, out
+
+
+def test_moe_fp4_c5_full_size():
+    """C5 at its benchmark workload: 2048 tokens, 256 MXFP4 experts top-6 + FP8
+    shared, the persistent 64-row FP4 tiles the benchmark runs; targeted rows
+    hit the hottest expert's full and ragged tiles, a cold expert and the
+    shared segment."""
+    T, E, k = 2048, 256, 6
+    c, g = make_case_gpu(T, 4096, 2048, E, k, seed=17, fp4=True, bias_std=0)
+    _full_size_check(c, g, T, E, k, bm=64)
 
 
 def test_moe_prefill_full_size_properties():
@@ -161,7 +360,7 @@ def test_moe_prefill_full_size_properties():
     assert np.array_equal(d["perm"], rp) and np.array_equal(d["inv"], ri)
     # Zipf(1.1) profile: a head of experts with thousands of tokens, every expert used
     assert rc.max() > 16 * rc.mean() and (rc > 0).all()
-    rows = np.array([0, 1, 777, 4096, 5000, 8191])
+    rows = np.union1d([0, 1, 777, 4096, 5000, 8191], _targeted_rows(rc, ro, rp, k, T, 192))
     r = oracle_forward(c, logits_in=np.ascontiguousarray(d["logits"][rows]), rows=rows)
     got = out.float().cpu().numpy()[rows]
     assert max_abs_rel(got, r["out_f32"]) <= TOL

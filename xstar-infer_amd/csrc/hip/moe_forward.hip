@@ -39,7 +39,7 @@ static int prof_mark(int stage, hipStream_t st)
 
 struct WsLayout {
     size_t logits, idx, w, mask, wordprefix, counts, offsets, perm, inv, row_token, tiles, tiletab, part, cnt1, cnt2;
-    size_t xn, xq, xs, xmq, xms, actq, acts, actms, y;
+    size_t xn, xq, xs, xmq, xms, actq, acts, actms, y, ccnt;
     size_t total;
 };
 
@@ -70,6 +70,15 @@ static bool getenv_flag(const char *name, bool dflt)
 {
     const char *v = getenv(name);
     return v ? v[0] != '0' : dflt;
+}
+
+// XS_FUSE_COMBINE=1: the tall-tile down GEMM sums each token's rows itself
+// (moe_gemm_wide.hip, store_f32_tile) instead of the separate combine launch.
+// Same bits; measured slower at prefill (the block that completes a token
+// holds its CU through the gather), so it is off by default.
+static bool fuse_combine(const xs_moe_params *p)
+{
+    return use_wide(p) && getenv_flag("XS_FUSE_COMBINE", false);
 }
 
 static int use_stream(const xs_moe_params *p)
@@ -127,7 +136,8 @@ static WsLayout layout(const xs_moe_params *p)
     take(L.actq, R * I);
     take(L.acts, 4 * R * (I / 128));
     take(L.actms, fp4 ? S * (I / 32) : 0);
-    take(L.y, 2 * R * H);
+    take(L.y, 4 * R * H);
+    take(L.ccnt, fuse_combine(p) ? 4 * T * (H / 256) : 0);
     L.total = o;
     return L;
 }
@@ -256,9 +266,13 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     const int stream_tiles = fp4 ? routed_tiles : routed_tiles + shared_tiles;
     const bool stream = stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
                         (sm == 2 || (sm == 1 && stream_items(true, (int)I, stream_tiles) >= 2 * (int64_t)stream_blocks()));
+    const bool fused = fuse_combine(p);
     if (stream) {
         po.zero = WS(int32_t, cnt1);
         po.zero_n = stream_items(true, (int)I, tiles16_max(p)) + 1;
+    } else if (fused) {
+        po.zero = WS(int32_t, ccnt);
+        po.zero_n = T * (H / 256);
     }
     rc = launch_permute(idx, mask, T, E, k, shared_rows, WS(int32_t, wordprefix), po, st);
     if (rc) return rc;
@@ -292,8 +306,21 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     g2.K = (int)I;
     g2.N = (int)H;
     g2.bm = bm;
-    g2.Cy = WS(uint16_t, y);
+    g2.Cf = WS(float, y);
     g2.ldc = H;
+    if (fused) {
+        g2.fuse_combine = 1;
+        g2.pos_token = po.row_token;
+        g2.inv = inv;
+        g2.cw = w;
+        g2.topk = (int)k;
+        g2.has_shared = shared_rows ? 1 : 0;
+        g2.shared_base = S;
+        g2.ccnt = WS(int32_t, ccnt);
+        g2.out = t->out;
+        g2.residual = t->residual;
+        g2.out_dtype = p->x_dtype;
+    }
 
     if (stream) {
         g1.part = g2.part = WS(float, part);
@@ -360,9 +387,11 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     }
     // 5. weighted combine (+ shared), one cast to the output dtype
     if ((rc = prof_mark(6, st))) return rc;
-    rc = launch_combine(WS(uint16_t, y), inv, w, T, k, H, S, shared_rows ? 1 : 0, t->out, p->x_dtype, st,
-                        t->residual);
-    if (rc) return rc;
+    if (!fused) {
+        rc = launch_combine(WS(float, y), inv, w, T, k, H, S, shared_rows ? 1 : 0, t->out, p->x_dtype, st,
+                            t->residual);
+        if (rc) return rc;
+    }
     if ((rc = prof_mark(7, st))) return rc;
 
     // optional inspection outputs
@@ -376,6 +405,12 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     if ((rc = cp(t->offsets, offsets, 4 * (size_t)(E + 1)))) return rc;
     if ((rc = cp(t->perm, po.perm, 4 * (size_t)S))) return rc;
     if ((rc = cp(t->inv, inv, 4 * (size_t)S))) return rc;
+    const size_t R = (size_t)(S + shared_rows);
+    if (!fp4) {
+        if ((rc = cp(t->act_q, WS(uint8_t, actq), R * (size_t)I))) return rc;
+        if ((rc = cp(t->act_s, WS(float, acts), 4 * R * (size_t)(I / 128)))) return rc;
+    }
+    if ((rc = cp(t->y_rows, WS(float, y), 4 * R * (size_t)H))) return rc;
 #undef WS
     return XS_OK;
 }

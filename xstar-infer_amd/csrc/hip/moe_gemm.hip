@@ -447,6 +447,17 @@ __global__ __launch_bounds__(BM >= 64 ? 512 : 256) void moe_gemm_kernel(GemmArgs
             *reinterpret_cast<v4i *>(a.Cq + (size_t)(pos0 + r) * a.N + n0 + c * 16) =
                 *reinterpret_cast<const v4i *>(stg + r * SROW + c * 16);
         }
+    } else if (a.Cf) {
+        // f32 rows, straight from the accumulators: a lane's 4 columns are one
+        // 16-byte store (these tiles serve small batches; y is small)
+#pragma unroll
+        for (int i = 0; i < S::MI; ++i)
+#pragma unroll
+            for (int j = 0; j < S::NJ; ++j) {
+                const int r = wm * S::TM + 16 * i + l16;
+                const int c = n0 + wn * S::TN + 16 * j + 4 * g;
+                if (r < rows && c < a.N) *reinterpret_cast<v4f *>(a.Cf + (size_t)(pos0 + r) * a.ldc + c) = acc[i][j];
+            }
     } else {
         constexpr int SROW = 264;         // staging row stride (bf16 elements): conflict-free 8-byte writes
         uint16_t *stg = reinterpret_cast<uint16_t *>(smem);   // [BM][SROW] bf16
@@ -531,71 +542,86 @@ int launch_gemm(const GemmArgs &a, bool gateup, bool fp4, int grid_y, hipStream_
 // are in flight together.
 // The expert outputs are read exactly once: non-temporal loads (measured at
 // C3: combine 105 -> 93 us).
-__device__ __forceinline__ void load8_nt(const uint16_t *p, float *v)
+// 8 f32 values read once (the per-slot rows are not read again)
+__device__ __forceinline__ void load8_nt(const float *p, float *v)
 {
-    const v4i r = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(p));
+    const v4f a = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p));
+    const v4f b = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p + 4));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        v[2 * i] = __uint_as_float((uint32_t)r[i] << 16);
-        v[2 * i + 1] = __uint_as_float((uint32_t)r[i] & 0xFFFF0000u);
+        v[i] = a[i];
+        v[4 + i] = b[i];
     }
 }
 
-template <typename OutT>
-__global__ __launch_bounds__(512) void combine_kernel(const uint16_t *__restrict__ y,
+// One block per token, 8 columns per thread.  The top-k is a template
+// argument, so every row's loads are issued before the first add (the gather
+// is latency-bound otherwise).  Sum order: shared row, then slots 0 .. k-1 as
+// acc + w_j * y_j (each product and sum rounded), then the residual; one cast.
+template <typename OutT, int K>
+__global__ __launch_bounds__(512) void combine_kernel(const float *__restrict__ y,
                                                       const int32_t *__restrict__ inv,
-                                                      const float *__restrict__ w, int k, int H,
+                                                      const float *__restrict__ w, int H,
                                                       int64_t shared_base, int has_shared,
                                                       const OutT *residual, OutT *out)
 {
+#pragma clang fp contract(off)
     const int t = blockIdx.x;
-    int pos[16];
-    float wt[16];
+    int pos[K];
+    float wt[K];
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-        if (j < k) {
-            pos[j] = inv[(size_t)t * k + j];
-            wt[j] = w[(size_t)t * k + j];
-        }
+    for (int j = 0; j < K; ++j) {
+        pos[j] = inv[(size_t)t * K + j];
+        wt[j] = w[(size_t)t * K + j];
+    }
     for (int c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
-        float acc[8];
+        float acc[8], v[K][8], r[8];
         if (has_shared) load8_nt(y + (size_t)(shared_base + t) * H + c, acc);
         else
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[i] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            if (j < k) {
-                float v[8];
-                load8_nt(y + (size_t)pos[j] * H + c, v);
+        for (int j = 0; j < K; ++j) load8_nt(y + (size_t)pos[j] * H + c, v[j]);
+        if (residual) load8(residual + (size_t)t * H + c, r);   // out may alias residual
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(wt[j], v[i]));
-            }
-        }
-        if (residual) {   // the block's residual add, before the one rounding (out may alias residual)
-            float r[8];
-            load8(residual + (size_t)t * H + c, r);
+        for (int j = 0; j < K; ++j)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(r[i], acc[i]);
-        }
+            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + wt[j] * v[j][i];   // no contraction (pragma above)
+        if (residual)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = r[i] + acc[i];
         store8(out + (size_t)t * H + c, acc);
     }
 }
 
-int launch_combine(const uint16_t *y, const int32_t *inv, const float *w, int64_t T, int64_t k,
+template <typename OutT, int K>
+static void launch_combine_k(int k, dim3 grid, dim3 block, hipStream_t st, const float *y, const int32_t *inv,
+                             const float *w, int H, int64_t shared_base, int has_shared, const void *residual,
+                             void *out)
+{
+    if constexpr (K > 1) {
+        if (k < K) {
+            launch_combine_k<OutT, K - 1>(k, grid, block, st, y, inv, w, H, shared_base, has_shared, residual, out);
+            return;
+        }
+    }
+    combine_kernel<OutT, K><<<grid, block, 0, st>>>(y, inv, w, H, shared_base, has_shared,
+                                                    (const OutT *)residual, (OutT *)out);
+}
+
+int launch_combine(const float *y, const int32_t *inv, const float *w, int64_t T, int64_t k,
                    int64_t H, int64_t shared_base, int has_shared, void *out, int out_dtype,
                    hipStream_t st, const void *residual)
 {
     if (T == 0) return XS_OK;
+    if (k < 1 || k > 16) return set_error(XS_ERR_INVALID, "combine: top_k %lld outside [1, 16]", (long long)k);
     const int nt = (int)(H / 8 < 64 ? 64 : (H / 8 > 512 ? 512 : (H / 8 + 63) / 64 * 64));
     if (out_dtype == XS_BF16)
-        combine_kernel<uint16_t><<<dim3((unsigned)T), dim3(nt), 0, st>>>(y, inv, w, (int)k, (int)H, shared_base,
-                                                                         has_shared, (const uint16_t *)residual,
-                                                                         (uint16_t *)out);
+        launch_combine_k<uint16_t, 16>((int)k, dim3((unsigned)T), dim3(nt), st, y, inv, w, (int)H, shared_base,
+                                       has_shared, residual, out);
     else
-        combine_kernel<float><<<dim3((unsigned)T), dim3(nt), 0, st>>>(y, inv, w, (int)k, (int)H, shared_base,
-                                                                      has_shared, (const float *)residual,
-                                                                      (float *)out);
+        launch_combine_k<float, 16>((int)k, dim3((unsigned)T), dim3(nt), st, y, inv, w, (int)H, shared_base,
+                                    has_shared, residual, out);
     XS_LAUNCH_CHECK();
     return XS_OK;
 }

@@ -25,8 +25,24 @@ struct GemmArgs {
     int xcd_order;             // tall-tile kernels: work grouped per XCD (set by launch_gemm_wide)
     uint8_t *Cq;               // gate_up: act rows [*, I] FP8
     void *Cs;                  // gate_up: f32 [*, I/128] or e8m0 [*, I/32]
-    uint16_t *Cy;              // down: bf16 rows [*, ldc]
+    uint16_t *Cy;              // down: bf16 rows [*, ldc] (the single GEMM's output)
+    float *Cf;                 // down: f32 rows [*, ldc] (the MoE layer's per-slot outputs); set: used instead of Cy
     int64_t ldc;
+    // down GEMM with the weighted combine fused into its epilogue (tall tiles):
+    // each (token, 256-column slab) counter counts the token's rows stored so
+    // far; the block whose rows complete a token sums them in f32 in the fixed
+    // order (shared, then slots 0..k-1, then residual) and writes out.
+    int fuse_combine;
+    const int32_t *pos_token;  // position -> token (routed rows, then the shared segment)
+    const int32_t *inv;        // [T, k] slot -> position
+    const float *cw;           // [T, k] combine weights
+    int topk;
+    int has_shared;            // shared row of token t at position shared_base + t
+    int64_t shared_base;
+    int32_t *ccnt;             // [T, H/256] counters, zero on entry
+    void *out;                 // [T, H] of out_dtype
+    const void *residual;      // [T, H] of out_dtype or NULL (may alias out)
+    int out_dtype;
     // persistent (stream-K) kernels, moe_gemm_stream.hip:
     float *part;               // partial tiles of split items: stream_part_bytes()
     int32_t *cnt;              // per-item arrival counters, zero on entry
@@ -48,7 +64,7 @@ bool stream_fits(int bm, bool fp4, int64_t tiles_max, int64_t rows_max);
 int64_t stream_items(bool gateup, int N, int64_t tiles_max);
 size_t stream_part_bytes(int64_t items_max, int K, int bm);
 int launch_gemm_stream(const GemmArgs &a, bool gateup, bool fp4, int tiles_max, int64_t rows_max, hipStream_t st);
-int launch_combine(const uint16_t *y, const int32_t *inv, const float *w, int64_t T, int64_t k,
+int launch_combine(const float *y, const int32_t *inv, const float *w, int64_t T, int64_t k,
                    int64_t H, int64_t shared_base, int has_shared, void *out, int out_dtype,
                    hipStream_t st, const void *residual = nullptr);
 

@@ -424,6 +424,10 @@ __global__ __launch_bounds__(kNT) void moe_gemm_stream_kernel(GemmArgs a)
                 for (int j = 0; j < C::NJ; ++j) {
                     const int c = n0 + 64 * wn + 16 * j + 4 * g;
                     if (c >= a.N) continue;
+                    if (a.Cf) {
+                        *reinterpret_cast<v4f *>(a.Cf + (size_t)(pos0 + r) * a.ldc + c) = acc[i][j];
+                        continue;
+                    }
                     v2i pk;
                     pk[0] = (int)((uint32_t)bf16_from_f32(acc[i][j][0]) | ((uint32_t)bf16_from_f32(acc[i][j][1]) << 16));
                     pk[1] = (int)((uint32_t)bf16_from_f32(acc[i][j][2]) | ((uint32_t)bf16_from_f32(acc[i][j][3]) << 16));

@@ -111,6 +111,120 @@ __device__ __forceinline__ void wait_vm()
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// 4 consecutive f32 values, read around the L2 (system scope): rows another
+// XCD stored with system-scope stores are seen without an L2 invalidation.
+__device__ __forceinline__ v4f load4_sys(const float *p)
+{
+    uint64_t *q = reinterpret_cast<uint64_t *>(const_cast<float *>(p));
+    const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return v4f{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)), __uint_as_float((uint32_t)b),
+               __uint_as_float((uint32_t)(b >> 32))};
+}
+
+// Down epilogue with f32 rows: acc[i][j][v] is token row 16 (wm + 2 i) + r16,
+// column n0 + 64 wn + 16 j + 4 g + v.  The tile is staged through the ring in
+// two halves (BM/2 rows of 1 KB each, padded to 1040 B) and stored as whole
+// rows.  With fuse_combine the rows are stored around the L2 (system scope),
+// then every row bumps its (token, slab) counter; a row that completes its
+// token (the counter reaches k + shared) puts the token on the block's list,
+// and the block sums the listed tokens' rows in the combine's fixed order:
+// shared row, then slots 0 .. k-1 as acc + w_j * y_j (each product and sum
+// rounded, no FMA), then the residual, and writes the slab of out with the
+// one cast.  The sum does not depend on which block finishes a token.
+template <int BM>
+__device__ __forceinline__ void store_f32_tile(const GemmArgs &a, const v4f (&acc)[BM / 32][4], int pos0, int rows,
+                                               int slab, int wm, int wn, uint8_t *smem, float *red)
+{
+#pragma clang fp contract(off)
+    constexpr int MI = BM / 32, HR = BM / 2, FS = 260;
+    static_assert(HR * FS * 4 <= kRing, "staging tile");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int n0 = slab * 256;
+    const bool fuse = a.fuse_combine != 0;
+    float *fs = reinterpret_cast<float *>(smem);
+    __syncthreads();   // every wave is past its loop: the ring is free for staging
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        // rows [h HR, h HR + HR) are the subtiles i in [h MI/2, h MI/2 + MI/2)
+#pragma unroll
+        for (int i = h * (MI / 2); i < (h + 1) * (MI / 2); ++i) {
+            const int rl = 16 * (wm + 2 * i) + r16 - h * HR;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *reinterpret_cast<v4f *>(fs + rl * FS + 64 * wn + 16 * j + 4 * g) = acc[i][j];
+        }
+        __syncthreads();
+        if (fuse) {
+#pragma unroll 4
+            for (int pass = 0; pass < HR / 4; ++pass) {
+                const int rl = 4 * pass + (tid >> 7), c = 2 * (tid & 127), row = h * HR + rl;
+                if (row < rows)
+                    __hip_atomic_store(reinterpret_cast<uint64_t *>(a.Cf + (size_t)(pos0 + row) * a.ldc + n0 + c),
+                                       *reinterpret_cast<const uint64_t *>(fs + rl * FS + c), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        } else {
+#pragma unroll 4
+            for (int pass = 0; pass < HR / 8; ++pass) {
+                const int rl = 8 * pass + (tid >> 6), c = 4 * (tid & 63), row = h * HR + rl;
+                if (row < rows)
+                    *reinterpret_cast<v4f *>(a.Cf + (size_t)(pos0 + row) * a.ldc + n0 + c) =
+                        *reinterpret_cast<const v4f *>(fs + rl * FS + c);
+            }
+        }
+        __syncthreads();   // the staging rows are free again
+    }
+    if (!fuse) return;
+
+    wait_vm<0>();          // this thread's rows have reached memory
+    int *lst = reinterpret_cast<int *>(red);   // [0]: count, [1 ..]: tokens this block completes
+    if (tid == 0) lst[0] = 0;
+    __syncthreads();       // ... every thread's, and the list is empty
+    const int nslab = a.N / 256, need = a.topk + a.has_shared;
+    if (tid < rows) {
+        const int t = a.pos_token[pos0 + tid];
+        const int old = __hip_atomic_fetch_add(a.ccnt + (size_t)t * nslab + slab, 1, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+        if (old == need - 1) lst[1 + atomicAdd(&lst[0], 1)] = t;
+    }
+    __syncthreads();
+    const int nl = lst[0];
+    const int c = n0 + 4 * lane;
+    for (int q = wave; q < nl; q += kNW) {
+        const int t = lst[1 + q];
+        v4f s = a.has_shared ? load4_sys(a.Cf + (size_t)(a.shared_base + t) * a.ldc + c) : v4f{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < a.topk; ++j) {
+            const int p = a.inv[(size_t)t * a.topk + j];
+            const float wt = a.cw[(size_t)t * a.topk + j];
+            const v4f y = load4_sys(a.Cf + (size_t)p * a.ldc + c);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) s[v] = s[v] + wt * y[v];   // no contraction (pragma above)
+        }
+        const size_t o = (size_t)t * a.N + c;
+        if (a.out_dtype == XS_BF16) {
+            if (a.residual) {
+                const v2i r = *reinterpret_cast<const v2i *>(reinterpret_cast<const uint16_t *>(a.residual) + o);
+                s[0] = __uint_as_float((uint32_t)r[0] << 16) + s[0];
+                s[1] = __uint_as_float((uint32_t)r[0] & 0xFFFF0000u) + s[1];
+                s[2] = __uint_as_float((uint32_t)r[1] << 16) + s[2];
+                s[3] = __uint_as_float((uint32_t)r[1] & 0xFFFF0000u) + s[3];
+            }
+            v2i pk;
+            pk[0] = (int)((uint32_t)bf16_from_f32(s[0]) | ((uint32_t)bf16_from_f32(s[1]) << 16));
+            pk[1] = (int)((uint32_t)bf16_from_f32(s[2]) | ((uint32_t)bf16_from_f32(s[3]) << 16));
+            *reinterpret_cast<v2i *>(reinterpret_cast<uint16_t *>(a.out) + o) = pk;
+        } else {
+            if (a.residual) {
+                const v4f r = *reinterpret_cast<const v4f *>(reinterpret_cast<const float *>(a.residual) + o);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) s[v] = r[v] + s[v];
+            }
+            *reinterpret_cast<v4f *>(reinterpret_cast<float *>(a.out) + o) = s;
+        }
+    }
+}
+
 #ifdef XS_WIDE_TRACE
 // Development builds only: per-block phase timestamps (100 MHz wall clock).
 __device__ uint64_t g_wide_trace[2][16384][6];
@@ -350,6 +464,8 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
                 *reinterpret_cast<v4i *>(a.Cq + (size_t)(pos0 + row) * a.N + n0 + 16 * c) =
                     *reinterpret_cast<const v4i *>(qs + row * QS + 16 * c);
         }
+    } else if (a.Cf) {
+        store_f32_tile<BM>(a, acc, pos0, rows, slab, wm, wn, smem, red);
     } else {
         // output column n0 + 64 wn + 16 j + 4 g + v.  The bf16 tile is staged in
         // the ring (rows padded to 528 B: a half-wave's 16-row x 2-lane 8-byte

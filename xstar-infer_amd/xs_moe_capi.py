@@ -32,7 +32,8 @@ class MoeTensors(C.Structure):
     _fields_ = [(n, P) for n in (
         "x", "router_w", "router_bias", "w13", "w13_scale", "w2", "w2_scale",
         "shared_w13", "shared_w13_scale", "shared_w2", "shared_w2_scale", "out",
-        "logits", "topk_idx", "topk_w", "counts", "offsets", "perm", "inv", "norm_weight", "residual")]
+        "logits", "topk_idx", "topk_w", "counts", "offsets", "perm", "inv", "norm_weight", "residual",
+        "act_q", "act_s", "y_rows")]
 
 
 EXPORTS = {
@@ -271,7 +272,8 @@ class MoeLayer:
 
     def forward(self, x, out=None, debug=None, residual=None):
         """debug: optional dict of preallocated device tensors with keys among
-        logits, topk_idx, topk_w, counts, offsets, perm, inv.  residual: optional
+        logits, topk_idx, topk_w, counts, offsets, perm, inv, act_q, act_s, y_rows
+        (shapes in include/xs_moe.h).  residual: optional
         [T, H] tensor (dtype of x) added to the output before its rounding; it
         may be `out` itself."""
         import torch
@@ -288,6 +290,7 @@ class MoeLayer:
                        _ptr(sh[1]), _ptr(sh[2]), _ptr(sh[3]), _ptr(out),
                        *[_ptr(d.get(n)) for n in ("logits", "topk_idx", "topk_w", "counts",
                                                  "offsets", "perm", "inv")],
-                       _ptr(self.norm_weight), _ptr(residual))
+                       _ptr(self.norm_weight), _ptr(residual),
+                       *[_ptr(d.get(n)) for n in ("act_q", "act_s", "y_rows")])
         check(lib().xs_moe_forward(C.byref(p), C.byref(t), _ptr(ws), ws.numel(), _stream()))
         return out
