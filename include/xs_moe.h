@@ -230,6 +230,23 @@ int xs_moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *worksp
                    size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
+ * xs_moe_forward without a caller workspace.  No counterpart in the reference:
+ * for callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation.  The layer's
+ * scratch lives in a static device array of XS_NOALLOC_SCRATCH_BYTES per GPU
+ * (held until the process ends); params whose workspace
+ * (xs_moe_workspace_size) exceeds it are rejected with XS_ERR_WORKSPACE (V4-Flash
+ * shape: FP8 up to 256 tokens, MXFP4 up to about 200).  Calls nothing that
+ * allocates.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams, or threads) race; calls in one
+ * stream order are safe, because each forward re-arms what must start at zero.
+ * Same semantics and outputs as xs_moe_forward.
+ * ------------------------------------------------------------------------- */
+#define XS_NOALLOC_SCRATCH_BYTES (64u * 1024u * 1024u)
+size_t xs_moe_noalloc_scratch_bytes(void);
+int xs_moe_forward_noalloc(const xs_moe_params *p, const xs_moe_tensors *t, void *stream);
+
+/* ---------------------------------------------------------------------------
  * Per-stage timing hook (no reference counterpart; the reference times ops with
  * torch.cuda.Event around whole calls, bench/bench_splitkv.py:86-105).  While
  * enabled, xs_moe_forward records a HIP event at each stage boundary on its

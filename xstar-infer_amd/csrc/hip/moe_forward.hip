@@ -9,6 +9,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 namespace xs {
 
@@ -439,11 +440,57 @@ static size_t gemm_ws(int64_t M, int64_t K, size_t *o_s, size_t *o_meta)
     return q + s + 256 + al(tile_table_bytes(M, 0, 1, 16));
 }
 
+// ------------------------------------------- forward without a caller workspace
+// The workspace of xs_moe_forward_noalloc: a fixed device array in the code
+// object, one copy per GPU, held until the process ends.  Host code never
+// passes `scratch` itself (on the host it names a stand-in, not device
+// memory): each device's address comes from hipGetSymbolAddress, taken once
+// per device with that device current.
+static constexpr size_t kNoallocScratch = (size_t)XS_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoallocScratch];
+
+static constexpr int kMaxDevices = 64;
+static void *g_scratch_ptr[kMaxDevices] = {};
+static std::mutex g_scratch_mu;
+
+static int scratch_for_current_device(void **out)
+{
+    int dev = 0;
+    XS_HIP(hipGetDevice(&dev));
+    XS_REQUIRE(dev >= 0 && dev < kMaxDevices, "device index %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        XS_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        XS_REQUIRE(p != nullptr && ((uintptr_t)p & 255) == 0, "scratch symbol address is null or misaligned");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return XS_OK;
+}
+
 }  // namespace xs
 
 using namespace xs;
 
 extern "C" {
+
+size_t xs_moe_noalloc_scratch_bytes(void) { return kNoallocScratch; }
+
+int xs_moe_forward_noalloc(const xs_moe_params *p, const xs_moe_tensors *t, void *stream)
+{
+    int rc = check_params(p);
+    if (rc) return rc;
+    const size_t need = layout(p).total;
+    if (need > kNoallocScratch)
+        return set_error(XS_ERR_WORKSPACE,
+                         "xs_moe_forward_noalloc: these params need %zu bytes of scratch; the static scratch holds %zu "
+                         "(use xs_moe_forward with a workspace)",
+                         need, kNoallocScratch);
+    void *ws = nullptr;
+    if ((rc = scratch_for_current_device(&ws))) return rc;
+    return moe_forward(p, t, ws, kNoallocScratch, (hipStream_t)stream);
+}
 
 size_t xs_moe_workspace_size(const xs_moe_params *p)
 {

@@ -59,6 +59,8 @@ EXPORTS = {
     "xs_gemm_fp8_blockscale": (C.c_int, [P, P, P, I64, I64, I64, P, P, C.c_size_t, P]),
     "xs_moe_workspace_size": (C.c_size_t, [P]),
     "xs_moe_forward": (C.c_int, [P, P, P, C.c_size_t, P]),
+    "xs_moe_noalloc_scratch_bytes": (C.c_size_t, []),
+    "xs_moe_forward_noalloc": (C.c_int, [P, P, P]),
     "xs_moe_profile_enable": (C.c_int, [C.c_int]),
     "xs_moe_profile_read": (C.c_int, [P, C.c_int, P]),
 }
@@ -293,4 +295,17 @@ class MoeLayer:
                        _ptr(self.norm_weight), _ptr(residual),
                        *[_ptr(d.get(n)) for n in ("act_q", "act_s", "y_rows")])
         check(lib().xs_moe_forward(C.byref(p), C.byref(t), _ptr(ws), ws.numel(), _stream()))
+        return out
+
+    def forward_noalloc(self, x, out):
+        """The same forward through xs_moe_forward_noalloc: the library's static
+        scratch instead of a workspace; `out` is preallocated by the caller."""
+        T = x.shape[0]
+        p = self.params(T, _dtype_code(x))
+        sh = self.shared or (None, None, None, None)
+        t = MoeTensors(_ptr(x), _ptr(self.router_w), _ptr(self.router_bias), _ptr(self.w13),
+                       _ptr(self.w13_scale), _ptr(self.w2), _ptr(self.w2_scale), _ptr(sh[0]),
+                       _ptr(sh[1]), _ptr(sh[2]), _ptr(sh[3]), _ptr(out), *([None] * 7),
+                       _ptr(self.norm_weight), None, None, None, None)
+        check(lib().xs_moe_forward_noalloc(C.byref(p), C.byref(t), _stream()))
         return out
