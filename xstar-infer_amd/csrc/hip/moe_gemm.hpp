@@ -23,6 +23,7 @@ struct GemmArgs {
     int bm;                    // tile rows: 16, 32, 64 or 128
     int stream_w;              // tiled kernels: non-temporal weight loads (large launches)
     int xcd_order;             // tall-tile kernels: work grouped per XCD (set by launch_gemm_wide)
+    int short_deep;            // tall-tile kernels: tiles of <= 64 rows run 64-row stages, 4 weight stages
     uint8_t *Cq;               // gate_up: act rows [*, I] FP8
     void *Cs;                  // gate_up: f32 [*, I/128] or e8m0 [*, I/32]
     uint16_t *Cy;              // down: bf16 rows [*, ldc] (the single GEMM's output)

@@ -39,15 +39,16 @@
 namespace xs {
 namespace {
 
-constexpr int kNW = 8;               // waves per block
-constexpr int kNT = 64 * kNW;        // threads
 constexpr int kRing = 148 * 1024;    // LDS bytes of the operand ring
 constexpr int kTrash = 1024;         // LDS target of padding DMAs
 
-template <int BM, bool DEEP_A>
+// Ring modes: 0 = 2 activation + 3 weight stages, 1 = 3 + 2, 2 = 2 + 4, 3 = 3 + 3.
+// NW waves per block: 4 along the weight rows times NW / 4 along the tokens.
+template <int BM, int MODE, int NW>
 struct WCfg {
+    static constexpr int WM = NW / 4;                      // waves along the tokens
     static constexpr int NS16 = BM / 16;                   // 16-token subtiles per tile
-    static constexpr int MI = NS16 / 2;                    // per wave row
+    static constexpr int MI = NS16 / WM;                   // subtiles per wave: s16 = wm + WM i
     static constexpr int A_BYTES = BM * 128;               // activation rows of one K step
     static constexpr int W_BYTES = 256 * 128;              // weight rows of one K step
     static constexpr int S_BYTES = BM * 4;                 // activation row scales
@@ -57,11 +58,11 @@ struct WCfg {
     // with several tiles, whose weight slabs the tiles share through L2) wait on
     // their activation rows: 3 + 2 stages.  Shorter tiles stream their weights
     // from HBM: 2 + 3 stages.
-    static constexpr int NAR = DEEP_A ? 3 : 2;
-    static constexpr int NWR = DEEP_A ? 2 : 3;
+    static constexpr int NAR = (MODE == 1 || MODE == 3) ? 3 : 2;
+    static constexpr int NWR = MODE == 1 ? 2 : (MODE == 2 ? 4 : 3);
     static constexpr int DA = NAR - 1, DW = NWR - 1;
-    static constexpr int NA = BM / 8 / kNW;                // 1 KB activation DMAs per wave and step
-    static constexpr int NB = 256 / 8 / kNW;               // 1 KB weight DMAs per wave and step
+    static constexpr int NA = BM / 8 / NW;                 // 1 KB activation DMAs per wave and step
+    static constexpr int NB = 256 / 8 / NW;                // 1 KB weight DMAs per wave and step
     static constexpr int NSA = S_BYTES / 256;              // scale DMAs (waves 0 .. NSA-1)
     static constexpr int PER_STEP = NA + NB + 1;           // loads per wave per step
     // Each iteration issues the operand with the shorter prefetch distance first.
@@ -73,6 +74,7 @@ struct WCfg {
     static constexpr int X = XW < XA ? XW : XA;
     static constexpr int PRO = DA > DW ? DA : DW;          // prologue iterations
     static_assert(BM % 64 == 0 && DA >= 1 && DW >= 1 && NAR * AS_BYTES + NWR * W_BYTES <= kRing, "tile");
+    static_assert(NA >= 1 && NSA <= NW && MI % 2 == 0, "waves");
 };
 
 __device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }
@@ -132,12 +134,12 @@ __device__ __forceinline__ v4f load4_sys(const float *p)
 // shared row, then slots 0 .. k-1 as acc + w_j * y_j (each product and sum
 // rounded, no FMA), then the residual, and writes the slab of out with the
 // one cast.  The sum does not depend on which block finishes a token.
-template <int BM>
-__device__ __forceinline__ void store_f32_tile(const GemmArgs &a, const v4f (&acc)[BM / 32][4], int pos0, int rows,
-                                               int slab, int wm, int wn, uint8_t *smem, float *red)
+template <int BM, int NW>
+__device__ __forceinline__ void store_f32_tile(const GemmArgs &a, const v4f (&acc)[BM / 16 / (NW / 4)][4], int pos0,
+                                               int rows, int slab, int wm, int wn, uint8_t *smem, float *red)
 {
 #pragma clang fp contract(off)
-    constexpr int MI = BM / 32, HR = BM / 2, FS = 260;
+    constexpr int WM = NW / 4, MI = BM / 16 / WM, HR = BM / 2, FS = 260, NT = 64 * NW;
     static_assert(HR * FS * 4 <= kRing, "staging tile");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
@@ -150,15 +152,15 @@ __device__ __forceinline__ void store_f32_tile(const GemmArgs &a, const v4f (&ac
         // rows [h HR, h HR + HR) are the subtiles i in [h MI/2, h MI/2 + MI/2)
 #pragma unroll
         for (int i = h * (MI / 2); i < (h + 1) * (MI / 2); ++i) {
-            const int rl = 16 * (wm + 2 * i) + r16 - h * HR;
+            const int rl = 16 * (wm + WM * i) + r16 - h * HR;
 #pragma unroll
             for (int j = 0; j < 4; ++j) *reinterpret_cast<v4f *>(fs + rl * FS + 64 * wn + 16 * j + 4 * g) = acc[i][j];
         }
         __syncthreads();
         if (fuse) {
 #pragma unroll 4
-            for (int pass = 0; pass < HR / 4; ++pass) {
-                const int rl = 4 * pass + (tid >> 7), c = 2 * (tid & 127), row = h * HR + rl;
+            for (int pass = 0; pass < HR / (NT / 128); ++pass) {
+                const int rl = (NT / 128) * pass + (tid >> 7), c = 2 * (tid & 127), row = h * HR + rl;
                 if (row < rows)
                     __hip_atomic_store(reinterpret_cast<uint64_t *>(a.Cf + (size_t)(pos0 + row) * a.ldc + n0 + c),
                                        *reinterpret_cast<const uint64_t *>(fs + rl * FS + c), __ATOMIC_RELAXED,
@@ -166,8 +168,8 @@ __device__ __forceinline__ void store_f32_tile(const GemmArgs &a, const v4f (&ac
             }
         } else {
 #pragma unroll 4
-            for (int pass = 0; pass < HR / 8; ++pass) {
-                const int rl = 8 * pass + (tid >> 6), c = 4 * (tid & 63), row = h * HR + rl;
+            for (int pass = 0; pass < HR / (NT / 64); ++pass) {
+                const int rl = (NT / 64) * pass + (tid >> 6), c = 4 * (tid & 63), row = h * HR + rl;
                 if (row < rows)
                     *reinterpret_cast<v4f *>(a.Cf + (size_t)(pos0 + row) * a.ldc + n0 + c) =
                         *reinterpret_cast<const v4f *>(fs + rl * FS + c);
@@ -191,7 +193,7 @@ __device__ __forceinline__ void store_f32_tile(const GemmArgs &a, const v4f (&ac
     __syncthreads();
     const int nl = lst[0];
     const int c = n0 + 4 * lane;
-    for (int q = wave; q < nl; q += kNW) {
+    for (int q = wave; q < nl; q += NW) {
         const int t = lst[1 + q];
         v4f s = a.has_shared ? load4_sys(a.Cf + (size_t)(a.shared_base + t) * a.ldc + c) : v4f{0.f, 0.f, 0.f, 0.f};
         for (int j = 0; j < a.topk; ++j) {
@@ -235,10 +237,11 @@ __device__ uint64_t g_wide_trace[2][16384][6];
 #define XS_WTRACE(ev)
 #endif
 
-template <int BM, bool GATEUP, bool FULL, bool DEEP_A>
+template <int BM, bool GATEUP, bool FULL, int MODE, int NW>
 __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int rows, int slab, uint8_t *smem)
 {
-    using C = WCfg<BM, DEEP_A>;
+    using C = WCfg<BM, MODE, NW>;
+    constexpr int kNW = NW, kNT = 64 * NW;
     const int KB = a.K / 128;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -328,10 +331,10 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         wrow[j] = GATEUP ? (j < 2 ? 0 : 128) + 32 * wn + 16 * (j & 1) + r16 : 64 * wn + 16 * j + r16;
-    // 16-token subtiles of this wave: s16 = wm + 2 i, live when 16 s16 < rows
+    // 16-token subtiles of this wave: s16 = wm + WM i, live when 16 s16 < rows
     int nlive = 0;
 #pragma unroll
-    for (int i = 0; i < C::MI; ++i) nlive += 16 * (wm + 2 * i) < rows ? 1 : 0;
+    for (int i = 0; i < C::MI; ++i) nlive += 16 * (wm + C::WM * i) < rows ? 1 : 0;
 
     v4f acc[C::MI][4];
 #pragma unroll
@@ -360,7 +363,7 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
         // wait for that prefetch.
         float sav[C::MI];
 #pragma unroll
-        for (int i = 0; i < C::MI; ++i) sav[i] = (FULL || i < nlive) ? sS[16 * (wm + 2 * i) + r16] : 0.f;
+        for (int i = 0; i < C::MI; ++i) sav[i] = (FULL || i < nlive) ? sS[16 * (wm + C::WM * i) + r16] : 0.f;
         // Operand layout of v_mfma_f32_16x16x128_f8f6f4: lane 16g + r holds row r
         // with K bytes [16g, 16g+16) and [64+16g, 64+16g+16): LDS chunks g, g+4.
         v8i wf[4];
@@ -371,7 +374,7 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
                         *reinterpret_cast<const v4i *>(rp + swz8(wrow[j], g + 4) * 16));
         }
         auto read_b = [&](int i) -> v8i {
-            const int row = 16 * (wm + 2 * i) + r16;
+            const int row = 16 * (wm + C::WM * i) + r16;
             const uint8_t *rp = sA + row * 128;
             return cat(*reinterpret_cast<const v4i *>(rp + swz8(row, g) * 16),
                        *reinterpret_cast<const v4i *>(rp + swz8(row, g + 4) * 16));
@@ -403,6 +406,19 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
                     for (int v = 0; v < 4; ++v) acc[m][j][v] = __builtin_fmaf(q[m & 1][j][v], c, acc[m][j][v]);
                 }
             }
+            if (FULL && i >= 1 && i < C::MI) {
+                // Issue order of the region: the fragment prefetch, then each
+                // MFMA of subtile i followed by a share of the fold of i-1, whose
+                // products finished during the previous region.  Left to itself
+                // the scheduler puts the whole fold first, where it waits on the
+                // MFMAs that produced it while the matrix core idles.
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS reads
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);   // VALU
+                }
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -410,7 +426,7 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
     XS_WTRACE(2);
 
     // ------------------------------------------------------------ epilogue
-    // acc[i][j][v]: token row 16 (wm + 2 i) + r16; A-tile j row 4 g + v.
+    // acc[i][j][v]: token row 16 (wm + WM i) + r16; A-tile j row 4 g + v.
     if (GATEUP) {
         // act feature (within the block's 128): 32 wn + 16 jj + 4 g + v, jj = 0, 1
         float act[C::MI][2][4];
@@ -427,7 +443,7 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
                 }
             m = fmaxf(m, __shfl_xor(m, 16, WAVE));
             m = fmaxf(m, __shfl_xor(m, 32, WAVE));
-            if (g == 0) red[wn * BM + 16 * (wm + 2 * i) + r16] = m;
+            if (g == 0) red[wn * BM + 16 * (wm + C::WM * i) + r16] = m;
         }
         __syncthreads();   // every wave is past its loop: the ring is free for staging
         // The FP8 tile is staged in the ring (rows padded to 144 B: a wave's
@@ -441,7 +457,7 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
         const int nsc = a.N / 128;
 #pragma unroll
         for (int i = 0; i < C::MI; ++i) {
-            const int row = 16 * (wm + 2 * i) + r16;
+            const int row = 16 * (wm + C::WM * i) + r16;
             float amax = 0.f;
 #pragma unroll
             for (int w = 0; w < 4; ++w) amax = fmaxf(amax, red[w * BM + row]);
@@ -458,14 +474,14 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
         }
         __syncthreads();
 #pragma unroll
-        for (int pass = 0; pass < BM / 64; ++pass) {
-            const int row = 64 * pass + (tid >> 3), c = tid & 7;
+        for (int pass = 0; pass < BM / (kNT / 8); ++pass) {
+            const int row = (kNT / 8) * pass + (tid >> 3), c = tid & 7;
             if (row < rows)
                 *reinterpret_cast<v4i *>(a.Cq + (size_t)(pos0 + row) * a.N + n0 + 16 * c) =
                     *reinterpret_cast<const v4i *>(qs + row * QS + 16 * c);
         }
     } else if (a.Cf) {
-        store_f32_tile<BM>(a, acc, pos0, rows, slab, wm, wn, smem, red);
+        store_f32_tile<BM, NW>(a, acc, pos0, rows, slab, wm, wn, smem, red);
     } else {
         // output column n0 + 64 wn + 16 j + 4 g + v.  The bf16 tile is staged in
         // the ring (rows padded to 528 B: a half-wave's 16-row x 2-lane 8-byte
@@ -476,7 +492,7 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
         __syncthreads();   // every wave is past its loop: the ring is free for staging
 #pragma unroll
         for (int i = 0; i < C::MI; ++i) {
-            const int row = 16 * (wm + 2 * i) + r16;
+            const int row = 16 * (wm + C::WM * i) + r16;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 v2i pk;
@@ -487,8 +503,8 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
         }
         __syncthreads();
 #pragma unroll
-        for (int pass = 0; pass < BM / 16; ++pass) {
-            const int row = 16 * pass + (tid >> 5), c = tid & 31;
+        for (int pass = 0; pass < BM / (kNT / 32); ++pass) {
+            const int row = (kNT / 32) * pass + (tid >> 5), c = tid & 31;
             if (row < rows)
                 *reinterpret_cast<v4i *>(a.Cy + (size_t)(pos0 + row) * a.ldc + n0 + 8 * c) =
                     *reinterpret_cast<const v4i *>(ys + row * YS + 16 * c);
@@ -496,8 +512,8 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
     }
 }
 
-template <int BM, bool GATEUP>
-__global__ __launch_bounds__(kNT) void moe_gemm_wide_kernel(GemmArgs a)
+template <int BM, bool GATEUP, int NW>
+__global__ __launch_bounds__(64 * NW) void moe_gemm_wide_kernel(GemmArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int4 *tab = reinterpret_cast<const int4 *>(a.tile_tab);   // shared + routed tiles
@@ -525,9 +541,19 @@ __global__ __launch_bounds__(kNT) void moe_gemm_wide_kernel(GemmArgs a)
     }
     XS_WTRACE(0);
     const int4 d = tab[1 + tile];   // {expert, first position, rows}
-    if (d.z >= BM) run_tile<BM, GATEUP, true, true>(a, d.x, d.y, BM, slab, smem);
-    else if (d.z > 128) run_tile<BM, GATEUP, false, true>(a, d.x, d.y, d.z, slab, smem);
-    else run_tile<BM, GATEUP, false, false>(a, d.x, d.y, d.z, slab, smem);
+    if constexpr (NW == 8) {
+        // 192-row tiles: full tiles 3 + 2 stages, partial ones past 128 rows too
+        if (d.z >= BM) run_tile<BM, GATEUP, true, 1, NW>(a, d.x, d.y, BM, slab, smem);
+        else if (d.z > 128) run_tile<BM, GATEUP, false, 1, NW>(a, d.x, d.y, d.z, slab, smem);
+        else if (d.z > 64 || !a.short_deep) run_tile<BM, GATEUP, false, 0, NW>(a, d.x, d.y, d.z, slab, smem);
+        // tiles of up to 64 rows (single-tile experts: a weight stream from HBM)
+        // lay out 64-row activation stages, which leaves LDS for 4 weight stages
+        else run_tile<64, GATEUP, false, 2, NW>(a, d.x, d.y, d.z, slab, smem);
+    } else {
+        static_assert(NW == 4, "waves");
+        if (d.z >= BM) run_tile<BM, GATEUP, true, 3, NW>(a, d.x, d.y, BM, slab, smem);
+        else run_tile<BM, GATEUP, false, 3, NW>(a, d.x, d.y, d.z, slab, smem);
+    }
     XS_WTRACE(3);
 #ifdef XS_WIDE_TRACE
     if (threadIdx.x == 0 && blockIdx.x + gridDim.x * blockIdx.y < 16384) {
@@ -537,13 +563,14 @@ __global__ __launch_bounds__(kNT) void moe_gemm_wide_kernel(GemmArgs a)
 #endif
 }
 
-template <int BM, bool GATEUP>
+template <int BM, bool GATEUP, int NW>
 int launch_wide(const GemmArgs &a, int grid_y, hipStream_t st)
 {
     if (grid_y <= 0) return XS_OK;
+    constexpr int kNT = 64 * NW;
     const size_t smem = (size_t)kRing + kTrash + 8 * (size_t)(a.K / 128) + 4 * 4 * BM;
     if (smem > 160 * 1024) return set_error(XS_ERR_UNSUPPORTED, "K=%d needs %zu bytes of LDS", a.K, smem);
-    auto fn = moe_gemm_wide_kernel<BM, GATEUP>;
+    auto fn = moe_gemm_wide_kernel<BM, GATEUP, NW>;
     static bool attr_set = false;
     if (!attr_set) {
         XS_HIP(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
@@ -562,8 +589,9 @@ int launch_wide(const GemmArgs &a, int grid_y, hipStream_t st)
 
 }  // namespace
 
-// 192-row tiles: 2 ring stages; 128-row tiles (3 stages) measured slower on the
-// V4-Flash prefill layer (more weight re-reads across an expert's tiles).
+// 192-row tiles on 8 waves (2 per SIMD).  Measured slower on the V4-Flash
+// prefill layer: 128-row tiles on 4 waves (one per SIMD, 3 + 3 stages) and
+// 128-row tiles on 8 waves with 3 + 3 stages.
 constexpr int kWideBM = 192;
 int wide_tile_rows() { return kWideBM; }
 
@@ -576,7 +604,9 @@ int launch_gemm_wide(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
     const char *ord = getenv("XS_WIDE_ORDER");
     // XS_WIDE_ORDER=0: one block per (slab, tile) in grid order (measurements)
     b.xcd_order = !(ord && ord[0] == '0') && (gateup ? a.N / 128 : a.N / 256) % 4 == 0;
-    return gateup ? launch_wide<kWideBM, true>(b, grid_y, st) : launch_wide<kWideBM, false>(b, grid_y, st);
+    const char *sd = getenv("XS_WIDE_SHORT");
+    b.short_deep = !(sd && sd[0] == '0');
+    return gateup ? launch_wide<kWideBM, true, 8>(b, grid_y, st) : launch_wide<kWideBM, false, 8>(b, grid_y, st);
 }
 
 }  // namespace xs
