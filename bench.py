@@ -91,25 +91,33 @@ def routed_expert_count(layer, x):
     return int((routed_counts(layer, x) > 0).sum())
 
 
-def cpu_baseline(g, sample_tokens):
-    """The reference's CPU path restated (oracle.moe_ref_f32: gemm_cpu loop order,
-    f32 mlp per expert, single thread) on the first `sample_tokens` tokens of the
-    workload, with the FP8 weights dequantized to f32 (as a reference user would
-    load them)."""
-    import numpy as np
-    import torch
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _ref_f32_seconds(g, T0, T1, torch):
+    """The reference's CPU path restated (oracle.moe_ref_f32: gemm_cpu i->kk->j
+    order with transB strided reads, f32 mlp() per expert, weighted sum plus the
+    shared expert; single thread) on tokens [T0, T1) of a synthetic layer, with
+    the FP8 weights dequantized to f32 (as a reference user would load them).
+    Returns (seconds, experts touched)."""
     import oracle
 
-    x = g["x"][:sample_tokens].float().cpu().numpy()
+    x = g["x"][T0:T1].float().cpu().numpy()
     wr = g["router_w"].float().cpu().numpy()
     bias = g["bias"].cpu().numpy() if g["bias"] is not None else None
-    logits = oracle.router_logits(x, wr, False)
-    idx, _ = oracle.route(logits, bias, g["k"])
+    idx, _ = oracle.route(oracle.router_logits(x, wr, False), bias, g["k"])
     touched = sorted(set(idx.ravel().tolist()))
 
-    def deq(q, s):
+    def deq(q, s_):
         v = q.view(torch.float8_e4m3fn).float()
-        rep = s.repeat_interleave(128, -2).repeat_interleave(128, -1)
+        rep = s_.repeat_interleave(128, -2).repeat_interleave(128, -1)
         return (v * rep).cpu().numpy()
 
     w13 = {e: deq(g["w13"][e], g["s13"][e]) for e in touched}
@@ -118,12 +126,42 @@ def cpu_baseline(g, sample_tokens):
     shared = (deq(sh[0], sh[1]), deq(sh[2], sh[3])) if sh is not None else None
     t0 = time.perf_counter()
     oracle.moe_ref_f32(x, wr, bias, w13, w2, g["k"], shared=shared)
-    dt = time.perf_counter() - t0
-    return dict(value=sample_tokens / dt, unit="tokens/s", cores=1, kind="port",
-                sample=(f"first {sample_tokens} tokens of the prefill workload, reference-path f32 "
-                        f"(gemm_cpu i->kk->j order, mlp per expert, 1 thread; {len(touched)} experts "
-                        f"+ shared touched); {dt:.2f} s on {os.cpu_count()} visible cores"),
-                seconds=dt)
+    return time.perf_counter() - t0, len(touched)
+
+
+def cpu_baseline(g_prefill, g_decode, torch, slice_tokens=64):
+    """BASELINE protocol: one core (this thread pinned to one CPU), configs C1,
+    C4 at T = 1 and 16, and a slice of C3; C3's tokens/s is the slice's rate, a
+    per-token extrapolation of the full 8192-token layer."""
+    cpus = sorted(os.sched_getaffinity(0))
+    os.sched_setaffinity(0, {cpus[0]})
+    try:
+        runs = {}
+        import numpy as np
+        import oracle
+        rng = np.random.default_rng(11)   # C1: f32, everything ~ N(0, 0.02), zero bias
+        n = lambda *sh: (rng.standard_normal(sh) * 0.02).astype(np.float32)  # noqa: E731
+        x1, wr1, w13, w2 = n(64, 256), n(8, 256), n(8, 256, 256), n(8, 256, 128)
+        t0 = time.perf_counter()
+        oracle.moe_ref_f32(x1, wr1, None, w13, w2, 2, shared=(n(256, 256), n(256, 128)))
+        dt = time.perf_counter() - t0
+        runs["C1_tiny_f32_64tok"] = {"s": dt, "tokens_per_s": 64 / dt, "experts_touched": 8}
+        for Td in (1, 16):
+            dt, ne = _ref_f32_seconds(g_decode, 0, Td, torch)
+            runs[f"C4_decode_T{Td}"] = {"s": dt, "tokens_per_s": Td / dt, "experts_touched": ne}
+        dt, ne = _ref_f32_seconds(g_prefill, 0, slice_tokens, torch)
+        runs[f"C3_prefill_{slice_tokens}tok_slice"] = {"s": dt, "tokens_per_s": slice_tokens / dt,
+                                                       "experts_touched": ne,
+                                                       "extrapolated_8192tok_s": dt / slice_tokens * 8192}
+    finally:
+        os.sched_setaffinity(0, set(cpus))
+    c3 = runs[f"C3_prefill_{slice_tokens}tok_slice"]
+    return dict(value=c3["tokens_per_s"], unit="tokens/s", cores=1, kind="port",
+                sample=(f"C3 value = first {slice_tokens} tokens of the prefill workload (per-token "
+                        f"extrapolation to 8192 tokens: {c3['extrapolated_8192tok_s']:.0f} s); reference-path "
+                        f"f32 restated (gemm_cpu i->kk->j order, mlp per expert), 1 pinned core of "
+                        f"{len(cpus)} visible, CPU {_cpu_model()}"),
+                cpu_model=_cpu_model(), nproc=os.cpu_count(), visible_cpus=len(cpus), configs=runs)
 
 
 def main():
@@ -137,7 +175,7 @@ def main():
     ap.add_argument("--decode-tokens", default="1,16,64,256",
                     help="comma list of decode batch sizes (configs[3])")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=8)
+    ap.add_argument("--cpu-tokens", type=int, default=64, help="tokens of the C3 slice the CPU baseline times")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (the MoE operator is built and measured for a "
@@ -219,11 +257,19 @@ def prefill(a, X, torch):
                      "mfma_tflops": gu_flops / (gu_ms * 1e-3) / 1e12,
                      "mfma_frac": gu_flops / (gu_ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS},
     }
+    # the bit-exact router (gemm_cpu order, f32, no FMA) on the same workload
+    lx = layer_from(g, router_exact=True)
+    msx, stx = time_forward(lx, g["x"], a.steps, a.warmup, profile=True)
+    res["router_exact"] = {"ms_per_step": msx, "router_logits_ms": stx["router_logits"],
+                           "router_logits_ms_mfma": stages["router_logits"],
+                           "extra_frac_of_layer": (msx - ms) / ms}
+    del lx
     del layer
     if not a.no_cpu:
         log("cpu baseline ...")
-        cb = cpu_baseline(g, a.cpu_tokens)
-        res["cpu_baseline"] = {kk: cb[kk] for kk in ("value", "unit", "cores", "kind", "sample")}
+        gdc = synth_layer(16, H, I, E, K_TOP, seed=1, bias_std=0.0)
+        res["cpu_baseline"] = cpu_baseline(g, gdc, torch, a.cpu_tokens)
+        del gdc
     del g
     torch.cuda.empty_cache()
     return res
@@ -241,9 +287,13 @@ def decode(a, X, torch):
         msd, st = time_forward(L, xd, max(a.steps, 50), a.warmup, profile=True)
         ned = routed_expert_count(L, xd)
         by = (ned + 1) * expert_bytes(H, I, False) + E * H * 2 + Td * H * 4
+        Lx = layer_from(gd, router_exact=True)
+        msx, stx = time_forward(Lx, xd, max(a.steps, 50), a.warmup, profile=True)
         dec[str(Td)] = {"ms": msd, "experts_touched": ned + 1, "hbm_gbs": by / (msd * 1e-3) / 1e9,
                         "frac_hbm_peak": by / (msd * 1e-3) / 1e9 / PEAK_HBM_GBS,
-                        "tokens_per_s": Td / (msd * 1e-3), "stage_ms": st}
+                        "tokens_per_s": Td / (msd * 1e-3), "stage_ms": st,
+                        "router_exact": {"ms": msx, "router_logits_ms": stx["router_logits"],
+                                         "extra_frac_of_layer": (msx - msd) / msd}}
     del gd
     torch.cuda.empty_cache()
     return dec

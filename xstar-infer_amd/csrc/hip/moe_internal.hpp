@@ -29,6 +29,22 @@ __device__ __forceinline__ void load8(const float *p, float *v)
     }
 }
 
+// 4 consecutive elements -> f32 (8-byte aligned for bf16, 16-byte for f32).
+__device__ __forceinline__ void load4(const uint16_t *p, float *v)
+{
+    v2i r = *reinterpret_cast<const v2i *>(p);
+    v[0] = __uint_as_float((uint32_t)r[0] << 16);
+    v[1] = __uint_as_float((uint32_t)r[0] & 0xFFFF0000u);
+    v[2] = __uint_as_float((uint32_t)r[1] << 16);
+    v[3] = __uint_as_float((uint32_t)r[1] & 0xFFFF0000u);
+}
+__device__ __forceinline__ void load4(const float *p, float *v)
+{
+    v4f a = *reinterpret_cast<const v4f *>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = a[i];
+}
+
 // 8 f32 values -> 8 consecutive outputs (bf16 RNE or f32).
 __device__ __forceinline__ void store8(uint16_t *p, const float *v)
 {

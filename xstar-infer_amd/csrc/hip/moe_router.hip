@@ -26,10 +26,33 @@ __device__ __forceinline__ void clear_mask(uint32_t *mask, int64_t words)
 }
 
 // ------------------------------------------------------------ exact logits
-// 256 threads = 16 tokens x 16 experts; k-chunks of 64 staged in LDS; each
-// thread owns one (t, e) and accumulates sequentially in k with separately
-// rounded products (no contraction), as gemm_cpu does.
+// gemm_cpu order: each logit is one sequential f32 chain over k (a separately
+// rounded product added to the running sum, no contraction), so the work is
+// latency-bound chains.  A lane owns TB chains: one expert, TB tokens (one
+// token for small batches, where the chains' latency is the cost; four for
+// large ones, where the LDS reads shared by the four chains are).  The block
+// holds 64 experts x 4 TB tokens (TB per wave).  K moves in chunks of 256: the
+// chunk of the 64 router rows is converted to f32 into LDS (rows padded to
+// 260 floats, so a lane's 16-byte reads of its own row hit distinct banks),
+// the token rows too (read as broadcasts), and the next chunk's loads are in
+// flight while the chains run over the current one.
+constexpr int kXC = 256;                 // K chunk
+constexpr int kXR = kXC + 4;             // padded LDS row (floats)
+
 template <typename T>
+struct ChainLoad;
+template <>
+struct ChainLoad<uint16_t> {
+    static constexpr int N = 8;          // 16-byte loads per thread per chunk (64 bf16)
+    v4i r[N];
+};
+template <>
+struct ChainLoad<float> {
+    static constexpr int N = 16;         // 64 f32
+    v4i r[N];
+};
+
+template <typename T, int TB>
 __global__ __launch_bounds__(256) void router_logits_exact_kernel(const T *__restrict__ x,
                                                                   const T *__restrict__ wr,
                                                                   int Tn, int E, int H,
@@ -38,25 +61,101 @@ __global__ __launch_bounds__(256) void router_logits_exact_kernel(const T *__res
 {
 #pragma clang fp contract(off)
     clear_mask(mask, mask_words);
-    __shared__ float xs_[16][65];
-    __shared__ float ws_[16][65];
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
-    float acc = 0.0f;
-    for (int k0 = 0; k0 < H; k0 += 64) {
-        for (int i = threadIdx.x; i < 16 * 64; i += 256) {
-            int r = i >> 6, c = i & 63;
-            int tt = min(t0 + r, Tn - 1), ee = min(e0 + r, E - 1);
-            xs_[r][c] = to_f32(x[(size_t)tt * H + k0 + c]);
-            ws_[r][c] = to_f32(wr[(size_t)ee * H + k0 + c]);
+    extern __shared__ __attribute__((aligned(16))) float xsm[];
+    float *Ws = xsm;                      // [64][kXR]
+    float *Xs = xsm + 64 * kXR;           // [4 TB][kXC]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int e0 = blockIdx.x * 64, t0 = blockIdx.y * 4 * TB + wave * TB;
+    // loader mapping: router row lr (4 threads per row, 64 consecutive k each);
+    // this wave's TB token rows, 4 consecutive k per lane.  H is a multiple of
+    // 128: a last chunk of 128 loads (and runs) half.
+    const int lr = tid >> 2, lc = (tid & 3) * 64;
+    const T *wrow = wr + (size_t)min(e0 + lr, E - 1) * H + lc;
+    ChainLoad<T> ld;
+    float xv[TB][4];
+    auto fetch = [&](int k0) {
+        const int rem = min(kXC, H - k0);
+        if (lc < rem) {
+#pragma unroll
+            for (int i = 0; i < ChainLoad<T>::N; ++i)
+                ld.r[i] = *reinterpret_cast<const v4i *>(wrow + k0 + i * (16 / sizeof(T)));
         }
+        if (lane * 4 < rem) {
+#pragma unroll
+            for (int j = 0; j < TB; ++j) load4(x + (size_t)min(t0 + j, Tn - 1) * H + k0 + lane * 4, xv[j]);
+        }
+    };
+    auto store = [&]() {
+        float *dst = Ws + lr * kXR + lc;
+        if constexpr (sizeof(T) == 2) {
+#pragma unroll
+            for (int i = 0; i < ChainLoad<T>::N; ++i) {
+                v4f lo, hi;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    lo[2 * j] = __uint_as_float((uint32_t)ld.r[i][j] << 16);
+                    lo[2 * j + 1] = __uint_as_float((uint32_t)ld.r[i][j] & 0xFFFF0000u);
+                    hi[2 * j] = __uint_as_float((uint32_t)ld.r[i][j + 2] << 16);
+                    hi[2 * j + 1] = __uint_as_float((uint32_t)ld.r[i][j + 2] & 0xFFFF0000u);
+                }
+                *reinterpret_cast<v4f *>(dst + 8 * i) = lo;
+                *reinterpret_cast<v4f *>(dst + 8 * i + 4) = hi;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < ChainLoad<T>::N; ++i)
+                *reinterpret_cast<v4i *>(dst + 4 * i) = ld.r[i];
+        }
+#pragma unroll
+        for (int j = 0; j < TB; ++j)
+            *reinterpret_cast<v4f *>(Xs + (wave * TB + j) * kXC + lane * 4) = v4f{xv[j][0], xv[j][1], xv[j][2], xv[j][3]};
+    };
+    float acc[TB];
+#pragma unroll
+    for (int j = 0; j < TB; ++j) acc[j] = 0.0f;
+    fetch(0);
+    for (int k0 = 0; k0 < H; k0 += kXC) {
+        __syncthreads();                  // the previous chunk's chains are done with LDS
+        store();
+        if (k0 + kXC < H) fetch(k0 + kXC);
         __syncthreads();
-#pragma unroll 8
-        for (int c = 0; c < 64; ++c) acc = acc + xs_[ty][c] * ws_[tx][c];   // no contraction (pragma above)
-        __syncthreads();
+        const float *wl = Ws + lane * kXR;
+        const float *xl = Xs + wave * TB * kXC;
+        const int rem = min(kXC, H - k0);
+#pragma unroll 4
+        for (int k = 0; k < rem; k += 4) {
+            const v4f w4 = *reinterpret_cast<const v4f *>(wl + k);
+            v4f x4[TB];
+#pragma unroll
+            for (int j = 0; j < TB; ++j) x4[j] = *reinterpret_cast<const v4f *>(xl + j * kXC + k);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < TB; ++j) acc[j] = acc[j] + x4[j][i] * w4[i];   // no contraction (pragma above)
+        }
     }
-    int t = t0 + ty, e = e0 + tx;
-    if (t < Tn && e < E) logits[(size_t)t * E + e] = acc;
+    const int e = e0 + lane;
+#pragma unroll
+    for (int j = 0; j < TB; ++j)
+        if (t0 + j < Tn && e < E) logits[(size_t)(t0 + j) * E + e] = acc[j];
+}
+
+template <typename T, int TB>
+static int launch_exact(const T *x, const T *wr, int64_t T_, int64_t E, int64_t H, float *logits, uint32_t *mask,
+                        int64_t mask_words, hipStream_t st)
+{
+    const size_t smem = sizeof(float) * (64 * kXR + 4 * TB * kXC);
+    static bool attr_set = false;
+    if (!attr_set) {
+        XS_HIP(hipFuncSetAttribute((const void *)router_logits_exact_kernel<T, TB>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        attr_set = true;
+    }
+    dim3 grid((unsigned)((E + 63) / 64), (unsigned)((T_ + 4 * TB - 1) / (4 * TB))), block(256);
+    router_logits_exact_kernel<T, TB><<<grid, block, smem, st>>>(x, wr, (int)T_, (int)E, (int)H, logits, mask,
+                                                                 mask_words);
+    XS_LAUNCH_CHECK();
+    return XS_OK;
 }
 
 // FP8 1x128 of one 8-column chunk c8 of a row: the 16 lanes of an aligned
@@ -490,14 +589,17 @@ int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, in
         return set_error(XS_ERR_INVALID, "router: the activation quant is folded into the decode path only");
     if (T == 0) return XS_OK;
     if (exact || dtype == XS_F32) {
-        dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16)), block(256);
+        // one token per lane while the chains' latency is the cost (measured up to
+        // 256 tokens: 4 per lane was 2.5x slower there), four for large batches
         if (dtype == XS_F32)
-            router_logits_exact_kernel<float><<<grid, block, 0, st>>>((const float *)x, (const float *)wr,
-                                                                      (int)T, (int)E, (int)H, logits,
-                                                                      mask_clear, mask_words);
-        else
-            router_logits_exact_kernel<uint16_t><<<grid, block, 0, st>>>(
-                (const uint16_t *)x, (const uint16_t *)wr, (int)T, (int)E, (int)H, logits, mask_clear, mask_words);
+            return T <= 2048 ? launch_exact<float, 1>((const float *)x, (const float *)wr, T, E, H, logits, mask_clear,
+                                                    mask_words, st)
+                           : launch_exact<float, 4>((const float *)x, (const float *)wr, T, E, H, logits, mask_clear,
+                                                    mask_words, st);
+        return T <= 2048 ? launch_exact<uint16_t, 1>((const uint16_t *)x, (const uint16_t *)wr, T, E, H, logits,
+                                                   mask_clear, mask_words, st)
+                       : launch_exact<uint16_t, 4>((const uint16_t *)x, (const uint16_t *)wr, T, E, H, logits,
+                                                   mask_clear, mask_words, st);
     } else if (T > 256) {
         // prefill: 128 tokens x 128 experts per block through an LDS ring, K split nsplit ways
         static bool attr_set = false;
