@@ -44,7 +44,7 @@ constexpr int kTrash = 1024;         // LDS target of padding DMAs
 
 // Ring modes: 0 = 2 activation + 3 weight stages, 1 = 3 + 2, 2 = 2 + 4, 3 = 3 + 3.
 // NW waves per block: 4 along the weight rows times NW / 4 along the tokens.
-template <int BM, int MODE, int NW>
+template <int BM, int MODE, int NW, int DMAW = NW>
 struct WCfg {
     static constexpr int WM = NW / 4;                      // waves along the tokens
     static constexpr int NS16 = BM / 16;                   // 16-token subtiles per tile
@@ -61,8 +61,9 @@ struct WCfg {
     static constexpr int NAR = (MODE == 1 || MODE == 3) ? 3 : 2;
     static constexpr int NWR = MODE == 1 ? 2 : (MODE == 2 ? 4 : 3);
     static constexpr int DA = NAR - 1, DW = NWR - 1;
-    static constexpr int NA = BM / 8 / NW;                 // 1 KB activation DMAs per wave and step
-    static constexpr int NB = 256 / 8 / NW;                // 1 KB weight DMAs per wave and step
+    // the first DMAW waves issue the loads (DMAW < NW: the other waves only compute)
+    static constexpr int NA = BM / 8 / DMAW;               // 1 KB activation DMAs per loading wave and step
+    static constexpr int NB = 256 / 8 / DMAW;              // 1 KB weight DMAs per loading wave and step
     static constexpr int NSA = S_BYTES / 256;              // scale DMAs (waves 0 .. NSA-1)
     static constexpr int PER_STEP = NA + NB + 1;           // loads per wave per step
     // Each iteration issues the operand with the shorter prefetch distance first.
@@ -74,7 +75,7 @@ struct WCfg {
     static constexpr int X = XW < XA ? XW : XA;
     static constexpr int PRO = DA > DW ? DA : DW;          // prologue iterations
     static_assert(BM % 64 == 0 && DA >= 1 && DW >= 1 && NAR * AS_BYTES + NWR * W_BYTES <= kRing, "tile");
-    static_assert(NA >= 1 && NSA <= NW && MI % 2 == 0, "waves");
+    static_assert(NA >= 1 && NSA <= DMAW && DMAW <= NW && MI % 2 == 0, "waves");
 };
 
 __device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }
@@ -237,11 +238,11 @@ __device__ uint64_t g_wide_trace[2][16384][6];
 #define XS_WTRACE(ev)
 #endif
 
-template <int BM, bool GATEUP, bool FULL, int MODE, int NW>
+template <int BM, bool GATEUP, bool FULL, int MODE, int NW, int DMAW = NW>
 __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int rows, int slab, uint8_t *smem)
 {
-    using C = WCfg<BM, MODE, NW>;
-    constexpr int kNW = NW, kNT = 64 * NW;
+    using C = WCfg<BM, MODE, NW, DMAW>;
+    constexpr int kNW = DMAW, kNT = 64 * NW;   // kNW: waves that issue DMAs
     const int KB = a.K / 128;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -342,16 +343,19 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
+    const bool dma_wave = wave < DMAW;
     __syncthreads();   // sB visible
+    if (dma_wave) {
 #pragma unroll
-    for (int j = -C::PRO; j < 0; ++j) issue(j);
+        for (int j = -C::PRO; j < 0; ++j) issue(j);
+    }
     XS_WTRACE(1);
 
     const int sbi = GATEUP ? 0 : (wn >> 1);   // down: the wave's 128-row scale block
     for (int kb = 0; kb < KB; ++kb) {
-        wait_vm<C::X>();          // this wave's loads of step kb landed
+        if (dma_wave) wait_vm<C::X>();   // this wave's loads of step kb landed
         __syncthreads();          // ... and every wave's; the slots of step kb-1 are free
-        issue(kb);
+        if (dma_wave) issue(kb);
         const uint8_t *sA = smem + (kb % C::NAR) * C::AS_BYTES;
         const float *sS = reinterpret_cast<const float *>(sA + C::A_BYTES);
         const uint8_t *sW = smem + C::NAR * C::AS_BYTES + (kb % C::NWR) * C::W_BYTES;
@@ -543,12 +547,17 @@ __global__ __launch_bounds__(64 * NW) void moe_gemm_wide_kernel(GemmArgs a)
     const int4 d = tab[1 + tile];   // {expert, first position, rows}
     if constexpr (NW == 8) {
         // 192-row tiles: full tiles 3 + 2 stages, partial ones past 128 rows too
-        if (d.z >= BM) run_tile<BM, GATEUP, true, 1, NW>(a, d.x, d.y, BM, slab, smem);
-        else if (d.z > 128) run_tile<BM, GATEUP, false, 1, NW>(a, d.x, d.y, d.z, slab, smem);
-        else if (d.z > 64 || !a.short_deep) run_tile<BM, GATEUP, false, 0, NW>(a, d.x, d.y, d.z, slab, smem);
+        // the 4 waves of wm = 0 (one per SIMD) issue every DMA, the other 4
+        // only compute: after each step's barrier one wave per SIMD goes
+        // straight to its MFMAs while the other issues the step's loads
+        // (measured 4% faster on the V4-Flash prefill layer than all 8 loading)
+        constexpr int DW = NW / 2;
+        if (d.z >= BM) run_tile<BM, GATEUP, true, 1, NW, DW>(a, d.x, d.y, BM, slab, smem);
+        else if (d.z > 128) run_tile<BM, GATEUP, false, 1, NW, DW>(a, d.x, d.y, d.z, slab, smem);
+        else if (d.z > 64 || !a.short_deep) run_tile<BM, GATEUP, false, 0, NW, DW>(a, d.x, d.y, d.z, slab, smem);
         // tiles of up to 64 rows (single-tile experts: a weight stream from HBM)
         // lay out 64-row activation stages, which leaves LDS for 4 weight stages
-        else run_tile<64, GATEUP, false, 2, NW>(a, d.x, d.y, d.z, slab, smem);
+        else run_tile<64, GATEUP, false, 2, NW, DW>(a, d.x, d.y, d.z, slab, smem);
     } else {
         static_assert(NW == 4, "waves");
         if (d.z >= BM) run_tile<BM, GATEUP, true, 3, NW>(a, d.x, d.y, BM, slab, smem);
