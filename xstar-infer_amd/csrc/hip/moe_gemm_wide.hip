@@ -289,8 +289,9 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
     const bool sa_real = wave < C::NSA;
     const uint32_t oS = (uint32_t)token_of(sa_real ? 64 * wave + lane : 0) * (uint32_t)(KB * 4);
     const uint8_t *gS = reinterpret_cast<const uint8_t *>(a.As);
-    // an expert whose rows fit one tile reads its weights once: stream them
-    const bool stream_w = a.offsets[e + 1] - a.offsets[e] <= BM;
+    // an expert whose rows fit one partial tile reads its weights once: stream
+    // them (full tiles keep the default policy, so their loop has no branch)
+    const bool stream_w = !FULL && a.offsets[e + 1] - a.offsets[e] <= BM;
 
     const uint32_t wring_lds = ring_lds + (uint32_t)(C::NAR * C::AS_BYTES);
     // operands of step kb into ring slot kb % depth; kb < 0 (prologue padding)
@@ -315,6 +316,27 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
 #pragma unroll
             for (int u = 0; u < C::NB; ++u)
                 dma16(Bexp + (size_t)kk * 128, oW[u], kb < 0 ? trash_lds : st + 1024 * (wave + kNW * u));
+        }
+    };
+    // the d-th load of iteration kb in issue order (W rows, then A rows and the
+    // row scales when W_FIRST, else A first): one DMA instruction.  Full tiles
+    // never stream their weights with the non-temporal hint (their experts have
+    // more tiles reading the same slab), so this path has no branch.
+    auto issue_one = [&](int kb, int d) {
+        const int dw = C::W_FIRST ? d : d - (C::NA + 1);
+        const int da = C::W_FIRST ? d - C::NB : d;
+        if (dw >= 0 && dw < C::NB) {
+            const int k2 = kb + C::DW;
+            const int kk = k2 < KB ? k2 : KB - 1;
+            dma16(Bexp + (size_t)kk * 128, oW[dw], wring_lds + (uint32_t)((k2 % C::NWR) * C::W_BYTES) + 1024 * (wave + kNW * dw));
+        } else if (da >= 0 && da < C::NA) {
+            const int k2 = kb + C::DA;
+            const int kk = k2 < KB ? k2 : KB - 1;
+            dma16(a.A + (size_t)kk * 128, oA[da], ring_lds + (uint32_t)((k2 % C::NAR) * C::AS_BYTES) + 1024 * (wave + kNW * da));
+        } else if (da == C::NA) {
+            const int k2 = kb + C::DA;
+            const int kk = k2 < KB ? k2 : KB - 1;
+            dma4(gS + (size_t)kk * 4, oS, sa_real ? ring_lds + (uint32_t)((k2 % C::NAR) * C::AS_BYTES) + C::A_BYTES + 256 * wave : trash_lds);
         }
     };
     auto issue = [&](int kb) {   // the loads of iteration kb: A(kb + DA), W(kb + DW)
@@ -355,7 +377,10 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
     for (int kb = 0; kb < KB; ++kb) {
         if (dma_wave) wait_vm<C::X>();   // this wave's loads of step kb landed
         __syncthreads();          // ... and every wave's; the slots of step kb-1 are free
-        if (dma_wave) issue(kb);
+        // Full tiles spread the step's DMAs over its subtiles (below): a DMA
+        // instruction holds the issuing wave until the memory pipeline takes it,
+        // so a burst of them after the barrier keeps that wave off its MFMAs.
+        if (dma_wave && !FULL) issue(kb);
         const uint8_t *sA = smem + (kb % C::NAR) * C::AS_BYTES;
         const float *sS = reinterpret_cast<const float *>(sA + C::A_BYTES);
         const uint8_t *sW = smem + C::NAR * C::AS_BYTES + (kb % C::NWR) * C::W_BYTES;
@@ -393,6 +418,12 @@ __device__ __forceinline__ void run_tile(const GemmArgs &a, int e, int pos0, int
         v4f q[2][4];
 #pragma unroll
         for (int i = 0; i <= C::MI; ++i) {
+            if (FULL && dma_wave && i < C::MI) {
+                // DMA d of this step goes out in subtile d * MI / PER_STEP
+#pragma unroll
+                for (int d = 0; d < C::PER_STEP; ++d)
+                    if (d * C::MI / C::PER_STEP == i) issue_one(kb, d);
+            }
             if (i < C::MI && (FULL || i < nlive)) {
                 if (i + PB < C::MI && (FULL || i + PB < nlive)) bx[(i + PB) % (PB + 1)] = read_b(i + PB);
 #pragma unroll
