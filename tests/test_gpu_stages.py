@@ -200,7 +200,8 @@ def test_permute_rejects_invalid_idx(case):
     assert np.array_equal(inv.cpu().numpy(), ri) and np.array_equal(offsets.cpu().numpy(), ro)
 
 
-@pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (40, 256, 384), (1, 128, 128), (2100, 512, 1024)])
+@pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (40, 256, 384), (1, 128, 128), (2100, 512, 1024),
+                                   (200, 1024, 4096), (130, 384, 2048), (33000, 256, 256)])
 def test_gemm_fp8_blockscale(M, N, K):
     """C = dequant(quant1x128(A)) . dequant(B)^T vs a float64 reference on the
     same quantized operands (the activation quantizer is bit-exact, so the
@@ -218,3 +219,6 @@ def test_gemm_fp8_blockscale(M, N, K):
     ref = ad @ bd.T
     err = np.abs(got - ref).max() / np.abs(ref).max()
     assert err < 4e-3, err
+    # split-K partials are summed in split order: a second call gives the same bits
+    again = X.gemm_fp8_blockscale(_bf16_dev(a), torch.from_numpy(bq).cuda(), torch.from_numpy(bs).cuda())
+    assert torch.equal(again, out)

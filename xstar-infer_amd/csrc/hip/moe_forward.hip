@@ -417,27 +417,15 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
 }
 
 // --------------------------------------------------- single FP8 GEMM (C = A.B^T)
-// One segment of M rows: offsets and the tile table (entry 0: {tiles, 0}).
-__global__ void single_segment_kernel(int32_t *offsets, int4 *tab, int M, int bm)
-{
-    const int nt = (M + bm - 1) / bm;
-    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-    if (i == 0) {
-        offsets[0] = 0;
-        offsets[1] = M;
-        offsets[2] = M;
-        tab[0] = int4{nt, 0, 0, 0};
-    }
-    if (i < nt) tab[1 + i] = int4{0, i * bm, min(bm, M - i * bm), (i & 0xffff) | (min(nt, 0x7fff) << 16)};
-}
-
-static size_t gemm_ws(int64_t M, int64_t K, size_t *o_s, size_t *o_meta)
+// Workspace: A quantized [M, K] e4m3 + [M, K/128] f32, then the dense kernel's
+// partial tiles and counters (only when M is small enough for split-K).
+static size_t gemm_ws(int64_t M, int64_t K, size_t *o_s, size_t *o_part)
 {
     size_t q = al((size_t)M * K);
     size_t s = al(4 * (size_t)M * (K / 128));
     *o_s = q;
-    *o_meta = q + s;
-    return q + s + 256 + al(tile_table_bytes(M, 0, 1, 16));
+    *o_part = q + s;
+    return q + s + al(dense_part_bytes(M));
 }
 
 // ------------------------------------------- forward without a caller workspace
@@ -543,38 +531,22 @@ int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int
                "misaligned operand: A, B and C need 16-byte, Bs 4-byte alignment");
     XS_REQUIRE(M >= 0 && M < (1 << 24) && N >= 128 && N % 128 == 0 && K >= 128 && K % 128 == 0,
                "shape mismatch: N and K must be multiples of 128");
-    size_t o_s, o_meta;
-    size_t need = gemm_ws(M, K, &o_s, &o_meta);
+    size_t o_s, o_part;
+    size_t need = gemm_ws(M, K, &o_s, &o_part);
     if (!workspace || workspace_bytes < need)
         return set_error(XS_ERR_WORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, need);
     if (M == 0) return XS_OK;
     hipStream_t st = (hipStream_t)stream;
     char *ws = (char *)workspace;
-    int rc = launch_quant_act(A, XS_BF16, M, K, (uint8_t *)ws, ws + o_s, 0, st);
+    float *part = dense_part_bytes(M) ? (float *)(ws + o_part) : nullptr;
+    // the split counters sit in the last 1 KB of the partial region; the
+    // quant launch clears them
+    int32_t *cnt = part ? (int32_t *)(ws + o_part + dense_part_bytes(M) - 1024) : nullptr;
+    const int ncnt = part ? dense_counters(M, N) : 0;
+    int rc = launch_quant_act(A, XS_BF16, M, K, (uint8_t *)ws, ws + o_s, 0, st, cnt, ncnt);
     if (rc) return rc;
-    int32_t *offsets = (int32_t *)(ws + o_meta);
-    int4 *tab = reinterpret_cast<int4 *>(ws + o_meta + 256);
-    const int bm = M >= 2048 ? 128 : (M >= 1024 ? 64 : (M >= 256 ? 32 : 16));
-    const int nt = (int)((M + bm - 1) / bm);
-    single_segment_kernel<<<dim3((unsigned)((nt + 256) / 256)), dim3(256), 0, st>>>(offsets, tab, (int)M, bm);
-    XS_LAUNCH_CHECK();
-    GemmArgs g = {};
-    g.A = (const uint8_t *)ws;
-    g.As = ws + o_s;
-    g.B = B;
-    g.Bs = Bs;
-    g.offsets = offsets;
-    g.tile_off = nullptr;
-    g.tile_tab = reinterpret_cast<const int32_t *>(tab);
-    g.e_lo = 0;
-    g.e_hi = 1;
-    g.E = 1;
-    g.K = (int)K;
-    g.N = (int)N;
-    g.bm = bm;
-    g.Cy = (uint16_t *)C;
-    g.ldc = N;
-    return launch_gemm(g, false, false, (int)((M + bm - 1) / bm), st);
+    return launch_gemm_dense((const uint8_t *)ws, (const float *)(ws + o_s), B, Bs, (uint16_t *)C, M, N, K, part,
+                             cnt, st);
 }
 
 }  // extern "C"

@@ -102,8 +102,17 @@ int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, i
                  int64_t n_group, int64_t topk_group, int renorm, float scaling, int32_t *idx,
                  float *w, uint32_t *mask, int mask_words, int nsplit, float *logits_out,
                  hipStream_t st);
+// zero[0 .. zero_n) is cleared by the same launch (counters of a following kernel).
 int launch_quant_act(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, void *s,
-                     int mx, hipStream_t st);
+                     int mx, hipStream_t st, int32_t *zero = nullptr, int zero_n = 0);
+// Dense FP8 block-scaled GEMM (gemm_dense.hip): C [M, N] bf16 = A [M, K] (e4m3,
+// f32 1x128 row scales) . B [N, K]^T (e4m3, f32 128x128 block scales).  part
+// (dense_part_bytes(M), the last 1 KB the counters) is used when the tiles do
+// not fill the chip; the counters (dense_counters(M, N) of them) are zero on entry.
+size_t dense_part_bytes(int64_t M);
+int dense_counters(int64_t M, int64_t N);
+int launch_gemm_dense(const uint8_t *A, const float *As, const uint8_t *B, const float *Bs, uint16_t *C,
+                      int64_t M, int64_t N, int64_t K, float *part, int32_t *cnt, hipStream_t st);
 
 // RMSNorm of rows x [rows, hidden] -> y (same dtype); with q/s non-null also the
 // FP8 1x128 quantization of y (hidden % 128 == 0).

@@ -629,9 +629,10 @@ int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, in
 template <typename T>
 __global__ __launch_bounds__(256) void quant_act_fp8_kernel(const T *__restrict__ x, int64_t rows,
                                                             int cols, uint8_t *__restrict__ q,
-                                                            float *__restrict__ s)
+                                                            float *__restrict__ s, int32_t *zero, int zero_n)
 {
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid < zero_n) zero[gid] = 0;
     const int per_row = cols / 8;
     const int64_t row = gid / per_row;
     if (row >= rows) return;
@@ -667,10 +668,10 @@ __global__ __launch_bounds__(256) void quant_act_mxfp8_kernel(const T *__restric
 }
 
 int launch_quant_act(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, void *s,
-                     int mx, hipStream_t st)
+                     int mx, hipStream_t st, int32_t *zero, int zero_n)
 {
     if (rows == 0) return XS_OK;
-    int64_t threads = rows * (cols / 8);
+    int64_t threads = std::max(rows * (cols / 8), (int64_t)zero_n);
     dim3 grid((unsigned)((threads + 255) / 256)), block(256);
     if (mx) {
         if (dtype == XS_F32)
@@ -679,9 +680,9 @@ int launch_quant_act(const void *x, int dtype, int64_t rows, int64_t cols, uint8
             quant_act_mxfp8_kernel<uint16_t><<<grid, block, 0, st>>>((const uint16_t *)x, rows, (int)cols, q, (uint8_t *)s);
     } else {
         if (dtype == XS_F32)
-            quant_act_fp8_kernel<float><<<grid, block, 0, st>>>((const float *)x, rows, (int)cols, q, (float *)s);
+            quant_act_fp8_kernel<float><<<grid, block, 0, st>>>((const float *)x, rows, (int)cols, q, (float *)s, zero, zero_n);
         else
-            quant_act_fp8_kernel<uint16_t><<<grid, block, 0, st>>>((const uint16_t *)x, rows, (int)cols, q, (float *)s);
+            quant_act_fp8_kernel<uint16_t><<<grid, block, 0, st>>>((const uint16_t *)x, rows, (int)cols, q, (float *)s, zero, zero_n);
     }
     XS_LAUNCH_CHECK();
     return XS_OK;
