@@ -147,6 +147,15 @@ int xs_quant_weight_mxfp4(const void *w, int dtype, int64_t batch, int64_t n, in
  * A [M, K] bf16 activations (quantized per 1x128 inside, workspace holds them),
  * B [N, K] e4m3 with Bs [N/128, K/128] f32 block scales, C [M, N] bf16.
  * K % 128 == 0, N % 128 == 0. */
+/* Fragment-order copy of e4m3 weights for the weight-direct prefill GEMMs.
+ * No counterpart in the reference (a layout of this library, made once when a
+ * layer's weights are loaded).  w [batch, n, k] row-major e4m3 -> out, same
+ * size: 16-byte chunk c = ((b * n/16 + t) * k/128 + kb) * 128 + 64 h + l holds
+ * w[b][16 t + l % 16][128 kb + 64 h + 16 (l / 16) .. + 16) (h = 0, 1; l = 0..63),
+ * the operand layout of v_mfma_f32_16x16x128_f8f6f4.  n % 16 == 0,
+ * k % 128 == 0, 16-byte aligned, out not overlapping w. */
+int xs_pack_weight_fp8_frag(const uint8_t *w, int64_t batch, int64_t n, int64_t k, uint8_t *out, void *stream);
+
 size_t xs_gemm_fp8_blockscale_workspace_size(int64_t M, int64_t K);
 int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int64_t M,
                            int64_t N, int64_t K, void *C, void *workspace,
@@ -211,6 +220,16 @@ typedef struct {
     uint8_t *act_q;            /* [R, I] e4m3: SwiGLU output after its FP8 1x128 re-quant */
     float *act_s;              /* [R, I/128] f32 scales of act_q */
     float *y_rows;             /* [R, H] f32: each row's down projection, before the combine */
+    /* optional: the FP8 weights again, packed in MFMA fragment order by
+     * xs_pack_weight_fp8_frag (w13 as [E, 2I, H], w2 as [E, H, I], the shared
+     * expert's as E = 1; same byte counts as the row-major tensors).  When the
+     * layer gives all it has (FP8 routed experts, and the shared expert's if
+     * present), the prefill GEMMs load their weights straight into registers
+     * from these copies, with the same results bit for bit.  NULL = not given. */
+    const void *w13_frag;
+    const void *w2_frag;
+    const void *shared_w13_frag;
+    const void *shared_w2_frag;
 } xs_moe_tensors;
 
 /* Device workspace the forward needs for these params (bytes, 256-aligned). */

@@ -243,7 +243,13 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     // 3. permute: (expert, token)-sorted positions, tile offsets
     if ((rc = prof_mark(3, st))) return rc;
     const bool wide = use_wide(p);
-    const int bm = wide ? wide_tile_rows() : pick_bm((double)S / (double)E);
+    const bool fused = fuse_combine(p);
+    // weight-direct tall tiles when the layer gave fragment-packed weights
+    // (XS_WIDE_DIRECT=0 keeps the LDS-ring kernels: measurements, tests)
+    const bool direct = wide && !fused && t->w13_frag && t->w2_frag &&
+                        (!p->has_shared || (t->shared_w13_frag && t->shared_w2_frag)) && wd_supported(H, I) &&
+                        getenv_flag("XS_WIDE_DIRECT", true);
+    const int bm = direct ? wd_tile_rows() : wide ? wide_tile_rows() : pick_bm((double)S / (double)E);
     PermuteOut po = {};
     po.counts = WS(int32_t, counts);
     po.offsets = offsets;
@@ -267,7 +273,6 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     const int stream_tiles = fp4 ? routed_tiles : routed_tiles + shared_tiles;
     const bool stream = stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
                         (sm == 2 || (sm == 1 && stream_items(true, (int)I, stream_tiles) >= 2 * (int64_t)stream_blocks()));
-    const bool fused = fuse_combine(p);
     if (stream) {
         po.zero = WS(int32_t, cnt1);
         po.zero_n = stream_items(true, (int)I, tiles16_max(p)) + 1;
@@ -284,6 +289,8 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     g1.B = (const uint8_t *)t->w13;
     g1.Bs = t->w13_scale;
     g1.Bsh = (const uint8_t *)t->shared_w13;
+    g1.Bp = (const uint8_t *)t->w13_frag;
+    g1.Bshp = (const uint8_t *)t->shared_w13_frag;
     g1.Bssh = t->shared_w13_scale;
     g1.offsets = offsets;
     g1.tile_off = tiles;
@@ -299,6 +306,8 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     g2.B = (const uint8_t *)t->w2;
     g2.Bs = t->w2_scale;
     g2.Bsh = (const uint8_t *)t->shared_w2;
+    g2.Bp = (const uint8_t *)t->w2_frag;
+    g2.Bshp = (const uint8_t *)t->shared_w2_frag;
     g2.Bssh = t->shared_w2_scale;
     g2.offsets = offsets;
     g2.tile_off = tiles;
@@ -337,16 +346,18 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g1.Cs = WS(float, acts);
         g1.e_lo = 0;
         g1.e_hi = (int)E + (shared_rows ? 1 : 0);
-        rc = stream ? launch_gemm_stream(g1, true, false, stream_tiles, rows_all, st)
-             : wide ? launch_gemm_wide(g1, true, routed_tiles + shared_tiles, st)
+        rc = stream   ? launch_gemm_stream(g1, true, false, stream_tiles, rows_all, st)
+             : direct ? launch_gemm_wd(g1, true, routed_tiles + shared_tiles, st)
+             : wide   ? launch_gemm_wide(g1, true, routed_tiles + shared_tiles, st)
                     : launch_gemm(g1, true, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
         if ((rc = prof_mark(5, st))) return rc;
         g2.As = WS(float, acts);
         g2.e_lo = 0;
         g2.e_hi = g1.e_hi;
-        rc = stream ? launch_gemm_stream(g2, false, false, stream_tiles, rows_all, st)
-             : wide ? launch_gemm_wide(g2, false, routed_tiles + shared_tiles, st)
+        rc = stream   ? launch_gemm_stream(g2, false, false, stream_tiles, rows_all, st)
+             : direct ? launch_gemm_wd(g2, false, routed_tiles + shared_tiles, st)
+             : wide   ? launch_gemm_wide(g2, false, routed_tiles + shared_tiles, st)
                     : launch_gemm(g2, false, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
     } else {

@@ -12,6 +12,8 @@ struct GemmArgs {
     const uint8_t *B;          // routed weights [E, Nrows, K] (FP4: [E, Nrows, K/2])
     const void *Bs;            // routed scales
     const uint8_t *Bsh;        // shared expert weights (FP8), used for e == E
+    const uint8_t *Bp;         // routed FP8 weights packed in fragment order (weight-direct kernels) or NULL
+    const uint8_t *Bshp;       // shared expert weights packed in fragment order
     const float *Bssh;         // shared expert scales
     const int32_t *offsets;    // [E+2] row offsets per expert (E = shared segment)
     const int32_t *tile_off;   // [E+2] tile offsets for tile height bm
@@ -56,6 +58,12 @@ int launch_gemm(const GemmArgs &a, bool gateup, bool fp4, int grid_y, hipStream_
 // a.tile_tab the tile table for that height.
 int wide_tile_rows();
 int launch_gemm_wide(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st);
+// Weight-direct tall-tile FP8 GEMMs (moe_gemm_wd.hip): the same tiles and
+// results as launch_gemm_wide, from fragment-packed weights (a.Bp, a.Bshp);
+// gate_up, or down with f32 rows (a.Cf).
+int launch_gemm_wd(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st);
+int wd_tile_rows();
+bool wd_supported(int64_t H, int64_t I);   // the layer shapes the weight-direct kernels take
 // Persistent stream-K GEMMs (moe_gemm_stream.hip): FP8 with a.bm 16 or 32,
 // MXFP4 with a.bm 16, 32 or 64.  tiles_max bounds the tile count of the
 // launch's range of the tile table, rows_max the positions; a.cnt holds one

@@ -33,7 +33,7 @@ class MoeTensors(C.Structure):
         "x", "router_w", "router_bias", "w13", "w13_scale", "w2", "w2_scale",
         "shared_w13", "shared_w13_scale", "shared_w2", "shared_w2_scale", "out",
         "logits", "topk_idx", "topk_w", "counts", "offsets", "perm", "inv", "norm_weight", "residual",
-        "act_q", "act_s", "y_rows")]
+        "act_q", "act_s", "y_rows", "w13_frag", "w2_frag", "shared_w13_frag", "shared_w2_frag")]
 
 
 EXPORTS = {
@@ -55,6 +55,7 @@ EXPORTS = {
     "xs_rmsnorm": (C.c_int, [P, P, C.c_int, I64, I64, C.c_float, P, P, P, P]),
     "xs_quant_weight_fp8_block": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P]),
     "xs_quant_weight_mxfp4": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P]),
+    "xs_pack_weight_fp8_frag": (C.c_int, [P, I64, I64, I64, P, P]),
     "xs_gemm_fp8_blockscale_workspace_size": (C.c_size_t, [I64, I64]),
     "xs_gemm_fp8_blockscale": (C.c_int, [P, P, P, I64, I64, I64, P, P, C.c_size_t, P]),
     "xs_moe_workspace_size": (C.c_size_t, [P]),
@@ -238,13 +239,27 @@ def gemm_fp8_blockscale(a, bq, bs, out=None, workspace=None):
     return out
 
 
+def pack_weight_fp8_frag(w):
+    """[..., n, k] e4m3 (uint8 or float8 view) -> a tensor of the same shape and
+    bytes in MFMA fragment order (xs_pack_weight_fp8_frag)."""
+    import torch
+    w = _u8(w).contiguous()
+    n, k = w.shape[-2], w.shape[-1]
+    batch = w.numel() // (n * k)
+    out = torch.empty_like(w)
+    check(lib().xs_pack_weight_fp8_frag(_ptr(w), batch, n, k, _ptr(out), _stream()))
+    return out
+
+
 class MoeLayer:
-    """Holds weights (device tensors) and calls xs_moe_forward."""
+    """Holds weights (device tensors) and calls xs_moe_forward.  frag=True also
+    keeps fragment-packed copies of the FP8 weights, which the prefill GEMMs
+    load straight into registers (same results)."""
 
     def __init__(self, router_w, w13, w13_scale, w2, w2_scale, top_k, router_bias=None,
                  shared=None, routed_format=XS_FP8_E4M3, n_group=1, topk_group=1,
                  renormalize=True, routed_scaling=1.0, router_exact=False, norm_weight=None,
-                 norm_eps=1e-6):
+                 norm_eps=1e-6, frag=False):
         self.router_w, self.router_bias = router_w, router_bias
         self.norm_weight, self.norm_eps = norm_weight, norm_eps
         self.w13, self.w13_scale, self.w2, self.w2_scale = _u8(w13), w13_scale, _u8(w2), w2_scale
@@ -255,6 +270,12 @@ class MoeLayer:
         self.E, self.H = router_w.shape
         self.I = w2.shape[-1] * (2 if routed_format == XS_FP4_E2M1X2 else 1)
         self._ws = None
+        self.frag = (None, None, None, None)
+        if frag and routed_format == XS_FP8_E4M3:
+            f = [pack_weight_fp8_frag(self.w13), pack_weight_fp8_frag(self.w2), None, None]
+            if self.shared is not None:
+                f[2], f[3] = pack_weight_fp8_frag(self.shared[0]), pack_weight_fp8_frag(self.shared[2])
+            self.frag = tuple(f)
 
     def params(self, T, x_dtype):
         return MoeParams(T, self.H, self.I, self.E, self.top_k, self.n_group, self.topk_group,
@@ -293,7 +314,8 @@ class MoeLayer:
                        *[_ptr(d.get(n)) for n in ("logits", "topk_idx", "topk_w", "counts",
                                                  "offsets", "perm", "inv")],
                        _ptr(self.norm_weight), _ptr(residual),
-                       *[_ptr(d.get(n)) for n in ("act_q", "act_s", "y_rows")])
+                       *[_ptr(d.get(n)) for n in ("act_q", "act_s", "y_rows")],
+                       *[_ptr(f) for f in self.frag])
         check(lib().xs_moe_forward(C.byref(p), C.byref(t), _ptr(ws), ws.numel(), _stream()))
         return out
 
@@ -306,6 +328,6 @@ class MoeLayer:
         t = MoeTensors(_ptr(x), _ptr(self.router_w), _ptr(self.router_bias), _ptr(self.w13),
                        _ptr(self.w13_scale), _ptr(self.w2), _ptr(self.w2_scale), _ptr(sh[0]),
                        _ptr(sh[1]), _ptr(sh[2]), _ptr(sh[3]), _ptr(out), *([None] * 7),
-                       _ptr(self.norm_weight), None, None, None, None)
+                       _ptr(self.norm_weight), None, None, None, None, *[_ptr(f) for f in self.frag])
         check(lib().xs_moe_forward_noalloc(C.byref(p), C.byref(t), _stream()))
         return out
