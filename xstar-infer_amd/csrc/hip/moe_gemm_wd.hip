@@ -22,10 +22,10 @@
 //     loop keeps the products of one subtile at a time, folded while the next
 //     subtile's MFMAs run);
 //   * activations (gathered token rows) alone use the LDS ring;
-//   * all loads are visible to the compiler (plain loads, and the LDS DMA
-//     builtin), so it tracks every register and counter wait itself; the
-//     block barrier carries no memory fence, and a step's activation stage is
-//     waited for explicitly.
+//   * the weight loads are plain loads, so the compiler tracks their registers
+//     and waits itself; the activation DMAs (which write no register) are
+//     issued from asm and waited for explicitly, and the block barrier
+//     carries no memory fence.
 #include "moe_gemm.hpp"
 
 namespace xs {
@@ -48,14 +48,24 @@ static_assert(kNSA >= kPD + 1 && kNSA * kStage + 8 * 1024 <= 160 * 1024 && kNSW 
 __device__ __forceinline__ int swz8(int r, int c) { return c ^ ((r >> 1) & 7); }
 __device__ __forceinline__ v8i cat(v4i a, v4i b) { return v8i{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]}; }
 typedef const __attribute__((address_space(1))) v4i gv4i;
-typedef __attribute__((address_space(3))) void lds_void;
 
-// LDS DMA through the compiler: lane i's `size` bytes from p land at lds + size i
-// (lds wave-uniform); the compiler sets M0 and the wait states.
-__device__ __forceinline__ void dma(const uint8_t *p, uint8_t *lds, int size)
+__device__ __forceinline__ uint32_t lds_addr(const void *p)
 {
-    if (size == 16) __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)lds, 16, 0, 0);
-    else __builtin_amdgcn_global_load_lds((const void *)p, (lds_void *)lds, 4, 0, 0);
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+// Wave-wide LDS DMA: lane i's 16 (4) bytes from sbase + voff land at lds + 16 i
+// (4 i).  Issued from asm, out of the compiler's sight: it writes no register,
+// and a compiler-visible DMA makes every later LDS read of the ring wait for
+// all of them (the ring's slots are one LDS object to its alias analysis), the
+// prefetch just issued included.  The wait states after the M0 write and the
+// scalar base are in the asm (s_nop 4); the counter waits are explicit.
+__device__ __forceinline__ void dma16(const uint8_t *sbase, uint32_t voff, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4(const uint8_t *sbase, uint32_t voff, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory");
 }
 // a wave-uniform pointer, made visibly uniform (SGPRs): the DMA then takes the
 // scalar-base form with a 32-bit lane offset instead of a 64-bit lane address
@@ -102,6 +112,7 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
 
     float *sB = reinterpret_cast<float *>(smem + kNSA * kStage);          // [2][KB] block scales
     float *red = sB + 2 * KB;                                            // [kNW][kBM] epilogue amax
+    uint8_t *trash = reinterpret_cast<uint8_t *>(red + kNW * kBM);       // [256] scale DMAs of the other waves
     {
         const float *Bsf = shared ? a.Bssh : reinterpret_cast<const float *>(a.Bs) + (size_t)e * (Nrows / 128) * KB;
         for (int q = tid; q < 2 * KB; q += kNT) {
@@ -134,12 +145,15 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
     const uint8_t *Wb0 = Wexp + (size_t)(wrow(0) / 16) * KB * 2048;
     const uint8_t *Wb1 = Wexp + (size_t)(wrow(1) / 16) * KB * 2048;
     const uint8_t *Sb = reinterpret_cast<const uint8_t *>(a.As);
+    const uint32_t ring = lds_addr(smem), trash_lds = lds_addr(trash);
     auto adma = [&](int k2) __attribute__((always_inline)) {
         const int kk = min(k2, KB - 1);
-        uint8_t *sl = smem + (k2 % kNSA) * kStage;
+        const uint32_t sl = ring + (uint32_t)((k2 % kNSA) * kStage);
 #pragma unroll
-        for (int u = 0; u < kNA; ++u) dma(a.A + (size_t)kk * 128 + oA[u], sl + 1024 * (wave + kNW * u), 16);
-        if (sw) dma(uniform(Sb + (size_t)kk * 4) + oS, sl + kAB + 256 * wave, 4);
+        for (int u = 0; u < kNA; ++u) dma16(uniform(a.A + (size_t)kk * 128), oA[u], sl + 1024 * (wave + kNW * u));
+        // every wave issues the scale DMA (the waves past the scales into the
+        // trash line), so every wave's counter sees the same loads
+        dma4(uniform(Sb + (size_t)kk * 4), oS, sw ? sl + kAB + 256 * wave : trash_lds);
     };
     // each fragment is loaded straight into the 8 registers its MFMA reads
     auto wload = [&](int k2, v8i (&w)[2]) __attribute__((always_inline)) {
@@ -155,10 +169,10 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
             w[1] = cat(*(gv4i *)(p1 + 16 * lane), *(gv4i *)(p1 + 16 * lane + 1024));
         }
     };
-    // loads per wave per step, in issue order: activation DMAs (+1 scale DMA
-    // on the scale waves) after the step's barrier, then the 4 weight loads
-    // after its last MFMA (into the registers that MFMA has just read)
-    constexpr int P = kNA + 4;
+    // loads per wave per step, in issue order: activation DMAs and the scale
+    // DMA after the step's barrier, then the 4 weight loads after its last
+    // MFMA (into the registers that MFMA has just read)
+    constexpr int P = kNA + 1 + 4;
 
     v4f acc[kMI][2];
 #pragma unroll
@@ -181,8 +195,7 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
             if (k >= KB) break;
             // loads retire in order: step k (activations and weights) has landed
             // when only the later kPD-1 steps' loads are outstanding
-            if (sw) wait_vm<(kPD - 1) * (P + 1)>();
-            else wait_vm<(kPD - 1) * P>();
+            wait_vm<(kPD - 1) * P>();
             barrier_lds();   // step k's activations landed everywhere; slot (k-1) % kNSA is free
             adma(k + kPD);
             const uint8_t *sA = smem + (k % kNSA) * kStage;
@@ -346,7 +359,7 @@ int launch_gemm_wd(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
     const int gx = gateup ? a.N / 128 : a.N / 256;
     if (a.K % (128 * kPD) || gx % 4 || !a.tile_tab || !a.Bp || !a.Bshp || (!gateup && !a.Cf))
         return set_error(XS_ERR_UNSUPPORTED, "weight-direct GEMM shape K=%d N=%d", a.K, a.N);
-    const size_t smem = (size_t)kNSA * kStage + 8 * (size_t)(a.K / 128) + 4 * kNW * kBM;
+    const size_t smem = (size_t)kNSA * kStage + 8 * (size_t)(a.K / 128) + 4 * kNW * kBM + 256;
     if (smem > 160 * 1024) return set_error(XS_ERR_UNSUPPORTED, "K=%d needs %zu bytes of LDS", a.K, smem);
     auto fn = gateup ? moe_gemm_wd_kernel<true> : moe_gemm_wd_kernel<false>;
     static bool attr_set[2] = {false, false};
