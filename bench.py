@@ -211,7 +211,9 @@ def prefill(a, X, torch):
     from moe_synth import synth_layer, layer_from, expert_bytes, layer_flops
     T = 8192
     g = synth_layer(T, H, I, E, K_TOP, seed=0, zipf=1.1)
-    layer = layer_from(g)
+    # XS_BENCH_FRAG=1: the layer also holds fragment-packed FP8 weights, and
+    # the prefill GEMMs take the weight-direct kernels (measurements)
+    layer = layer_from(g, frag=os.environ.get("XS_BENCH_FRAG", "0") == "1")
     ms, stages = time_forward(layer, g["x"], a.steps, a.warmup, profile=True)
     flops = layer_flops(T, H, I, E, K_TOP)
     counts = routed_counts(layer, g["x"])
