@@ -1,0 +1,314 @@
+// CPU emulation shim for the DMA-ring GEMM kernels: one host thread per GPU
+// lane, block barriers, wave exchanges for readfirstlane / shuffles / MFMA,
+// DMA ops queued per lane and landed at s_waitcnt (LATE mode) or at issue
+// (EARLY mode), bounds-checked against registered buffers and the LDS size.
+#pragma once
+#include <atomic>
+#include <barrier>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <deque>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <type_traits>
+#include <vector>
+#include <algorithm>
+#include <sys/mman.h>
+#include <unistd.h>
+
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __launch_bounds__(x)
+#define __HIP_MEMORY_SCOPE_AGENT 0
+#define __hip_atomic_fetch_add(p, v, o, s) __atomic_fetch_add(p, v, o)
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+static constexpr int WAVE = 64;
+struct alignas(16) int4 { int x, y, z, w; };
+using std::min;
+using std::max;
+#define static_assert(...)
+
+struct EmuDim { unsigned x = 0, y = 0, z = 0; };
+inline thread_local EmuDim threadIdx, blockIdx;
+inline EmuDim gridDim, blockDim;
+
+// ------------------------------------------------------------ global buffers
+struct Region { const uint8_t *p; size_t n; std::string name; };
+inline std::vector<Region> g_regions;
+inline std::atomic<long> g_errors{0};
+inline std::mutex g_print;
+#define EMU_ERR(...) do { std::lock_guard<std::mutex> _l(g_print); if (g_errors++ < 40) { fprintf(stderr, "[emu] b%u t%u: ", blockIdx.x, threadIdx.x); fprintf(stderr, __VA_ARGS__); fputc('\n', stderr); } } while (0)
+
+// buffer that ends at a PROT_NONE page: plain out-of-bounds accesses fault
+inline void *emu_alloc(size_t n, const char *name)
+{
+    const size_t pg = 4096, body = (n + pg - 1) / pg * pg;
+    uint8_t *base = (uint8_t *)mmap(nullptr, body + pg, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS, -1, 0);
+    mprotect(base + body, pg, PROT_NONE);
+    uint8_t *p = base + body - n;
+    g_regions.push_back({p, n, name});
+    return p;
+}
+inline const char *emu_check_global(const void *src, size_t n)
+{
+    const uint8_t *s = (const uint8_t *)src;
+    for (auto &r : g_regions)
+        if (s >= r.p && s + n <= r.p + r.n) return r.name.c_str();
+    return nullptr;
+}
+
+// ------------------------------------------------------------ block context
+enum { MODE_LATE = 0, MODE_EARLY = 1 };
+inline int g_mode = MODE_LATE;
+
+struct Op { int kind; const uint8_t *src; uint32_t dst; int n; int32_t *atom; int32_t *result; };
+struct Blk {
+    uint8_t *smem; size_t smem_size;
+    std::barrier<> *bar;
+    std::barrier<> *wbar[16];
+    uint64_t xch[16][64];
+    uint8_t wx[16][64][64];
+};
+inline thread_local Blk *tb;
+inline thread_local std::deque<Op> tq;
+inline thread_local int32_t t_claims[64];
+inline thread_local int t_nclaim;
+
+inline uint8_t *emu_smem() { return tb->smem; }
+inline uint32_t lds_addr(const void *p) { return (uint32_t)((const uint8_t *)p - tb->smem); }
+
+inline void __syncthreads() { tb->bar->arrive_and_wait(); }
+inline int wave_id() { return threadIdx.x / 64; }
+inline int lane_id() { return threadIdx.x % 64; }
+
+// wave-wide: every lane posts v, returns lane 0's; flags non-uniform values
+inline uint64_t wave_first(uint64_t v, const char *what)
+{
+    const int w = wave_id(), l = lane_id();
+    tb->xch[w][l] = v;
+    tb->wbar[w]->arrive_and_wait();
+    const uint64_t r = tb->xch[w][0];
+    if (r != v) EMU_ERR("non-uniform %s: lane %d has %llx, lane 0 %llx", what, l, (unsigned long long)v, (unsigned long long)r);
+    tb->wbar[w]->arrive_and_wait();
+    return r;
+}
+template <typename T>
+inline T emu_rfl(T v)
+{
+    uint64_t u = 0;
+    memcpy(&u, &v, sizeof(T));
+    u = wave_first(u, "readfirstlane");
+    T r;
+    memcpy(&r, &u, sizeof(T));
+    return r;
+}
+#define __builtin_amdgcn_readfirstlane(x) emu_rfl(x)
+#define __builtin_amdgcn_sched_barrier(x) ((void)0)
+
+inline float __shfl_xor(float v, int m, int)
+{
+    const int w = wave_id(), l = lane_id();
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    tb->xch[w][l] = u;
+    tb->wbar[w]->arrive_and_wait();
+    uint32_t o = (uint32_t)tb->xch[w][l ^ m];
+    tb->wbar[w]->arrive_and_wait();
+    float r;
+    memcpy(&r, &o, 4);
+    return r;
+}
+
+// ------------------------------------------------------------ DMA
+inline void land(const Op &o)
+{
+    if (o.kind == 1) {   // atomic: result delivered
+        if (o.result) *o.result = *o.result;   // value fixed at issue
+        return;
+    }
+    if (o.src) memcpy(tb->smem + o.dst, o.src, o.n);
+}
+inline void push(Op o)
+{
+    if (g_mode == MODE_EARLY) { land(o); return; }
+    if (o.kind == 0) memset(tb->smem + o.dst, 0xA5, o.n);   // poison until landed
+    tq.push_back(o);
+}
+inline void emu_wait(int n)
+{
+    while ((int)tq.size() > n) { land(tq.front()); tq.pop_front(); }
+}
+template <int N>
+inline void wait_vm() { emu_wait(N); }
+
+inline void dma_lane(const uint8_t *src, uint32_t lds_base, int bytes, const char *what)
+{
+    const uint32_t dst = lds_base + (uint32_t)(bytes * lane_id());
+    if (!emu_check_global(src, bytes)) EMU_ERR("%s: global source %p (+%d) outside every buffer", what, (const void *)src, bytes);
+    if ((size_t)dst + bytes > tb->smem_size) {
+        EMU_ERR("%s: LDS destination %u..%u past the %zu-byte allocation", what, dst, dst + bytes, tb->smem_size);
+        return;
+    }
+    bool ok = emu_check_global(src, bytes) != nullptr;
+    push(Op{0, ok ? src : nullptr, dst, bytes, nullptr, nullptr});
+}
+inline void dma16(const uint8_t *sbase, uint32_t voff, uint32_t lds)
+{
+    sbase = (const uint8_t *)wave_first((uint64_t)(uintptr_t)sbase, "dma16 sbase");
+    lds = (uint32_t)wave_first(lds, "dma16 lds");
+    dma_lane(sbase + voff, lds, 16, "dma16");
+}
+inline void dma16_nt(const uint8_t *sbase, uint32_t voff, uint32_t lds) { dma16(sbase, voff, lds); }
+inline void dma4(const uint8_t *sbase, uint32_t voff, uint32_t lds)
+{
+    sbase = (const uint8_t *)wave_first((uint64_t)(uintptr_t)sbase, "dma4 sbase");
+    lds = (uint32_t)wave_first(lds, "dma4 lds");
+    dma_lane(sbase + voff, lds, 4, "dma4");
+}
+inline void dma4s(const void *g, uint32_t lds)
+{
+    lds = (uint32_t)wave_first(lds, "dma4s lds");
+    dma_lane((const uint8_t *)g, lds, 4, "dma4s");
+}
+// returning atomic issued by one lane: the value is fixed now, readable after its wait
+inline uint32_t emu_atomic_issue(int32_t *p, uint32_t v)
+{
+    if (!emu_check_global(p, 4)) EMU_ERR("atomic outside every buffer");
+    const int32_t old = __atomic_fetch_add(p, (int32_t)v, __ATOMIC_RELAXED);
+    t_claims[t_nclaim & 63] = old;
+    Op o{1, nullptr, 0, 0, p, &t_claims[t_nclaim & 63]};
+    ++t_nclaim;
+    if (g_mode == MODE_LATE) tq.push_back(o);
+    return (uint32_t)old;
+}
+inline void emu_check_claim_retired()
+{
+    for (auto &o : tq)
+        if (o.kind == 1) EMU_ERR("claim read while its atomic is still outstanding");
+}
+
+// ------------------------------------------------------------ math stand-ins
+inline float __fdiv_rn(float a, float b) { return a / b; }
+inline float fast_sigmoid(float x) { return 1.f / (1.f + std::exp(-x)); }
+inline uint16_t bf16_from_f32(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return (uint16_t)((u + 0x7fff + ((u >> 16) & 1)) >> 16);
+}
+inline uint32_t e4m3_enc(float f)
+{
+    // round-to-nearest e4m3fn, saturating (values pre-clamped to +-448)
+    uint32_t s = std::signbit(f) ? 0x80 : 0;
+    float a = std::fabs(f);
+    if (!(a > 0)) return s;
+    int e;
+    float m = std::frexp(a, &e);   // a = m 2^e, m in [0.5, 1)
+    int E = e - 1 + 7;
+    if (E <= 0) {   // subnormal: step 2^-9
+        int q = (int)std::nearbyint(a * 512.f);
+        return s | (uint32_t)q;
+    }
+    int q = (int)std::nearbyint((m * 2 - 1) * 8);
+    if (q == 8) { q = 0; ++E; }
+    if (E > 15 || (E == 15 && q > 6)) { E = 15; q = 6; }
+    return s | (uint32_t)(E << 3) | (uint32_t)q;
+}
+inline uint32_t e4m3_pack2_hw(float a, float b) { return e4m3_enc(a) | (e4m3_enc(b) << 8); }
+inline float e4m3_dec(uint8_t b)
+{
+    const int s = b >> 7, E = (b >> 3) & 15, m = b & 7;
+    float v = E ? std::ldexp(1.f + m / 8.f, E - 7) : std::ldexp(m / 8.f, -6);
+    if (E == 15 && m == 7) v = NAN;
+    return s ? -v : v;
+}
+
+// v_mfma_f32_16x16x128_f8f6f4 (FP8 e4m3 both): lane 16g + r supplies row r,
+// K bytes [16g, 16g+16) and [64+16g, 64+16g+16); lane 16g + r receives
+// C[4g + v][r], C[m][n] = sum_k A[m][k] B[n][k]
+inline bool g_math = false;
+inline v4f emu_mfma(v8i a, v8i b, v4f c, int, int, int, int, int, int)
+{
+    if (!g_math) return c;
+    const int w = wave_id(), l = lane_id();
+    memcpy(tb->wx[w][l], &a, 32);
+    memcpy(tb->wx[w][l] + 32, &b, 32);
+    tb->wbar[w]->arrive_and_wait();
+    const int r = l & 15, g = l >> 4;
+    v4f out = c;
+    auto kbyte = [&](int lane_row, int k, int off) -> uint8_t {   // byte k of row lane_row
+        const int chunk = k / 16, gg = chunk & 3, hi = chunk >> 2;
+        return tb->wx[w][16 * gg + lane_row][off + 16 * hi + (k & 15)];
+    };
+    for (int v = 0; v < 4; ++v) {
+        float s = 0;
+        for (int k = 0; k < 128; ++k) s += e4m3_dec(kbyte(4 * g + v, k, 0)) * e4m3_dec(kbyte(r, k, 32));
+        out[v] += s;
+    }
+    tb->wbar[w]->arrive_and_wait();
+    return out;
+}
+#define __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4 emu_mfma
+
+// ------------------------------------------------------------ launch
+template <typename F>
+inline void emu_launch(F fn, unsigned gx, unsigned gy, unsigned nt, size_t smem, unsigned conc)
+{
+    gridDim = {gx, gy, 1};
+    blockDim = {nt, 1, 1};
+    std::vector<std::pair<unsigned, unsigned>> blocks;
+    for (unsigned y = 0; y < gy; ++y)
+        for (unsigned x = 0; x < gx; ++x) blocks.push_back({x, y});
+    for (size_t b0 = 0; b0 < blocks.size(); b0 += conc) {
+        const size_t nb = std::min<size_t>(conc, blocks.size() - b0);
+        std::vector<Blk *> bk(nb);
+        std::vector<std::thread> th;
+        for (size_t i = 0; i < nb; ++i) {
+            Blk *B = new Blk();
+            B->smem_size = smem;
+            B->smem = (uint8_t *)aligned_alloc(256, (smem + 255) / 256 * 256 + 256);
+            memset(B->smem, 0x5A, smem);
+            B->bar = new std::barrier<>(nt);
+            for (unsigned w = 0; w < nt / 64; ++w) B->wbar[w] = new std::barrier<>(64);
+            bk[i] = B;
+            for (unsigned t = 0; t < nt; ++t)
+                th.emplace_back([=] {
+                    threadIdx = {t, 0, 0};
+                    blockIdx = {blocks[b0 + i].first, blocks[b0 + i].second, 0};
+                    tb = B;
+                    tq.clear();
+                    fn();
+                    if (!tq.empty()) EMU_ERR("lane exits with %zu DMA ops outstanding", tq.size());
+                    emu_wait(0);
+                    B->wbar[t / 64]->arrive_and_drop();
+                    B->bar->arrive_and_drop();
+                });
+        }
+        for (auto &t : th) t.join();
+        for (auto *B : bk) {
+            free(B->smem);
+            delete B->bar;
+            for (unsigned w = 0; w < nt / 64; ++w) delete B->wbar[w];
+            delete B;
+        }
+    }
+}
+inline uint32_t emu_first_lane(uint32_t v)
+{
+    const int w = wave_id(), l = lane_id();
+    tb->xch[w][l] = v;
+    tb->wbar[w]->arrive_and_wait();
+    const uint32_t r = (uint32_t)tb->xch[w][0];
+    tb->wbar[w]->arrive_and_wait();
+    return r;
+}
