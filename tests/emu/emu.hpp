@@ -162,10 +162,59 @@ inline void dma_lane(const uint8_t *src, uint32_t lds_base, int bytes, const cha
     bool ok = emu_check_global(src, bytes) != nullptr;
     push(Op{0, ok ? src : nullptr, dst, bytes, nullptr, nullptr});
 }
+// Hazard model (g_hazard bits; off by default): 1 = an LDS DMA reads M0
+// before the s_mov_b32 m0 ahead of it has taken effect, so it lands at the
+// previous DMA's LDS destination; 2 = a VMEM instruction reads its scalar base
+// before the v_readfirstlane that wrote it has, so it uses the wave's
+// previous base.  Each DMA is hit with probability g_hazard_p, the same
+// choice for every lane of the wave (hash of block, wave, DMA ordinal).
+inline int g_hazard = 0;
+inline double g_hazard_p = 0.0;
+inline unsigned g_hazard_seed = 1;
+inline thread_local uint32_t t_m0 = 0;
+inline thread_local const uint8_t *t_sbase = nullptr;
+inline thread_local uint64_t t_ndma = 0;
+inline std::atomic<long> g_hazard_hits{0};
+inline bool hazard_hit(int salt)
+{
+    uint64_t z = ((uint64_t)blockIdx.x << 40) ^ ((uint64_t)blockIdx.y << 28) ^ ((uint64_t)wave_id() << 20) ^
+                 (t_ndma * 4 + salt) ^ ((uint64_t)g_hazard_seed << 52);
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    z ^= z >> 31;
+    return (double)(z >> 11) * (1.0 / 9007199254740992.0) < g_hazard_p;
+}
+inline uint32_t hazard_m0(uint32_t lds)
+{
+    uint32_t used = lds;
+    if ((g_hazard & 1) && t_ndma > 0 && hazard_hit(1)) {
+        used = t_m0;
+        if (lane_id() == 0) {
+            ++g_hazard_hits;
+            if (getenv("EMU_HAZARD_LOG")) { std::lock_guard<std::mutex> _l(g_print); fprintf(stderr, "[hit] b%u w%d dma#%llu: meant LDS %u, landed at %u\n", blockIdx.x, wave_id(), (unsigned long long)t_ndma, lds, used); }
+        }
+    }
+    t_m0 = lds;
+    return used;
+}
+inline const uint8_t *hazard_sbase(const uint8_t *sbase)
+{
+    const uint8_t *used = sbase;
+    if ((g_hazard & 2) && t_sbase && hazard_hit(2)) {
+        used = t_sbase;
+        if (lane_id() == 0) ++g_hazard_hits;
+    }
+    t_sbase = sbase;
+    return used;
+}
 inline void dma16(const uint8_t *sbase, uint32_t voff, uint32_t lds)
 {
     sbase = (const uint8_t *)wave_first((uint64_t)(uintptr_t)sbase, "dma16 sbase");
     lds = (uint32_t)wave_first(lds, "dma16 lds");
+    sbase = hazard_sbase(sbase);
+    lds = hazard_m0(lds);
+    ++t_ndma;
     dma_lane(sbase + voff, lds, 16, "dma16");
 }
 inline void dma16_nt(const uint8_t *sbase, uint32_t voff, uint32_t lds) { dma16(sbase, voff, lds); }
@@ -173,11 +222,16 @@ inline void dma4(const uint8_t *sbase, uint32_t voff, uint32_t lds)
 {
     sbase = (const uint8_t *)wave_first((uint64_t)(uintptr_t)sbase, "dma4 sbase");
     lds = (uint32_t)wave_first(lds, "dma4 lds");
+    sbase = hazard_sbase(sbase);
+    lds = hazard_m0(lds);
+    ++t_ndma;
     dma_lane(sbase + voff, lds, 4, "dma4");
 }
 inline void dma4s(const void *g, uint32_t lds)
 {
     lds = (uint32_t)wave_first(lds, "dma4s lds");
+    lds = hazard_m0(lds);
+    ++t_ndma;
     dma_lane((const uint8_t *)g, lds, 4, "dma4s");
 }
 // returning atomic issued by one lane: the value is fixed now, readable after its wait
@@ -287,6 +341,7 @@ inline void emu_launch(F fn, unsigned gx, unsigned gy, unsigned nt, size_t smem,
                     blockIdx = {blocks[b0 + i].first, blocks[b0 + i].second, 0};
                     tb = B;
                     tq.clear();
+                    t_m0 = 0; t_sbase = nullptr; t_ndma = 0;
                     fn();
                     if (!tq.empty()) EMU_ERR("lane exits with %zu DMA ops outstanding", tq.size());
                     emu_wait(0);

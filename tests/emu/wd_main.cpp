@@ -3,6 +3,7 @@
 // the kernel's own source, then both are checked against a float64
 // recomputation from the same FP8 inputs.
 // usage: wd_emu T E k zipf seed H I conc mode(0 late,1 early) math(0/1) shared(0/1)
+// EMU_HAZARD=1|2|3, EMU_HAZARD_P, EMU_HAZARD_SEED: the wait-state hazard model of emu.hpp
 #include "emu.hpp"
 #include <algorithm>
 #include <numeric>
@@ -37,6 +38,9 @@ int main(int argc, char **argv)
     g_mode = argc > 9 ? atoi(argv[9]) : 0;
     g_math = argc > 10 ? atoi(argv[10]) : 1;
     int shared = argc > 11 ? atoi(argv[11]) : 1;
+    if (getenv("EMU_HAZARD")) g_hazard = atoi(getenv("EMU_HAZARD"));
+    if (getenv("EMU_HAZARD_P")) g_hazard_p = atof(getenv("EMU_HAZARD_P"));
+    if (getenv("EMU_HAZARD_SEED")) g_hazard_seed = atoi(getenv("EMU_HAZARD_SEED"));
     const int BM = kBM;
     std::mt19937 rng(seed);
 
@@ -187,6 +191,7 @@ int main(int argc, char **argv)
         }
         printf("down y: max abs err %.4g, max |ref| %.4g, rel %.4g\n", maxerr, maxref, maxerr / maxref);
     }
+    if (g_hazard) printf("hazard hits %ld\n", g_hazard_hits.load());
     printf("errors %ld\n", g_errors.load());
     return g_errors.load() ? 1 : 0;
 }

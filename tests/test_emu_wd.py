@@ -50,3 +50,19 @@ def test_weight_direct_gemms_emulated(wd_emu):
     assert act < 0.0625, out[-2000:]
     # down is f32 accumulation of exact FP8 products
     assert y < 1e-5, out[-2000:]
+
+
+def test_emulated_check_catches_misdirected_dma(wd_emu):
+    # the same case with the M0 wait-state hazard modelled (1% of DMAs land at
+    # the previous DMA's LDS destination): the check above must then fail
+    env = dict(os.environ, EMU_HAZARD="1", EMU_HAZARD_P="0.01", EMU_HAZARD_SEED="7")
+    r = subprocess.run([wd_emu, "64", "4", "2", "1.1", "3", "1024", "512", "4", "0", "1", "1"],
+                       capture_output=True, text=True, timeout=600, env=env)
+    out = r.stdout + r.stderr
+    hits = int(re.search(r"hazard hits (\d+)", out).group(1))
+    assert hits > 0, out[-2000:]
+    m_act = re.search(r"gate_up act: .* rel (\S+)", out)
+    m_y = re.search(r"down y: .* rel (\S+)", out)
+    act = float(m_act.group(1)) if m_act else float("inf")
+    y = float(m_y.group(1)) if m_y else float("inf")
+    assert r.returncode != 0 or not (act < 0.0625 and y < 1e-5), out[-2000:]
