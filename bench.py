@@ -212,7 +212,7 @@ def prefill(a, X, torch):
     T = 8192
     g = synth_layer(T, H, I, E, K_TOP, seed=0, zipf=1.1)
     # XS_BENCH_FRAG=1: the layer also holds fragment-packed FP8 weights, and
-    # the prefill GEMMs take the weight-direct kernels (measurements)
+    # the prefill GEMMs take the weight-direct kernels
     layer = layer_from(g, frag=os.environ.get("XS_BENCH_FRAG", "0") == "1")
     ms, stages = time_forward(layer, g["x"], a.steps, a.warmup, profile=True)
     flops = layer_flops(T, H, I, E, K_TOP)
@@ -283,8 +283,9 @@ def decode(a, X, torch):
     from moe_synth import synth_layer, layer_from, expert_bytes
     dec = {}
     gd = synth_layer(256, H, I, E, K_TOP, seed=1, bias_std=0.0)
+    # XS_BENCH_FRAG=1: fragment-packed FP8 weights, weight-direct decode GEMMs
+    L = layer_from(gd, frag=os.environ.get("XS_BENCH_FRAG", "0") == "1")
     for Td in (int(t) for t in a.decode_tokens.split(",")):
-        L = layer_from(gd)
         xd = gd["x"][:Td].contiguous()
         msd, st = time_forward(L, xd, max(a.steps, 50), a.warmup, profile=True)
         ned = routed_expert_count(L, xd)

@@ -85,6 +85,18 @@ inline thread_local int32_t t_claims[64];
 inline thread_local int t_nclaim;
 
 inline uint8_t *emu_smem() { return tb->smem; }
+// static __shared__ arrays: carved from the block's LDS in declaration order
+// (every lane declares them in the same order, so all get the same offsets)
+inline thread_local size_t t_shoff = 0;
+template <typename T>
+inline T *emu_shared(size_t n)
+{
+    t_shoff = (t_shoff + 15) / 16 * 16;
+    T *p = reinterpret_cast<T *>(tb->smem + t_shoff);
+    t_shoff += n * sizeof(T);
+    if (t_shoff > tb->smem_size) EMU_ERR("static LDS arrays need %zu bytes, the launch gave %zu", t_shoff, tb->smem_size);
+    return p;
+}
 inline uint32_t lds_addr(const void *p) { return (uint32_t)((const uint8_t *)p - tb->smem); }
 
 inline void __syncthreads() { tb->bar->arrive_and_wait(); }
@@ -341,7 +353,7 @@ inline void emu_launch(F fn, unsigned gx, unsigned gy, unsigned nt, size_t smem,
                     blockIdx = {blocks[b0 + i].first, blocks[b0 + i].second, 0};
                     tb = B;
                     tq.clear();
-                    t_m0 = 0; t_sbase = nullptr; t_ndma = 0;
+                    t_m0 = 0; t_sbase = nullptr; t_ndma = 0; t_shoff = 0;
                     fn();
                     if (!tq.empty()) EMU_ERR("lane exits with %zu DMA ops outstanding", tq.size());
                     emu_wait(0);

@@ -250,6 +250,11 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
                         (!p->has_shared || (t->shared_w13_frag && t->shared_w2_frag)) && wd_supported(H, I) &&
                         getenv_flag("XS_WIDE_DIRECT", true);
     const int bm = direct ? wd_tile_rows() : wide ? wide_tile_rows() : pick_bm((double)S / (double)E);
+    // weight-direct decode GEMMs for 16-row tiles, likewise from the packed
+    // weights (XS_DECODE_DIRECT=0 keeps the LDS-ring and stream-K kernels)
+    const bool ddirect = !wide && !fp4 && bm == 16 && t->w13_frag && t->w2_frag &&
+                         (!p->has_shared || (t->shared_w13_frag && t->shared_w2_frag)) && wdd_supported(H, I) &&
+                         getenv_flag("XS_DECODE_DIRECT", true);
     PermuteOut po = {};
     po.counts = WS(int32_t, counts);
     po.offsets = offsets;
@@ -271,7 +276,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     // FP8: all tiles in one launch; MXFP4: the routed tiles (the FP8 shared
     // expert runs the tiled kernel)
     const int stream_tiles = fp4 ? routed_tiles : routed_tiles + shared_tiles;
-    const bool stream = stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
+    const bool stream = !ddirect && stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
                         (sm == 2 || (sm == 1 && stream_items(true, (int)I, stream_tiles) >= 2 * (int64_t)stream_blocks()));
     if (stream) {
         po.zero = WS(int32_t, cnt1);
@@ -348,6 +353,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g1.e_hi = (int)E + (shared_rows ? 1 : 0);
         rc = stream   ? launch_gemm_stream(g1, true, false, stream_tiles, rows_all, st)
              : direct ? launch_gemm_wd(g1, true, routed_tiles + shared_tiles, st)
+             : ddirect ? launch_gemm_wdd(g1, true, routed_tiles + shared_tiles, st)
              : wide   ? launch_gemm_wide(g1, true, routed_tiles + shared_tiles, st)
                     : launch_gemm(g1, true, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;
@@ -357,6 +363,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g2.e_hi = g1.e_hi;
         rc = stream   ? launch_gemm_stream(g2, false, false, stream_tiles, rows_all, st)
              : direct ? launch_gemm_wd(g2, false, routed_tiles + shared_tiles, st)
+             : ddirect ? launch_gemm_wdd(g2, false, routed_tiles + shared_tiles, st)
              : wide   ? launch_gemm_wide(g2, false, routed_tiles + shared_tiles, st)
                     : launch_gemm(g2, false, false, routed_tiles + shared_tiles, st);
         if (rc) return rc;

@@ -64,6 +64,11 @@ int launch_gemm_wide(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
 int launch_gemm_wd(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st);
 int wd_tile_rows();
 bool wd_supported(int64_t H, int64_t I);   // the layer shapes the weight-direct kernels take
+// Weight-direct decode GEMMs (moe_gemm_wdd.hip): 16-row tiles (a.bm 16), the
+// same results as launch_gemm at that height, from fragment-packed weights;
+// gate_up, or down with f32 rows (a.Cf).  K of 512, 1024, 2048 or 4096.
+int launch_gemm_wdd(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st);
+bool wdd_supported(int64_t H, int64_t I);
 // Persistent stream-K GEMMs (moe_gemm_stream.hip): FP8 with a.bm 16 or 32,
 // MXFP4 with a.bm 16, 32 or 64.  tiles_max bounds the tile count of the
 // launch's range of the tile table, rows_max the positions; a.cnt holds one

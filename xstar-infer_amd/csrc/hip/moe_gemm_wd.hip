@@ -357,7 +357,7 @@ int launch_gemm_wd(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
     if (grid_y <= 0) return XS_OK;
     if (a.bm != kBM) return set_error(XS_ERR_INVALID, "weight-direct GEMM needs %d-row tiles", kBM);
     const int gx = gateup ? a.N / 128 : a.N / 256;
-    if (a.K % (128 * kPD) || gx % 4 || !a.tile_tab || !a.Bp || !a.Bshp || (!gateup && !a.Cf))
+    if (a.K % (128 * kPD) || gx % 4 || !a.tile_tab || !a.Bp || (a.e_hi > a.E && !a.Bshp) || (!gateup && !a.Cf))
         return set_error(XS_ERR_UNSUPPORTED, "weight-direct GEMM shape K=%d N=%d", a.K, a.N);
     const size_t smem = (size_t)kNSA * kStage + 8 * (size_t)(a.K / 128) + 4 * kNW * kBM + 256;
     if (smem > 160 * 1024) return set_error(XS_ERR_UNSUPPORTED, "K=%d needs %zu bytes of LDS", a.K, smem);

@@ -253,7 +253,7 @@ def pack_weight_fp8_frag(w):
 
 class MoeLayer:
     """Holds weights (device tensors) and calls xs_moe_forward.  frag=True also
-    keeps fragment-packed copies of the FP8 weights, which the prefill GEMMs
+    keeps fragment-packed copies of the FP8 weights, which the prefill and decode GEMMs
     load straight into registers (same results)."""
 
     def __init__(self, router_w, w13, w13_scale, w2, w2_scale, top_k, router_bias=None,
