@@ -46,6 +46,7 @@ def main(src_path, hdr_path, out_path):
     body = replace(body, "*(gv4i *)(", "wd_gload(")
     body = replace(body, "extern __shared__ __attribute__((aligned(16))) uint8_t smem[];",
                    "uint8_t *smem = emu_smem();")
+    body = replace(body, 'asm volatile("" : "+v"(acc[fi][0]), "+v"(acc[fi][1]));', "")
     assert "asm volatile" not in body, "an asm statement the emulator has no stand-in for"
     ga = hdr[hdr.index("struct GemmArgs"):]
     ga = ga[:ga.index("};") + 2]

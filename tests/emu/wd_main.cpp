@@ -136,8 +136,14 @@ int main(int argc, char **argv)
         const int gy = tt + nsh;
         const unsigned nb = (unsigned)(((gy + 7) / 8 * (gx / 4) + 7) / 8 * 256);
         printf("pass %d: smem %zu, blocks %u\n", pass, smem, nb);
-        if (pass == 0) emu_launch([&] { moe_gemm_wd_kernel<true>(a); }, nb, 1, kNT, smem, conc);
-        else emu_launch([&] { moe_gemm_wd_kernel<false>(a); }, nb, 1, kNT, smem, conc);
+        // the launcher's choice: unrolled kernels for 4, 8, 16 and 32 K steps
+#define XS_EMU_KB(KBV)                                                                                  \
+        if (KB == KBV || KBV == 0) {                                                                    \
+            if (pass == 0) emu_launch([&] { moe_gemm_wd_kernel<true, KBV>(a); }, nb, 1, kNT, smem, conc); \
+            else emu_launch([&] { moe_gemm_wd_kernel<false, KBV>(a); }, nb, 1, kNT, smem, conc);          \
+        } else
+        XS_EMU_KB(4) XS_EMU_KB(8) XS_EMU_KB(16) XS_EMU_KB(32) XS_EMU_KB(0) {}
+#undef XS_EMU_KB
         printf("pass %d done, errors %ld\n", pass, g_errors.load());
     }
 

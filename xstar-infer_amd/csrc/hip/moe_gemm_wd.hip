@@ -91,10 +91,12 @@ __device__ __forceinline__ void barrier_lds()
 // (loaded and multiplied, never stored).  A tile short enough for that to
 // matter streams its expert's weights from HBM, which bounds it anyway, and a
 // single path keeps the register budget of one loop.
-template <bool GATEUP>
+// KBT > 0: K / 128, known at compile time (the K loop is unrolled in full, so the
+// compiler's waits for the weight registers are exact at every step); 0: any K.
+template <bool GATEUP, int KBT>
 __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, int rows, int slab, uint8_t *smem)
 {
-    const int KB = a.K / 128;   // a multiple of kPD (checked at launch)
+    const int KB = KBT ? KBT : a.K / 128;   // a multiple of kPD (checked at launch)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r16 = lane & 15, g = lane >> 4;
@@ -188,6 +190,7 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
     v4f q[2][2];
     float cl = 0.f, cl1 = 0.f;   // fold factors of the previous subtile (first fold: zeros)
     q[(kMI - 1) & 1][0] = q[(kMI - 1) & 1][1] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
     for (int k0 = 0; k0 < KB; k0 += kPD) {
 #pragma unroll
         for (int p = 0; p < kPD; ++p) {
@@ -226,6 +229,9 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
                     acc[fi][0][e] = __builtin_fmaf(q[fi & 1][0][e], cl, acc[fi][0][e]);
                     acc[fi][1][e] = __builtin_fmaf(q[fi & 1][1][e], cl1, acc[fi][1][e]);
                 }
+                // fold here: left to itself the compiler sinks the folds of the
+                // unrolled steps towards the epilogue and keeps their products live
+                asm volatile("" : "+v"(acc[fi][0]), "+v"(acc[fi][1]));
                 cl = ci;
                 cl1 = ci1;
             }
@@ -322,7 +328,7 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
     }
 }
 
-template <bool GATEUP>
+template <bool GATEUP, int KBT>
 __global__ __launch_bounds__(kNT) void moe_gemm_wd_kernel(GemmArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -338,7 +344,7 @@ __global__ __launch_bounds__(kNT) void moe_gemm_wd_kernel(GemmArgs a)
     const int slab = 4 * qq + (i & 3);
     if (tile >= tiles) return;
     const int4 d = tab[1 + tile];   // {expert, first position, rows}
-    run_tile_wd<GATEUP>(a, d.x, d.y, min(d.z, kBM), slab, smem);
+    run_tile_wd<GATEUP, KBT>(a, d.x, d.y, min(d.z, kBM), slab, smem);
 }
 
 }  // namespace
@@ -361,11 +367,19 @@ int launch_gemm_wd(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
         return set_error(XS_ERR_UNSUPPORTED, "weight-direct GEMM shape K=%d N=%d", a.K, a.N);
     const size_t smem = (size_t)kNSA * kStage + 8 * (size_t)(a.K / 128) + 4 * kNW * kBM + 256;
     if (smem > 160 * 1024) return set_error(XS_ERR_UNSUPPORTED, "K=%d needs %zu bytes of LDS", a.K, smem);
-    auto fn = gateup ? moe_gemm_wd_kernel<true> : moe_gemm_wd_kernel<false>;
-    static bool attr_set[2] = {false, false};
-    if (!attr_set[gateup]) {
+    // unrolled kernels for 4, 8, 16 and 32 K steps, the loop for other K
+    const int KB = a.K / 128;
+    const int ki = KB == 4 ? 1 : KB == 8 ? 2 : KB == 16 ? 3 : KB == 32 ? 4 : 0;
+    void (*const fns[2][5])(GemmArgs) = {
+        {moe_gemm_wd_kernel<false, 0>, moe_gemm_wd_kernel<false, 4>, moe_gemm_wd_kernel<false, 8>,
+         moe_gemm_wd_kernel<false, 16>, moe_gemm_wd_kernel<false, 32>},
+        {moe_gemm_wd_kernel<true, 0>, moe_gemm_wd_kernel<true, 4>, moe_gemm_wd_kernel<true, 8>,
+         moe_gemm_wd_kernel<true, 16>, moe_gemm_wd_kernel<true, 32>}};
+    auto fn = fns[gateup][ki];
+    static bool attr_set[2][5] = {};
+    if (!attr_set[gateup][ki]) {
         XS_HIP(hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-        attr_set[gateup] = true;
+        attr_set[gateup][ki] = true;
     }
     const int64_t groups = (grid_y + 7) / 8 * (gx / 4);   // 8-tile x 4-slab groups
     fn<<<dim3((unsigned)((groups + 7) / 8 * 256)), dim3(kNT), smem, st>>>(a);
