@@ -172,6 +172,11 @@ def test_load_fp8_layer_stacks_gate_up_on_host(tmp_path):
     w = xstar_cpp.load_moe_layer([p], "m", xstar_cpp.Device.CPU)
     _check_stacked(w, t, 3)
     assert torch.equal(cpp_to_torch(w.router_bias, (3,)), t["m.gate.e_score_correction_bias"])
+    # packed copies are made on the GPU only
+    assert w.w13_frag is None
+    with pytest.raises(RuntimeError, match="unsupported device"):
+        xstar_cpp.pack_moe_layer_frag(w)
+    assert w.w13_frag is None
 
 
 def test_load_sharded_checkpoint_without_shared_or_bias(tmp_path):

@@ -69,3 +69,31 @@ def test_decode_weight_direct_v4_oracle(T, monkeypatch):
     err = max_abs_rel(out.float().cpu().numpy(), r["out_f32"])
     print(f"T={T} max-abs-rel={err:.3e}")
     assert err <= 2e-2, err
+
+
+@pytest.mark.parametrize("T,H,I,E,k", [
+    (8, 512, 512, 16, 4),      # 16-row tiles: the decode GEMMs
+    (300, 1024, 512, 8, 2),    # tall tiles: the prefill GEMMs
+])
+def test_cpp_block_ffn_packed_weights(T, H, I, E, k, tmp_path):
+    """xstar_cpp.moe_block_ffn after pack_moe_layer_frag(w) gives the bits it
+    gave before packing."""
+    import xstar_cpp
+    from safetensors.torch import save_file
+    from bridge import torch_to_cpp, cpp_to_torch
+    from moe_cases import make_case
+    from test_gpu_weights import _checkpoint
+    print(f"case T={T} H={H} I={I} E={E} k={k}", flush=True)
+    c = make_case(T, H, I, E, k, seed=9)
+    p = str(tmp_path / "l.safetensors")
+    save_file(_checkpoint(c, "blk.mlp"), p)
+    w = xstar_cpp.load_moe_layer([p], "blk.mlp")
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a)).view(torch.bfloat16)  # noqa: E731
+    ht = xstar_cpp.to_cuda(torch_to_cpp(bf(c["x"])))
+    ln = xstar_cpp.to_cuda(torch_to_cpp(bf(np.full(H, 0x3f80, np.uint16))))   # ones
+    before = cpp_to_torch(xstar_cpp.to_cpu(xstar_cpp.moe_block_ffn(ht, ln, 1e-6, w, top_k=k)), (T, H))
+    assert w.w13_frag is None
+    xstar_cpp.pack_moe_layer_frag(w)
+    assert w.w13_frag is not None and w.shared_w2_frag is not None
+    after = cpp_to_torch(xstar_cpp.to_cpu(xstar_cpp.moe_block_ffn(ht, ln, 1e-6, w, top_k=k)), (T, H))
+    assert torch.equal(before.view(torch.int16), after.view(torch.int16))

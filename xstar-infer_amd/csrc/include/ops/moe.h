@@ -53,7 +53,9 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
  * of xstar_cpp/src/ops/transformer_block.cpp:75,353 with the MoE in place of mlp().
  * The norm is fused into the activation quantization and the residual into the
  * combine (added in f32 before the output's one rounding).  `w` comes from
- * load_moe_layer (ops/moe_weights.h).  Same checks and messages as moe().
+ * load_moe_layer (ops/moe_weights.h); after pack_moe_layer_frag(w) its packed
+ * FP8 weights go to the GEMMs that load weights straight into registers (same
+ * bits).  Same checks and messages as moe().
  */
 Tensor moe_block_ffn(const Tensor &h, const Tensor &ln2_w, float eps, const MoeLayerWeights &w, std::int64_t top_k,
                      std::int64_t n_group = 1, std::int64_t topk_group = 1, bool renormalize = true,

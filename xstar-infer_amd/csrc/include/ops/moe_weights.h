@@ -32,6 +32,8 @@ struct MoeLayerWeights
     // set when present in the checkpoint
     std::optional<Tensor> router_bias;         // [E] Float32
     std::optional<Tensor> shared_w13, shared_w13_scale, shared_w2, shared_w2_scale;  // 2-D, same formats
+    // set by pack_moe_layer_frag: the FP8 weights again, in MFMA fragment order
+    std::optional<Tensor> w13_frag, w2_frag, shared_w13_frag, shared_w2_frag;
 };
 
 /**
@@ -43,3 +45,13 @@ struct MoeLayerWeights
  * and the parser's messages.
  */
 MoeLayerWeights load_moe_layer(const std::vector<std::string> &paths, const std::string &prefix, Device device);
+
+/**
+ * Adds fragment-packed copies of the layer's FP8 expert weights (CUDA, FP8
+ * layers only; xs_pack_weight_fp8_frag), which moe_block_ffn then hands to the
+ * GEMMs that load weights straight into registers.  The results are the same
+ * bits; the FP8 expert weights take twice the device memory.  No reference
+ * counterpart.  Throws "unsupported device" (host weights) and "unsupported
+ * dtype" (MXFP4 layers).
+ */
+void pack_moe_layer_frag(MoeLayerWeights &w);

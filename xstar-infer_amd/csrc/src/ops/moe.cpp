@@ -28,13 +28,20 @@ void sync() { xs_check(xs_stream_synchronize(nullptr)); }
 
 }  // namespace
 
-Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
-           const Tensor &w13, const Tensor &w13_scale, const Tensor &w2, const Tensor &w2_scale,
-           const Tensor *shared_w13, const Tensor *shared_w13_scale,
-           const Tensor *shared_w2, const Tensor *shared_w2_scale,
-           std::int64_t top_k, std::int64_t n_group, std::int64_t topk_group,
-           bool renormalize, float routed_scaling, bool router_exact,
-           const Tensor *norm_weight, float norm_eps, const Tensor *residual)
+namespace {
+// fragment-packed copies of the FP8 weights (pack_moe_layer_frag), or none
+struct Frag {
+    const Tensor *w13 = nullptr, *w2 = nullptr, *shared_w13 = nullptr, *shared_w2 = nullptr;
+};
+}  // namespace
+
+static Tensor moe_core(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
+                       const Tensor &w13, const Tensor &w13_scale, const Tensor &w2, const Tensor &w2_scale,
+                       const Tensor *shared_w13, const Tensor *shared_w13_scale,
+                       const Tensor *shared_w2, const Tensor *shared_w2_scale,
+                       std::int64_t top_k, std::int64_t n_group, std::int64_t topk_group,
+                       bool renormalize, float routed_scaling, bool router_exact,
+                       const Tensor *norm_weight, float norm_eps, const Tensor *residual, const Frag &frag)
 {
     // ---- dtype ----
     if (!is_act(x.dtype())) throw std::runtime_error("unsupported dtype");
@@ -126,6 +133,20 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
         t.shared_w2 = shared_w2->data();
         t.shared_w2_scale = static_cast<const float *>(shared_w2_scale->data());
     }
+    if (frag.w13 && frag.w2 && !fp4) {
+        for (const Tensor *f : {frag.w13, frag.w2, frag.shared_w13, frag.shared_w2})
+            if (f) same_device(x, *f);
+        if (frag.w13->nbytes() != w13.nbytes() || frag.w2->nbytes() != w2.nbytes() ||
+            (frag.shared_w13 && has_shared && frag.shared_w13->nbytes() != shared_w13->nbytes()) ||
+            (frag.shared_w2 && has_shared && frag.shared_w2->nbytes() != shared_w2->nbytes()))
+            throw std::runtime_error("shape mismatch");
+        t.w13_frag = frag.w13->data();
+        t.w2_frag = frag.w2->data();
+        if (has_shared && frag.shared_w13 && frag.shared_w2) {
+            t.shared_w13_frag = frag.shared_w13->data();
+            t.shared_w2_frag = frag.shared_w2->data();
+        }
+    }
     t.out = out.data();
     t.norm_weight = norm_weight ? norm_weight->data() : nullptr;
     t.residual = residual ? residual->data() : nullptr;
@@ -134,15 +155,29 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
     return out;
 }
 
+Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
+           const Tensor &w13, const Tensor &w13_scale, const Tensor &w2, const Tensor &w2_scale,
+           const Tensor *shared_w13, const Tensor *shared_w13_scale,
+           const Tensor *shared_w2, const Tensor *shared_w2_scale,
+           std::int64_t top_k, std::int64_t n_group, std::int64_t topk_group,
+           bool renormalize, float routed_scaling, bool router_exact,
+           const Tensor *norm_weight, float norm_eps, const Tensor *residual)
+{
+    return moe_core(x, router_w, router_bias, w13, w13_scale, w2, w2_scale, shared_w13, shared_w13_scale, shared_w2,
+                    shared_w2_scale, top_k, n_group, topk_group, renormalize, routed_scaling, router_exact, norm_weight,
+                    norm_eps, residual, Frag{});
+}
+
 Tensor moe_block_ffn(const Tensor &h, const Tensor &ln2_w, float eps, const MoeLayerWeights &w, std::int64_t top_k,
                      std::int64_t n_group, std::int64_t topk_group, bool renormalize, float routed_scaling,
                      bool router_exact)
 {
     if (!w.router_w || !w.w13 || !w.w13_scale || !w.w2 || !w.w2_scale) throw std::runtime_error("shape mismatch");
     auto p = [](const std::optional<Tensor> &t) { return t ? &*t : nullptr; };
-    return moe(h, *w.router_w, p(w.router_bias), *w.w13, *w.w13_scale, *w.w2, *w.w2_scale, p(w.shared_w13),
-               p(w.shared_w13_scale), p(w.shared_w2), p(w.shared_w2_scale), top_k, n_group, topk_group, renormalize,
-               routed_scaling, router_exact, &ln2_w, eps, &h);
+    const Frag f{p(w.w13_frag), p(w.w2_frag), p(w.shared_w13_frag), p(w.shared_w2_frag)};
+    return moe_core(h, *w.router_w, p(w.router_bias), *w.w13, *w.w13_scale, *w.w2, *w.w2_scale, p(w.shared_w13),
+                    p(w.shared_w13_scale), p(w.shared_w2), p(w.shared_w2_scale), top_k, n_group, topk_group,
+                    renormalize, routed_scaling, router_exact, &ln2_w, eps, &h, f);
 }
 
 Tensor moe_router_logits(const Tensor &x, const Tensor &router_w, bool exact)

@@ -185,3 +185,25 @@ MoeLayerWeights load_moe_layer(const std::vector<std::string> &paths, const std:
     }
     return L;
 }
+
+void pack_moe_layer_frag(MoeLayerWeights &w)
+{
+    if (!w.w13 || !w.w2) throw std::runtime_error("shape mismatch");
+    if (w.w13->device() != Device::CUDA) throw std::runtime_error("unsupported device");
+    if (w.w13->dtype() != DType::Float8E4M3 || w.w2->dtype() != DType::Float8E4M3)
+        throw std::runtime_error("unsupported dtype");
+    auto pack = [](const Tensor &t, std::int64_t batch, std::int64_t n, std::int64_t k) {
+        Tensor out(t.shape(), t.dtype(), Device::CUDA);
+        xs_check(xs_pack_weight_fp8_frag(static_cast<const std::uint8_t *>(t.data()), batch, n, k,
+                                         static_cast<std::uint8_t *>(out.data()), nullptr));
+        return out;
+    };
+    const std::int64_t E = w.E, H = w.H, I = w.I;
+    w.w13_frag = pack(*w.w13, E, 2 * I, H);
+    w.w2_frag = pack(*w.w2, E, H, I);
+    if (w.shared_w13 && w.shared_w2) {
+        w.shared_w13_frag = pack(*w.shared_w13, 1, 2 * I, H);
+        w.shared_w2_frag = pack(*w.shared_w2, 1, H, I);
+    }
+    xs_check(xs_stream_synchronize(nullptr));
+}
