@@ -156,6 +156,17 @@ int xs_quant_weight_mxfp4(const void *w, int dtype, int64_t batch, int64_t n, in
  * k % 128 == 0, 16-byte aligned, out not overlapping w. */
 int xs_pack_weight_fp8_frag(const uint8_t *w, int64_t batch, int64_t n, int64_t k, uint8_t *out, void *stream);
 
+/* MXFP4 weights w [batch, n, k/2] (e2m1 pairs) and their e8m0 scales
+ * s [batch, n, k/32] -> out_w (same bytes as w) and out_s (same bytes as s) in
+ * the operand layout of v_mfma_scale_f32_16x16x128_f8f6f4 with an FP4 A
+ * operand: per 16-row tile and 128-K slice, lane 16 g + r's 16 bytes (row r,
+ * K = [32 g, 32 g + 32)) and its scale byte (row r, 32-block g).
+ * n % 16 == 0, k % 128 == 0, w and out_w 16-byte aligned, outputs not
+ * overlapping inputs.  No reference counterpart: the storage format of the
+ * weight-direct MXFP4 GEMMs. */
+int xs_pack_weight_mxfp4_frag(const uint8_t *w, const uint8_t *s, int64_t batch, int64_t n, int64_t k,
+                              uint8_t *out_w, uint8_t *out_s, void *stream);
+
 size_t xs_gemm_fp8_blockscale_workspace_size(int64_t M, int64_t K);
 int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int64_t M,
                            int64_t N, int64_t K, void *C, void *workspace,
@@ -220,16 +231,21 @@ typedef struct {
     uint8_t *act_q;            /* [R, I] e4m3: SwiGLU output after its FP8 1x128 re-quant */
     float *act_s;              /* [R, I/128] f32 scales of act_q */
     float *y_rows;             /* [R, H] f32: each row's down projection, before the combine */
-    /* optional: the FP8 weights again, packed in MFMA fragment order by
+    /* optional: the weights again, packed in MFMA fragment order.  FP8 layers:
      * xs_pack_weight_fp8_frag (w13 as [E, 2I, H], w2 as [E, H, I], the shared
      * expert's as E = 1; same byte counts as the row-major tensors).  When the
      * layer gives all it has (FP8 routed experts, and the shared expert's if
-     * present), the prefill GEMMs load their weights straight into registers
-     * from these copies, with the same results bit for bit.  NULL = not given. */
+     * present), the prefill and decode GEMMs load their weights straight into
+     * registers from these copies, with the same results bit for bit.  MXFP4
+     * layers: w13_frag / w2_frag and w13_scale_frag / w2_scale_frag from
+     * xs_pack_weight_mxfp4_frag (routed experts; the shared expert stays FP8
+     * and row-major).  NULL = not given. */
     const void *w13_frag;
     const void *w2_frag;
     const void *shared_w13_frag;
     const void *shared_w2_frag;
+    const void *w13_scale_frag;
+    const void *w2_scale_frag;
 } xs_moe_tensors;
 
 /* Device workspace the forward needs for these params (bytes, 256-aligned). */

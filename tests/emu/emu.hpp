@@ -299,26 +299,62 @@ inline float e4m3_dec(uint8_t b)
     return s ? -v : v;
 }
 
-// v_mfma_f32_16x16x128_f8f6f4 (FP8 e4m3 both): lane 16g + r supplies row r,
-// K bytes [16g, 16g+16) and [64+16g, 64+16g+16); lane 16g + r receives
-// C[4g + v][r], C[m][n] = sum_k A[m][k] B[n][k]
+inline float e2m1_dec(int nib)
+{
+    static const float mag[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+    return (nib & 8) ? -mag[nib & 7] : mag[nib & 7];
+}
+inline int emu_ilog2(float a)
+{
+    int e;
+    std::frexp(a, &e);
+    return e - 1;
+}
+inline int mx_exponent(float amax, int emax_elem)
+{
+    if (amax == 0.0f) return -127;
+    int se = emu_ilog2(amax) - emax_elem;
+    return se < -127 ? -127 : (se > 127 ? 127 : se);
+}
+
+// v_mfma_scale_f32_16x16x128_f8f6f4.  An FP8 e4m3 operand: lane 16g + r
+// supplies row r, K bytes [16g, 16g+16) and [64+16g, 64+16g+16).  An FP4 e2m1
+// operand (cbsz / blgp 4): lane 16g + r supplies row r, K = [32g, 32g+32) in
+// its first 16 bytes (element 2i in the low nibble).  The e8m0 scale of (row
+// r, 32-block b) comes from lane 16b + r's scale operand (byte opsel); scale
+// 0 with every opsel 0 and all-zero scale registers is the unscaled form used
+// for FP8 x FP8 (the kernels pass zeros).  Lane 16g + r receives C[4g + v][r],
+// C[m][n] = sum_k A[m][k] B[n][k].
 inline bool g_math = false;
-inline v4f emu_mfma(v8i a, v8i b, v4f c, int, int, int, int, int, int)
+inline v4f emu_mfma(v8i a, v8i b, v4f c, int cbsz, int blgp, int opa, int sa, int opb, int sb)
 {
     if (!g_math) return c;
     const int w = wave_id(), l = lane_id();
     memcpy(tb->wx[w][l], &a, 32);
     memcpy(tb->wx[w][l] + 32, &b, 32);
+    tb->xch[w][l] = ((uint64_t)(uint8_t)(sa >> (8 * opa)) << 8) | (uint8_t)(sb >> (8 * opb));
     tb->wbar[w]->arrive_and_wait();
     const int r = l & 15, g = l >> 4;
     v4f out = c;
-    auto kbyte = [&](int lane_row, int k, int off) -> uint8_t {   // byte k of row lane_row
+    auto elem = [&](int lane_row, int k, int off, bool fp4) -> float {   // element k of row lane_row
+        if (fp4) {
+            const uint8_t by = tb->wx[w][16 * (k / 32) + lane_row][off + (k % 32) / 2];
+            return e2m1_dec((k & 1) ? by >> 4 : by & 15);
+        }
         const int chunk = k / 16, gg = chunk & 3, hi = chunk >> 2;
-        return tb->wx[w][16 * gg + lane_row][off + 16 * hi + (k & 15)];
+        return e4m3_dec(tb->wx[w][16 * gg + lane_row][off + 16 * hi + (k & 15)]);
+    };
+    const bool scaled = cbsz == 4 || blgp == 4;
+    auto scl = [&](int lane_row, int blk, bool isa) -> float {
+        if (!scaled) return 1.f;
+        const uint64_t x = tb->xch[w][16 * blk + lane_row];
+        return std::ldexp(1.f, (int)(isa ? (x >> 8) & 0xff : x & 0xff) - 127);
     };
     for (int v = 0; v < 4; ++v) {
         float s = 0;
-        for (int k = 0; k < 128; ++k) s += e4m3_dec(kbyte(4 * g + v, k, 0)) * e4m3_dec(kbyte(r, k, 32));
+        for (int k = 0; k < 128; ++k)
+            s += elem(4 * g + v, k, 0, cbsz == 4) * scl(4 * g + v, k / 32, true) * elem(r, k, 32, blgp == 4) *
+                 scl(r, k / 32, false);
         out[v] += s;
     }
     tb->wbar[w]->arrive_and_wait();

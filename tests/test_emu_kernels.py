@@ -1,5 +1,5 @@
-"""Host emulation of the weight-direct GEMMs: prefill (moe_gemm_wd.hip) and
-decode (moe_gemm_wdd.hip).
+"""Host emulation of the weight-direct GEMMs: FP8 prefill (moe_gemm_wd.hip),
+FP8 decode (moe_gemm_wdd.hip) and MXFP4 (moe_gemm_wd4.hip).
 
 Each kernel's own source runs on the CPU with one thread per lane: each LDS DMA
 poisons its destination and lands only when the kernel's vmcnt wait retires it
@@ -23,7 +23,7 @@ CLANG = "/opt/rocm/llvm/bin/clang++"
 
 
 def _build(d, gen, src, main):
-    inc = {"gen_wd.py": "wd_emu.inc", "gen_wdd.py": "wdd_emu.inc"}[gen]
+    inc = {"gen_wd.py": "wd_emu.inc", "gen_wdd.py": "wdd_emu.inc", "gen_wd4.py": "wd4_emu.inc"}[gen]
     subprocess.run([sys.executable, os.path.join(EMU, gen), os.path.join(HIP, src),
                     os.path.join(HIP, "moe_gemm.hpp"), str(d / inc)], check=True, cwd=EMU)
     exe = d / main.replace(".cpp", "")
@@ -49,6 +49,11 @@ def wd_emu(emu_dir):
 @pytest.fixture(scope="module")
 def wdd_emu(emu_dir):
     return _build(emu_dir, "gen_wdd.py", "moe_gemm_wdd.hip", "wdd_main.cpp")
+
+
+@pytest.fixture(scope="module")
+def wd4_emu(emu_dir):
+    return _build(emu_dir, "gen_wd4.py", "moe_gemm_wd4.hip", "wd4_main.cpp")
 
 
 def _check(out, returncode):
@@ -82,6 +87,19 @@ def test_weight_direct_decode_gemms_emulated(wdd_emu, args):
     shared = "0" if args[0] == "40" else "1"
     r = subprocess.run([wdd_emu, *args, "8", "0", "1", shared], capture_output=True, text=True, timeout=600)
     _check(r.stdout + r.stderr, r.returncode)
+
+
+def test_weight_direct_mxfp4_gemms_emulated(wd4_emu):
+    # 64 tokens, 4 experts top-2, Zipf(1.1), 64-row tiles, H=1024, I=512 (the
+    # loop form); MXFP4 weights, MXFP8 activations, e8m0 scales
+    r = subprocess.run([wd4_emu, "64", "4", "2", "1.1", "3", "1024", "512", "4", "0", "1", "64"],
+                       capture_output=True, text=True, timeout=600)
+    out = r.stdout + r.stderr
+    assert r.returncode == 0 and "errors 0" in out, out[-3000:]
+    # every act element within the bound its block's e8m0 scale sets: the
+    # clamp at 448 x 2^se, else half an e4m3 step
+    assert int(re.search(r"outside the MXFP8 bound (\d+)", out).group(1)) == 0, out[-2000:]
+    assert float(re.search(r"down y: .* rel (\S+)", out).group(1)) < 1e-5, out[-2000:]
 
 
 def test_emulated_check_catches_misdirected_dma(wd_emu):

@@ -252,6 +252,11 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     const int bm = direct ? wd_tile_rows() : wide ? wide_tile_rows() : pick_bm((double)S / (double)E);
     // weight-direct decode GEMMs for 16-row tiles, likewise from the packed
     // weights (XS_DECODE_DIRECT=0 keeps the LDS-ring and stream-K kernels)
+    // weight-direct MXFP4 GEMMs for the routed experts on 64- and 128-row
+    // tiles, from packed weights and scales (XS_FP4_DIRECT=0: the tiled and
+    // stream-K kernels)
+    const bool direct4 = fp4 && (bm == 64 || bm == 128) && t->w13_frag && t->w2_frag && t->w13_scale_frag &&
+                         t->w2_scale_frag && wd4_supported(H, I) && getenv_flag("XS_FP4_DIRECT", true);
     const bool ddirect = !wide && !fp4 && bm == 16 && t->w13_frag && t->w2_frag &&
                          (!p->has_shared || (t->shared_w13_frag && t->shared_w2_frag)) && wdd_supported(H, I) &&
                          getenv_flag("XS_DECODE_DIRECT", true);
@@ -276,7 +281,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     // FP8: all tiles in one launch; MXFP4: the routed tiles (the FP8 shared
     // expert runs the tiled kernel)
     const int stream_tiles = fp4 ? routed_tiles : routed_tiles + shared_tiles;
-    const bool stream = !ddirect && stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
+    const bool stream = !ddirect && !direct4 && stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
                         (sm == 2 || (sm == 1 && stream_items(true, (int)I, stream_tiles) >= 2 * (int64_t)stream_blocks()));
     if (stream) {
         po.zero = WS(int32_t, cnt1);
@@ -374,8 +379,10 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         r1.Cs = WS(uint8_t, actms);
         r1.e_lo = 0;
         r1.e_hi = (int)E;
-        rc = stream ? launch_gemm_stream(r1, true, true, stream_tiles, rows_all, st)
-                    : launch_gemm(r1, true, true, routed_tiles, st);
+        r1.Bsp = (const uint8_t *)t->w13_scale_frag;
+        rc = stream    ? launch_gemm_stream(r1, true, true, stream_tiles, rows_all, st)
+             : direct4 ? launch_gemm_wd4(r1, true, routed_tiles, st)
+                       : launch_gemm(r1, true, true, routed_tiles, st);
         if (rc) return rc;
         if (shared_rows) {
             GemmArgs s1 = g1;
@@ -392,8 +399,10 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         r2.As = WS(uint8_t, actms);
         r2.e_lo = 0;
         r2.e_hi = (int)E;
-        rc = stream ? launch_gemm_stream(r2, false, true, stream_tiles, rows_all, st)
-                    : launch_gemm(r2, false, true, routed_tiles, st);
+        r2.Bsp = (const uint8_t *)t->w2_scale_frag;
+        rc = stream    ? launch_gemm_stream(r2, false, true, stream_tiles, rows_all, st)
+             : direct4 ? launch_gemm_wd4(r2, false, routed_tiles, st)
+                       : launch_gemm(r2, false, true, routed_tiles, st);
         if (rc) return rc;
         if (shared_rows) {
             GemmArgs s2 = g2;

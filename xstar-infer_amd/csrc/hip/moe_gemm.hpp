@@ -14,6 +14,7 @@ struct GemmArgs {
     const uint8_t *Bsh;        // shared expert weights (FP8), used for e == E
     const uint8_t *Bp;         // routed FP8 weights packed in fragment order (weight-direct kernels) or NULL
     const uint8_t *Bshp;       // shared expert weights packed in fragment order
+    const uint8_t *Bsp;        // MXFP4: routed weight scales packed in fragment order (weight-direct kernels)
     const float *Bssh;         // shared expert scales
     const int32_t *offsets;    // [E+2] row offsets per expert (E = shared segment)
     const int32_t *tile_off;   // [E+2] tile offsets for tile height bm
@@ -69,6 +70,11 @@ bool wd_supported(int64_t H, int64_t I);   // the layer shapes the weight-direct
 // gate_up, or down with f32 rows (a.Cf).  K of 512, 1024, 2048 or 4096.
 int launch_gemm_wdd(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st);
 bool wdd_supported(int64_t H, int64_t I);
+// Weight-direct MXFP4 GEMMs (moe_gemm_wd4.hip): the routed tiles of a 64- or
+// 128-row tile table, the same results as launch_gemm's MXFP4 tiles, from
+// packed weights and scales (a.Bp, a.Bsp); gate_up, or down with f32 rows.
+int launch_gemm_wd4(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st);
+bool wd4_supported(int64_t H, int64_t I);
 // Persistent stream-K GEMMs (moe_gemm_stream.hip): FP8 with a.bm 16 or 32,
 // MXFP4 with a.bm 16, 32 or 64.  tiles_max bounds the tile count of the
 // launch's range of the tile table, rows_max the positions; a.cnt holds one

@@ -33,7 +33,8 @@ class MoeTensors(C.Structure):
         "x", "router_w", "router_bias", "w13", "w13_scale", "w2", "w2_scale",
         "shared_w13", "shared_w13_scale", "shared_w2", "shared_w2_scale", "out",
         "logits", "topk_idx", "topk_w", "counts", "offsets", "perm", "inv", "norm_weight", "residual",
-        "act_q", "act_s", "y_rows", "w13_frag", "w2_frag", "shared_w13_frag", "shared_w2_frag")]
+        "act_q", "act_s", "y_rows", "w13_frag", "w2_frag", "shared_w13_frag", "shared_w2_frag",
+        "w13_scale_frag", "w2_scale_frag")]
 
 
 EXPORTS = {
@@ -56,6 +57,7 @@ EXPORTS = {
     "xs_quant_weight_fp8_block": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P]),
     "xs_quant_weight_mxfp4": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P]),
     "xs_pack_weight_fp8_frag": (C.c_int, [P, I64, I64, I64, P, P]),
+    "xs_pack_weight_mxfp4_frag": (C.c_int, [P, P, I64, I64, I64, P, P, P]),
     "xs_gemm_fp8_blockscale_workspace_size": (C.c_size_t, [I64, I64]),
     "xs_gemm_fp8_blockscale": (C.c_int, [P, P, P, I64, I64, I64, P, P, C.c_size_t, P]),
     "xs_moe_workspace_size": (C.c_size_t, [P]),
@@ -251,10 +253,23 @@ def pack_weight_fp8_frag(w):
     return out
 
 
+def pack_weight_mxfp4_frag(w, s):
+    """MXFP4 [..., n, k/2] weights and [..., n, k/32] e8m0 scales -> tensors of
+    the same shapes and bytes in MFMA fragment order (xs_pack_weight_mxfp4_frag)."""
+    import torch
+    w, s = _u8(w).contiguous(), _u8(s).contiguous()
+    n, k = w.shape[-2], w.shape[-1] * 2
+    batch = w.numel() // (n * k // 2)
+    ow, os_ = torch.empty_like(w), torch.empty_like(s)
+    check(lib().xs_pack_weight_mxfp4_frag(_ptr(w), _ptr(s), batch, n, k, _ptr(ow), _ptr(os_), _stream()))
+    return ow, os_
+
+
 class MoeLayer:
     """Holds weights (device tensors) and calls xs_moe_forward.  frag=True also
-    keeps fragment-packed copies of the FP8 weights, which the prefill and decode GEMMs
-    load straight into registers (same results)."""
+    keeps fragment-packed copies of the weights (FP8 layers: routed and shared;
+    MXFP4 layers: routed weights and scales), which the GEMMs load straight into
+    registers (same results)."""
 
     def __init__(self, router_w, w13, w13_scale, w2, w2_scale, top_k, router_bias=None,
                  shared=None, routed_format=XS_FP8_E4M3, n_group=1, topk_group=1,
@@ -270,12 +285,17 @@ class MoeLayer:
         self.E, self.H = router_w.shape
         self.I = w2.shape[-1] * (2 if routed_format == XS_FP4_E2M1X2 else 1)
         self._ws = None
-        self.frag = (None, None, None, None)
+        # w13_frag, w2_frag, shared_w13_frag, shared_w2_frag, w13_scale_frag, w2_scale_frag
+        self.frag = (None,) * 6
         if frag and routed_format == XS_FP8_E4M3:
-            f = [pack_weight_fp8_frag(self.w13), pack_weight_fp8_frag(self.w2), None, None]
+            f = [pack_weight_fp8_frag(self.w13), pack_weight_fp8_frag(self.w2), None, None, None, None]
             if self.shared is not None:
                 f[2], f[3] = pack_weight_fp8_frag(self.shared[0]), pack_weight_fp8_frag(self.shared[2])
             self.frag = tuple(f)
+        elif frag:
+            w13p, s13p = pack_weight_mxfp4_frag(self.w13, self.w13_scale)
+            w2p, s2p = pack_weight_mxfp4_frag(self.w2, self.w2_scale)
+            self.frag = (w13p, w2p, None, None, s13p, s2p)
 
     def params(self, T, x_dtype):
         return MoeParams(T, self.H, self.I, self.E, self.top_k, self.n_group, self.topk_group,
