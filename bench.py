@@ -330,7 +330,8 @@ def fp4_layer(a, X, torch):
     """MXFP4 routed experts (FP8 shared), 2048 tokens."""
     from moe_synth import synth_layer, layer_from, expert_bytes, layer_flops
     g4 = synth_layer(2048, H, I, E, K_TOP, seed=3, fp4=True)
-    L4 = layer_from(g4)
+    # XS_BENCH_FRAG=1: packed MXFP4 weights and scales, weight-direct GEMMs
+    L4 = layer_from(g4, frag=os.environ.get("XS_BENCH_FRAG", "0") == "1")
     ms4, st4 = time_forward(L4, g4["x"], a.steps, a.warmup, profile=True)
     ne4 = routed_expert_count(L4, g4["x"])
     by4 = ne4 * expert_bytes(H, I, True) + expert_bytes(H, I, False) + E * H * 2
