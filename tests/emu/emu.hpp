@@ -126,6 +126,7 @@ inline T emu_rfl(T v)
 }
 #define __builtin_amdgcn_readfirstlane(x) emu_rfl(x)
 #define __builtin_amdgcn_sched_barrier(x) ((void)0)
+#define __builtin_amdgcn_sched_group_barrier(a, b, c) ((void)0)
 
 inline float __shfl_xor(float v, int m, int)
 {

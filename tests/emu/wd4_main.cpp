@@ -3,12 +3,15 @@
 // BM-row tiles run from the kernel's own source, then both are checked
 // against a float64 recomputation from the same MXFP4 / MXFP8 inputs.
 // usage: wd4_emu T E k zipf seed H I conc mode(0 late,1 early) math(0/1) BM(64|128)
+// EMU_CMP_TILED=1 also runs the tiled MXFP4 kernel of moe_gemm.hip on the same
+// inputs and compares the bytes of the routed rows
 #include "emu.hpp"
 #include <algorithm>
 #include <numeric>
 #include <random>
 
 #include "wd4_emu.inc"
+#include "tiled_emu.inc"
 
 using namespace xs;
 using I4 = int4;
@@ -137,6 +140,33 @@ int main(int argc, char **argv)
         XS_EMU(64, 16) XS_EMU(64, 32) XS_EMU(64, 0) XS_EMU(128, 0) { fprintf(stderr, "unsupported\n"); return 2; }
 #undef XS_EMU
         printf("pass %d done, errors %ld\n", pass, g_errors.load());
+    }
+
+    if (getenv("EMU_CMP_TILED")) {
+        std::vector<uint8_t> q0(actq, actq + (size_t)S * I), s0(acts, acts + (size_t)S * (I / 32));
+        std::vector<float> y0(y, y + (size_t)S * H);
+        memset(actq, 0, (size_t)R * I);
+        memset(acts, 0, (size_t)R * (I / 32));
+        memset(y, 0, 4 * (size_t)R * H);
+        GemmArgs t1 = g1, t2 = g2;
+        t1.B = w13; t1.Bs = s13; t2.B = w2; t2.Bs = s2;
+        t1.Bp = t2.Bp = t1.Bsp = t2.Bsp = nullptr;
+        t1.e_lo = t2.e_lo = 0;
+        t1.e_hi = t2.e_hi = E;   // routed tiles only
+        using namespace xs::tiled;
+#define XS_EMU_T(BMV)                                                                                         \
+        if (BM == BMV) {                                                                                      \
+            emu_launch([&] { moe_gemm_kernel<BMV, true, true>(t1); }, I / 128, tt, Cfg<BMV, true>::NT,         \
+                       gemm_smem_bytes<BMV, true, true>(H), conc);                                            \
+            emu_launch([&] { moe_gemm_kernel<BMV, false, true>(t2); }, (H + 255) / 256, tt, Cfg<BMV, true>::NT, \
+                       gemm_smem_bytes<BMV, false, true>(I), conc);                                           \
+        }
+        XS_EMU_T(64) XS_EMU_T(128)
+#undef XS_EMU_T
+        const bool same = !memcmp(q0.data(), actq, q0.size()) && !memcmp(s0.data(), acts, s0.size()) &&
+                          !memcmp(y0.data(), y, 4 * y0.size());
+        printf("tiled kernel: errors %ld, identical bytes: %s\n", g_errors.load(), same ? "yes" : "NO");
+        if (!same) g_errors++;
     }
 
     if (g_math) {

@@ -3,7 +3,8 @@
 // run from the kernel's own source, then both are checked against a float64
 // recomputation from the same FP8 inputs.
 // usage: wdd_emu T E k zipf seed H I conc mode(0 late,1 early) math(0/1) shared(0/1)
-// (H and I in {512, 1024, 2048, 4096})
+// (H and I in {512, 1024, 2048, 4096}); EMU_CMP_TILED=1 also runs the tiled
+// kernel of moe_gemm.hip on the same inputs and compares the bytes
 // EMU_HAZARD=1|2|3, EMU_HAZARD_P, EMU_HAZARD_SEED: the wait-state hazard model of emu.hpp
 #include "emu.hpp"
 #include <algorithm>
@@ -11,6 +12,7 @@
 #include <random>
 
 #include "wdd_emu.inc"
+#include "tiled_emu.inc"
 
 using namespace xs;
 using I4 = int4;
@@ -149,6 +151,26 @@ int main(int argc, char **argv)
     printf("gate_up done, errors %ld\n", g_errors.load());
     run(g2, false);
     printf("down done, errors %ld\n", g_errors.load());
+
+    if (getenv("EMU_CMP_TILED")) {
+        // the reference kernel on the same inputs (row-major weights): every
+        // output byte must match
+        std::vector<uint8_t> q0(actq, actq + (size_t)R * I);
+        std::vector<float> s0(acts, acts + (size_t)R * (I / 128)), y0(y, y + (size_t)R * H);
+        memset(actq, 0, (size_t)R * I);
+        memset(acts, 0, 4 * (size_t)R * (I / 128));
+        memset(y, 0, 4 * (size_t)R * H);
+        GemmArgs t1 = g1, t2 = g2;
+        t1.Bp = t1.Bshp = t2.Bp = t2.Bshp = nullptr;
+        using namespace xs::tiled;
+        const size_t sm1 = gemm_smem_bytes<16, true, false>(H), sm2 = gemm_smem_bytes<16, false, false>(I);
+        emu_launch([&] { moe_gemm_kernel<16, true, false>(t1); }, I / 128, tt + nsh, Cfg<16, false>::NT, sm1, conc);
+        emu_launch([&] { moe_gemm_kernel<16, false, false>(t2); }, (H + 255) / 256, tt + nsh, Cfg<16, false>::NT, sm2, conc);
+        const bool same = !memcmp(q0.data(), actq, q0.size()) && !memcmp(s0.data(), acts, 4 * s0.size()) &&
+                          !memcmp(y0.data(), y, 4 * y0.size());
+        printf("tiled kernel: errors %ld, identical bytes: %s\n", g_errors.load(), same ? "yes" : "NO");
+        if (!same) g_errors++;
+    }
 
     if (g_math) {
         double maxerr = 0, maxref = 0;

@@ -26,6 +26,9 @@ def _build(d, gen, src, main):
     inc = {"gen_wd.py": "wd_emu.inc", "gen_wdd.py": "wdd_emu.inc", "gen_wd4.py": "wd4_emu.inc"}[gen]
     subprocess.run([sys.executable, os.path.join(EMU, gen), os.path.join(HIP, src),
                     os.path.join(HIP, "moe_gemm.hpp"), str(d / inc)], check=True, cwd=EMU)
+    # the tiled kernel of moe_gemm.hip, the reference of the bit-identity checks
+    subprocess.run([sys.executable, os.path.join(EMU, "gen_tiled.py"), os.path.join(HIP, "moe_gemm.hip"),
+                    str(d / "tiled_emu.inc")], check=True, cwd=EMU)
     exe = d / main.replace(".cpp", "")
     subprocess.run([CLANG, "-O2", "-std=c++20", "-pthread", "-Wno-psabi", "-I", EMU, "-I", str(d),
                     os.path.join(EMU, main), "-o", str(exe)], check=True)
@@ -85,17 +88,24 @@ def test_weight_direct_gemms_emulated(wd_emu):
 ])
 def test_weight_direct_decode_gemms_emulated(wdd_emu, args):
     shared = "0" if args[0] == "40" else "1"
-    r = subprocess.run([wdd_emu, *args, "8", "0", "1", shared], capture_output=True, text=True, timeout=600)
-    _check(r.stdout + r.stderr, r.returncode)
+    r = subprocess.run([wdd_emu, *args, "8", "0", "1", shared], capture_output=True, text=True, timeout=900,
+                       env=dict(os.environ, EMU_CMP_TILED="1"))
+    out = r.stdout + r.stderr
+    _check(out, r.returncode)
+    # the 16-row tiled kernel on the same inputs writes the same bytes: the
+    # MFMAs get the same operands and the folds run in the same order
+    assert "identical bytes: yes" in out, out[-2000:]
 
 
 def test_weight_direct_mxfp4_gemms_emulated(wd4_emu):
     # 64 tokens, 4 experts top-2, Zipf(1.1), 64-row tiles, H=1024, I=512 (the
     # loop form); MXFP4 weights, MXFP8 activations, e8m0 scales
     r = subprocess.run([wd4_emu, "64", "4", "2", "1.1", "3", "1024", "512", "4", "0", "1", "64"],
-                       capture_output=True, text=True, timeout=600)
+                       capture_output=True, text=True, timeout=900, env=dict(os.environ, EMU_CMP_TILED="1"))
     out = r.stdout + r.stderr
     assert r.returncode == 0 and "errors 0" in out, out[-3000:]
+    # the 64-row MXFP4 tiled kernel on the same inputs writes the same bytes
+    assert "identical bytes: yes" in out, out[-2000:]
     # every act element within the bound its block's e8m0 scale sets: the
     # clamp at 448 x 2^se, else half an e4m3 step
     assert int(re.search(r"outside the MXFP8 bound (\d+)", out).group(1)) == 0, out[-2000:]
