@@ -4,12 +4,15 @@
 // recomputation from the same FP8 inputs.
 // usage: wd_emu T E k zipf seed H I conc mode(0 late,1 early) math(0/1) shared(0/1)
 // EMU_HAZARD=1|2|3, EMU_HAZARD_P, EMU_HAZARD_SEED: the wait-state hazard model of emu.hpp
+// EMU_CMP_WIDE=1 also runs the tall-tile LDS-ring kernel of moe_gemm_wide.hip
+// (192-row tiles) on the same inputs and compares the bytes
 #include "emu.hpp"
 #include <algorithm>
 #include <numeric>
 #include <random>
 
 #include "wd_emu.inc"
+#include "wide_emu.inc"
 
 using namespace xs;
 using I4 = int4;
@@ -145,6 +148,47 @@ int main(int argc, char **argv)
         XS_EMU_KB(4) XS_EMU_KB(8) XS_EMU_KB(16) XS_EMU_KB(32) XS_EMU_KB(0) {}
 #undef XS_EMU_KB
         printf("pass %d done, errors %ld\n", pass, g_errors.load());
+    }
+
+    if (getenv("EMU_CMP_WIDE")) {
+        // the LDS-ring kernel on its own 192-row tile table: every output byte
+        // must match (the same per-row arithmetic in the same order)
+        const int WB = 192;
+        const int wsh = (SH + WB - 1) / WB;
+        int wt = 0;
+        for (int e = 0; e < E; ++e) wt += (cnt[e] + WB - 1) / WB;
+        I4 *wtab = (I4 *)emu_alloc(16 * (size_t)(1 + wt + wsh), "wide_tile_tab");
+        wtab[0] = {wt + wsh, wsh, 0, 0};
+        for (int t = 0; t < wsh; ++t) wtab[1 + t] = {E, S + t * WB, std::min(WB, SH - t * WB), t | (std::min(wsh, 0x7fff) << 16)};
+        for (int e = 0, toff = 0; e < E; ++e) {
+            const int nt = (cnt[e] + WB - 1) / WB;
+            for (int t = 0; t < nt; ++t)
+                wtab[1 + wsh + toff + t] = {e, offsets[e] + t * WB, std::min(WB, cnt[e] - t * WB), t | (std::min(nt, 0x7fff) << 16)};
+            toff += nt;
+        }
+        std::vector<uint8_t> q0(actq, actq + (size_t)R * I);
+        std::vector<float> s0(acts, acts + (size_t)R * (I / 128)), y0(y, y + (size_t)R * H);
+        memset(actq, 0, (size_t)R * I);
+        memset(acts, 0, 4 * (size_t)R * (I / 128));
+        memset(y, 0, 4 * (size_t)R * H);
+        GemmArgs w1 = g1, w2a = g2;
+        w1.Bp = w1.Bshp = w2a.Bp = w2a.Bshp = nullptr;
+        w1.tile_tab = w2a.tile_tab = (const int32_t *)wtab;
+        w1.bm = w2a.bm = WB;
+        w1.xcd_order = w2a.xcd_order = 1;
+        w1.short_deep = w2a.short_deep = 1;
+        for (int pass = 0; pass < 2; ++pass) {
+            const GemmArgs &a = pass ? w2a : w1;
+            const size_t smem = (size_t)xs::wide::kRing + xs::wide::kTrash + 8 * (size_t)(a.K / 128) + 4 * 4 * WB;
+            const int gx = pass ? a.N / 256 : a.N / 128;
+            const unsigned nb = (unsigned)(((wt + wsh + 7) / 8 * (gx / 4) + 7) / 8 * 256);
+            if (pass == 0) emu_launch([&] { xs::wide::moe_gemm_wide_kernel<192, true, 8>(a); }, nb, 1, 512, smem, conc);
+            else emu_launch([&] { xs::wide::moe_gemm_wide_kernel<192, false, 8>(a); }, nb, 1, 512, smem, conc);
+        }
+        const bool same = !memcmp(q0.data(), actq, q0.size()) && !memcmp(s0.data(), acts, 4 * s0.size()) &&
+                          !memcmp(y0.data(), y, 4 * y0.size());
+        printf("tall-tile kernel: errors %ld, identical bytes: %s\n", g_errors.load(), same ? "yes" : "NO");
+        if (!same) g_errors++;
     }
 
     if (g_math) {

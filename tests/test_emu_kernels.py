@@ -26,12 +26,15 @@ def _build(d, gen, src, main):
     inc = {"gen_wd.py": "wd_emu.inc", "gen_wdd.py": "wdd_emu.inc", "gen_wd4.py": "wd4_emu.inc"}[gen]
     subprocess.run([sys.executable, os.path.join(EMU, gen), os.path.join(HIP, src),
                     os.path.join(HIP, "moe_gemm.hpp"), str(d / inc)], check=True, cwd=EMU)
-    # the tiled kernel of moe_gemm.hip, the reference of the bit-identity checks
+    # the references of the bit-identity checks: the tiled kernel of
+    # moe_gemm.hip and the tall-tile LDS-ring kernel of moe_gemm_wide.hip
     subprocess.run([sys.executable, os.path.join(EMU, "gen_tiled.py"), os.path.join(HIP, "moe_gemm.hip"),
                     str(d / "tiled_emu.inc")], check=True, cwd=EMU)
+    subprocess.run([sys.executable, os.path.join(EMU, "gen_wide.py"), os.path.join(HIP, "moe_gemm_wide.hip"),
+                    str(d / "wide_emu.inc")], check=True, cwd=EMU)
     exe = d / main.replace(".cpp", "")
     subprocess.run([CLANG, "-O2", "-std=c++20", "-pthread", "-Wno-psabi", "-I", EMU, "-I", str(d),
-                    os.path.join(EMU, main), "-o", str(exe)], check=True)
+                    "-I", os.path.join(ROOT, "include"), os.path.join(EMU, main), "-o", str(exe)], check=True)
     return str(exe)
 
 
@@ -75,8 +78,12 @@ def test_weight_direct_gemms_emulated(wd_emu):
     # smallest shape the kernel takes: K a multiple of 512, grid x of 4): full,
     # partial and short tiles; DMAs land at their waits, not at issue
     r = subprocess.run([wd_emu, "64", "4", "2", "1.1", "3", "1024", "512", "4", "0", "1", "1"],
-                       capture_output=True, text=True, timeout=600)
-    _check(r.stdout + r.stderr, r.returncode)
+                       capture_output=True, text=True, timeout=900, env=dict(os.environ, EMU_CMP_WIDE="1"))
+    out = r.stdout + r.stderr
+    _check(out, r.returncode)
+    # the tall-tile LDS-ring kernel (192-row tiles) on the same inputs writes
+    # the same bytes: the same per-row arithmetic in the same order
+    assert "identical bytes: yes" in out, out[-2000:]
 
 
 @pytest.mark.parametrize("args", [
