@@ -150,6 +150,45 @@ int main(int argc, char **argv)
         printf("pass %d done, errors %ld\n", pass, g_errors.load());
     }
 
+    if (getenv("EMU_CMP_SHARED") && SH > 0) {
+        // the shared segment alone, in 128-row tiles the kernel computes
+        // itself (no tile table): the same bytes in the shared rows
+        std::vector<uint8_t> q0(actq + (size_t)S * I, actq + (size_t)R * I);
+        std::vector<float> s0(acts + (size_t)S * (I / 128), acts + (size_t)R * (I / 128));
+        std::vector<float> y0(y + (size_t)S * H, y + (size_t)R * H);
+        std::vector<uint8_t> qa(actq, actq + (size_t)R * I);   // restored afterwards
+        std::vector<float> sa(acts, acts + (size_t)R * (I / 128)), ya(y, y + (size_t)R * H);
+        memset(actq, 0, (size_t)R * I);
+        memset(acts, 0, 4 * (size_t)R * (I / 128));
+        memset(y, 0, 4 * (size_t)R * H);
+        GemmArgs h1 = g1, h2 = g2;
+        h1.tile_tab = h2.tile_tab = nullptr;
+        h1.Bp = h2.Bp = nullptr;
+        h1.sh_rows = h2.sh_rows = SH;
+        h1.shared_base = h2.shared_base = S;
+        h1.e_lo = h2.e_lo = E;
+        h1.e_hi = h2.e_hi = E + 1;
+        const int st = (SH + kBM - 1) / kBM;
+        for (int pass = 0; pass < 2; ++pass) {
+            const GemmArgs &a = pass ? h2 : h1;
+            const int KB = a.K / 128;
+            const size_t smem = (size_t)kNSA * kStage + 8 * (size_t)KB + 4 * kNW * kBM + 256;
+            const int gx = pass ? a.N / 256 : a.N / 128;
+            const unsigned nb = (unsigned)(((st + 7) / 8 * (gx / 4) + 7) / 8 * 256);
+            if (pass == 0) emu_launch([&] { moe_gemm_wd_kernel<true, 0>(a); }, nb, 1, kNT, smem, conc);
+            else emu_launch([&] { moe_gemm_wd_kernel<false, 0>(a); }, nb, 1, kNT, smem, conc);
+        }
+        bool same = !memcmp(q0.data(), actq + (size_t)S * I, q0.size()) &&
+                    !memcmp(s0.data(), acts + (size_t)S * (I / 128), 4 * s0.size()) &&
+                    !memcmp(y0.data(), y + (size_t)S * H, 4 * y0.size());
+        for (size_t i = 0; same && i < (size_t)S * I; ++i) same = actq[i] == 0;   // routed rows untouched
+        printf("shared segment alone: errors %ld, identical bytes: %s\n", g_errors.load(), same ? "yes" : "NO");
+        if (!same) g_errors++;
+        memcpy(actq, qa.data(), qa.size());
+        memcpy(acts, sa.data(), 4 * sa.size());
+        memcpy(y, ya.data(), 4 * ya.size());
+    }
+
     if (getenv("EMU_CMP_WIDE")) {
         // the LDS-ring kernel on its own 192-row tile table: every output byte
         // must match (the same per-row arithmetic in the same order)

@@ -78,12 +78,15 @@ def test_weight_direct_gemms_emulated(wd_emu):
     # smallest shape the kernel takes: K a multiple of 512, grid x of 4): full,
     # partial and short tiles; DMAs land at their waits, not at issue
     r = subprocess.run([wd_emu, "64", "4", "2", "1.1", "3", "1024", "512", "4", "0", "1", "1"],
-                       capture_output=True, text=True, timeout=900, env=dict(os.environ, EMU_CMP_WIDE="1"))
+                       capture_output=True, text=True, timeout=900,
+                       env=dict(os.environ, EMU_CMP_WIDE="1", EMU_CMP_SHARED="1"))
     out = r.stdout + r.stderr
     _check(out, r.returncode)
     # the tall-tile LDS-ring kernel (192-row tiles) on the same inputs writes
-    # the same bytes: the same per-row arithmetic in the same order
-    assert "identical bytes: yes" in out, out[-2000:]
+    # the same bytes: the same per-row arithmetic in the same order; so does
+    # the shared segment run alone, in 128-row tiles the kernel computes itself
+    assert "tall-tile kernel: errors 0, identical bytes: yes" in out, out[-2000:]
+    assert "shared segment alone: errors 0, identical bytes: yes" in out, out[-2000:]
 
 
 @pytest.mark.parametrize("args", [

@@ -257,6 +257,9 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     // stream-K kernels)
     const bool direct4 = fp4 && (bm == 64 || bm == 128) && t->w13_frag && t->w2_frag && t->w13_scale_frag &&
                          t->w2_scale_frag && wd4_supported(H, I) && getenv_flag("XS_FP4_DIRECT", true);
+    // ... and their FP8 shared expert on the weight-direct prefill kernel, in
+    // 128-row tiles of its own
+    const bool sdirect = direct4 && shared_rows && t->shared_w13_frag && t->shared_w2_frag && wd_supported(H, I);
     const bool ddirect = !wide && !fp4 && bm == 16 && t->w13_frag && t->w2_frag &&
                          (!p->has_shared || (t->shared_w13_frag && t->shared_w2_frag)) && wdd_supported(H, I) &&
                          getenv_flag("XS_DECODE_DIRECT", true);
@@ -391,7 +394,11 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
             s1.Cs = WS(float, acts);
             s1.e_lo = (int)E;
             s1.e_hi = (int)E + 1;
-            rc = launch_gemm(s1, true, false, shared_tiles, st);
+            s1.Bp = nullptr;
+            s1.sh_rows = sdirect ? shared_rows : 0;
+            s1.shared_base = S;
+            rc = sdirect ? launch_gemm_wd(s1, true, (int)((shared_rows + wd_tile_rows() - 1) / wd_tile_rows()), st)
+                         : launch_gemm(s1, true, false, shared_tiles, st);
             if (rc) return rc;
         }
         if ((rc = prof_mark(5, st))) return rc;
@@ -409,7 +416,11 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
             s2.As = WS(float, acts);
             s2.e_lo = (int)E;
             s2.e_hi = (int)E + 1;
-            rc = launch_gemm(s2, false, false, shared_tiles, st);
+            s2.Bp = nullptr;
+            s2.sh_rows = sdirect ? shared_rows : 0;
+            s2.shared_base = S;
+            rc = sdirect ? launch_gemm_wd(s2, false, (int)((shared_rows + wd_tile_rows() - 1) / wd_tile_rows()), st)
+                         : launch_gemm(s2, false, false, shared_tiles, st);
             if (rc) return rc;
         }
     }

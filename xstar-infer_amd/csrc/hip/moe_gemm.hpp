@@ -43,6 +43,10 @@ struct GemmArgs {
     int topk;
     int has_shared;            // shared row of token t at position shared_base + t
     int64_t shared_base;
+    // weight-direct prefill GEMM: > 0 = the launch covers the shared segment alone
+    // (positions shared_base .., this many rows) in 128-row tiles of its own,
+    // without a tile table
+    int64_t sh_rows;
     int32_t *ccnt;             // [T, H/256] counters, zero on entry
     void *out;                 // [T, H] of out_dtype
     const void *residual;      // [T, H] of out_dtype or NULL (may alias out)

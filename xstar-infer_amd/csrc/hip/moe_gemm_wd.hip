@@ -333,7 +333,7 @@ __global__ __launch_bounds__(kNT) void moe_gemm_wd_kernel(GemmArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int4 *tab = reinterpret_cast<const int4 *>(a.tile_tab);   // shared + routed tiles
-    const int tiles = tab[0].x;
+    const int tiles = a.sh_rows > 0 ? (int)((a.sh_rows + kBM - 1) / kBM) : tab[0].x;
     // 1-D grid, work grouped per XCD as in the tall-tile kernels: groups of 8
     // tiles x 4 slabs, XCD x (linear id L, L % 8 == x) takes groups x, x + 8, ...
     const int gx = GATEUP ? a.N / 128 : a.N / 256, nq = gx / 4;
@@ -343,7 +343,10 @@ __global__ __launch_bounds__(kNT) void moe_gemm_wd_kernel(GemmArgs a)
     const int tile = 8 * g + (i >> 2);
     const int slab = 4 * qq + (i & 3);
     if (tile >= tiles) return;
-    const int4 d = tab[1 + tile];   // {expert, first position, rows}
+    // {expert, first position, rows}: the table's, or the shared segment's own tiles
+    const int4 d = a.sh_rows > 0 ? int4{a.E, (int)(a.shared_base + (int64_t)kBM * tile),
+                                        (int)min((int64_t)kBM, a.sh_rows - (int64_t)kBM * tile), 0}
+                                 : tab[1 + tile];
     run_tile_wd<GATEUP, KBT>(a, d.x, d.y, min(d.z, kBM), slab, smem);
 }
 
@@ -361,10 +364,14 @@ bool wd_supported(int64_t H, int64_t I)
 int launch_gemm_wd(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
 {
     if (grid_y <= 0) return XS_OK;
-    if (a.bm != kBM) return set_error(XS_ERR_INVALID, "weight-direct GEMM needs %d-row tiles", kBM);
+    const bool sh_only = a.sh_rows > 0;   // the shared segment alone, in tiles of its own
+    if (!sh_only && a.bm != kBM) return set_error(XS_ERR_INVALID, "weight-direct GEMM needs %d-row tiles", kBM);
     const int gx = gateup ? a.N / 128 : a.N / 256;
-    if (a.K % (128 * kPD) || gx % 4 || !a.tile_tab || !a.Bp || (a.e_hi > a.E && !a.Bshp) || (!gateup && !a.Cf))
+    if (a.K % (128 * kPD) || gx % 4 || (!sh_only && (!a.tile_tab || !a.Bp)) || ((sh_only || a.e_hi > a.E) && !a.Bshp) ||
+        (!gateup && !a.Cf))
         return set_error(XS_ERR_UNSUPPORTED, "weight-direct GEMM shape K=%d N=%d", a.K, a.N);
+    if (sh_only && grid_y != (int)((a.sh_rows + kBM - 1) / kBM))
+        return set_error(XS_ERR_INVALID, "weight-direct GEMM: %d tiles for %lld shared rows", grid_y, (long long)a.sh_rows);
     const size_t smem = (size_t)kNSA * kStage + 8 * (size_t)(a.K / 128) + 4 * kNW * kBM + 256;
     if (smem > 160 * 1024) return set_error(XS_ERR_UNSUPPORTED, "K=%d needs %zu bytes of LDS", a.K, smem);
     // unrolled kernels for 4, 8, 16 and 32 K steps, the loop for other K

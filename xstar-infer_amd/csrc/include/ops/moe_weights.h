@@ -32,8 +32,9 @@ struct MoeLayerWeights
     // set when present in the checkpoint
     std::optional<Tensor> router_bias;         // [E] Float32
     std::optional<Tensor> shared_w13, shared_w13_scale, shared_w2, shared_w2_scale;  // 2-D, same formats
-    // set by pack_moe_layer_frag: the FP8 weights again, in MFMA fragment order
-    std::optional<Tensor> w13_frag, w2_frag, shared_w13_frag, shared_w2_frag;
+    // set by pack_moe_layer_frag: the weights again, in MFMA fragment order
+    // (MXFP4 layers: also their scales; the shared expert is FP8)
+    std::optional<Tensor> w13_frag, w2_frag, shared_w13_frag, shared_w2_frag, w13_scale_frag, w2_scale_frag;
 };
 
 /**
@@ -47,11 +48,12 @@ struct MoeLayerWeights
 MoeLayerWeights load_moe_layer(const std::vector<std::string> &paths, const std::string &prefix, Device device);
 
 /**
- * Adds fragment-packed copies of the layer's FP8 expert weights (CUDA, FP8
- * layers only; xs_pack_weight_fp8_frag), which moe_block_ffn then hands to the
- * GEMMs that load weights straight into registers.  The results are the same
- * bits; the FP8 expert weights take twice the device memory.  No reference
+ * Adds fragment-packed copies of the layer's expert weights (CUDA only;
+ * xs_pack_weight_fp8_frag, and for MXFP4 routed experts
+ * xs_pack_weight_mxfp4_frag with their scales), which moe_block_ffn then hands
+ * to the GEMMs that load weights straight into registers.  The results are the
+ * same bits; the expert weights take twice the device memory.  No reference
  * counterpart.  Throws "unsupported device" (host weights) and "unsupported
- * dtype" (MXFP4 layers).
+ * dtype".
  */
 void pack_moe_layer_frag(MoeLayerWeights &w);

@@ -32,6 +32,7 @@ namespace {
 // fragment-packed copies of the FP8 weights (pack_moe_layer_frag), or none
 struct Frag {
     const Tensor *w13 = nullptr, *w2 = nullptr, *shared_w13 = nullptr, *shared_w2 = nullptr;
+    const Tensor *w13_scale = nullptr, *w2_scale = nullptr;   // MXFP4 layers
 };
 }  // namespace
 
@@ -133,15 +134,20 @@ static Tensor moe_core(const Tensor &x, const Tensor &router_w, const Tensor *ro
         t.shared_w2 = shared_w2->data();
         t.shared_w2_scale = static_cast<const float *>(shared_w2_scale->data());
     }
-    if (frag.w13 && frag.w2 && !fp4) {
-        for (const Tensor *f : {frag.w13, frag.w2, frag.shared_w13, frag.shared_w2})
+    if (frag.w13 && frag.w2 && (!fp4 || (frag.w13_scale && frag.w2_scale))) {
+        for (const Tensor *f : {frag.w13, frag.w2, frag.shared_w13, frag.shared_w2, frag.w13_scale, frag.w2_scale})
             if (f) same_device(x, *f);
         if (frag.w13->nbytes() != w13.nbytes() || frag.w2->nbytes() != w2.nbytes() ||
+            (fp4 && (frag.w13_scale->nbytes() != w13_scale.nbytes() || frag.w2_scale->nbytes() != w2_scale.nbytes())) ||
             (frag.shared_w13 && has_shared && frag.shared_w13->nbytes() != shared_w13->nbytes()) ||
             (frag.shared_w2 && has_shared && frag.shared_w2->nbytes() != shared_w2->nbytes()))
             throw std::runtime_error("shape mismatch");
         t.w13_frag = frag.w13->data();
         t.w2_frag = frag.w2->data();
+        if (fp4) {
+            t.w13_scale_frag = frag.w13_scale->data();
+            t.w2_scale_frag = frag.w2_scale->data();
+        }
         if (has_shared && frag.shared_w13 && frag.shared_w2) {
             t.shared_w13_frag = frag.shared_w13->data();
             t.shared_w2_frag = frag.shared_w2->data();
@@ -174,7 +180,8 @@ Tensor moe_block_ffn(const Tensor &h, const Tensor &ln2_w, float eps, const MoeL
 {
     if (!w.router_w || !w.w13 || !w.w13_scale || !w.w2 || !w.w2_scale) throw std::runtime_error("shape mismatch");
     auto p = [](const std::optional<Tensor> &t) { return t ? &*t : nullptr; };
-    const Frag f{p(w.w13_frag), p(w.w2_frag), p(w.shared_w13_frag), p(w.shared_w2_frag)};
+    const Frag f{p(w.w13_frag), p(w.w2_frag), p(w.shared_w13_frag), p(w.shared_w2_frag), p(w.w13_scale_frag),
+                 p(w.w2_scale_frag)};
     return moe_core(h, *w.router_w, p(w.router_bias), *w.w13, *w.w13_scale, *w.w2, *w.w2_scale, p(w.shared_w13),
                     p(w.shared_w13_scale), p(w.shared_w2), p(w.shared_w2_scale), top_k, n_group, topk_group,
                     renormalize, routed_scaling, router_exact, &ln2_w, eps, &h, f);

@@ -6,6 +6,7 @@
 #include <memory>
 #include <stdexcept>
 #include <unordered_map>
+#include <utility>
 
 #include "weight_io.h"
 #include "xs_moe.h"
@@ -190,7 +191,9 @@ void pack_moe_layer_frag(MoeLayerWeights &w)
 {
     if (!w.w13 || !w.w2) throw std::runtime_error("shape mismatch");
     if (w.w13->device() != Device::CUDA) throw std::runtime_error("unsupported device");
-    if (w.w13->dtype() != DType::Float8E4M3 || w.w2->dtype() != DType::Float8E4M3)
+    const bool fp4 = w.w13->dtype() == DType::Float4E2M1x2;
+    if ((!fp4 && w.w13->dtype() != DType::Float8E4M3) || w.w2->dtype() != w.w13->dtype() || !w.w13_scale ||
+        !w.w2_scale)
         throw std::runtime_error("unsupported dtype");
     auto pack = [](const Tensor &t, std::int64_t batch, std::int64_t n, std::int64_t k) {
         Tensor out(t.shape(), t.dtype(), Device::CUDA);
@@ -198,9 +201,26 @@ void pack_moe_layer_frag(MoeLayerWeights &w)
                                          static_cast<std::uint8_t *>(out.data()), nullptr));
         return out;
     };
+    auto pack4 = [](const Tensor &t, const Tensor &s, std::int64_t batch, std::int64_t n, std::int64_t k) {
+        std::pair<Tensor, Tensor> o{Tensor(t.shape(), t.dtype(), Device::CUDA), Tensor(s.shape(), s.dtype(), Device::CUDA)};
+        xs_check(xs_pack_weight_mxfp4_frag(static_cast<const std::uint8_t *>(t.data()),
+                                           static_cast<const std::uint8_t *>(s.data()), batch, n, k,
+                                           static_cast<std::uint8_t *>(o.first.data()),
+                                           static_cast<std::uint8_t *>(o.second.data()), nullptr));
+        return o;
+    };
     const std::int64_t E = w.E, H = w.H, I = w.I;
-    w.w13_frag = pack(*w.w13, E, 2 * I, H);
-    w.w2_frag = pack(*w.w2, E, H, I);
+    if (fp4) {
+        auto a = pack4(*w.w13, *w.w13_scale, E, 2 * I, H);
+        auto b = pack4(*w.w2, *w.w2_scale, E, H, I);
+        w.w13_frag = std::move(a.first);
+        w.w13_scale_frag = std::move(a.second);
+        w.w2_frag = std::move(b.first);
+        w.w2_scale_frag = std::move(b.second);
+    } else {
+        w.w13_frag = pack(*w.w13, E, 2 * I, H);
+        w.w2_frag = pack(*w.w2, E, H, I);
+    }
     if (w.shared_w13 && w.shared_w2) {
         w.shared_w13_frag = pack(*w.shared_w13, 1, 2 * I, H);
         w.shared_w2_frag = pack(*w.shared_w2, 1, H, I);

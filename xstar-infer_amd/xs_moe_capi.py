@@ -295,7 +295,10 @@ class MoeLayer:
         elif frag:
             w13p, s13p = pack_weight_mxfp4_frag(self.w13, self.w13_scale)
             w2p, s2p = pack_weight_mxfp4_frag(self.w2, self.w2_scale)
-            self.frag = (w13p, w2p, None, None, s13p, s2p)
+            sh13p = sh2p = None   # the FP8 shared expert
+            if self.shared is not None:
+                sh13p, sh2p = pack_weight_fp8_frag(self.shared[0]), pack_weight_fp8_frag(self.shared[2])
+            self.frag = (w13p, w2p, sh13p, sh2p, s13p, s2p)
 
     def params(self, T, x_dtype):
         return MoeParams(T, self.H, self.I, self.E, self.top_k, self.n_group, self.topk_group,
