@@ -168,7 +168,7 @@ PYBIND11_MODULE(xstar_cpp, m)
         .def_property_readonly("shared_w2_frag", &opt_member<&MoeLayerWeights::shared_w2_frag>)
         .def_property_readonly("w13_scale_frag", &opt_member<&MoeLayerWeights::w13_scale_frag>)
         .def_property_readonly("w2_scale_frag", &opt_member<&MoeLayerWeights::w2_scale_frag>);
-    m.def("pack_moe_layer_frag", &pack_moe_layer_frag, py::arg("w"));
+    m.def("pack_moe_layer_frag", &pack_moe_layer_frag, py::arg("w"), py::arg("packed_only") = false);
     m.def("load_moe_layer", &load_moe_layer, py::arg("paths"), py::arg("prefix"), py::arg("device") = Device::CUDA);
 
     m.def("moe_router_logits", &moe_router_logits, py::arg("x"), py::arg("router_w"), py::arg("exact") = false);

@@ -174,8 +174,23 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     int rc = check_params(p);
     if (rc) return rc;
     if (p->T == 0) return XS_OK;   // empty input: nothing is read or written (its tensors may be null)
-    XS_REQUIRE(t && t->x && t->router_w && t->w13 && t->w13_scale && t->w2 && t->w2_scale && t->out,
-               "null pointer");
+    XS_REQUIRE(t && t->x && t->router_w && t->out, "null pointer");
+    // packed-only layer: the routed weights are given only in fragment order
+    // (w13 / w2 NULL, w13_frag / w2_frag set; MXFP4: with their packed scales)
+    const bool packed_only = !t->w13 && !t->w2;
+    const bool fp4_layer = p->routed_format == XS_FP4_E2M1X2;
+    if (packed_only) {
+        XS_REQUIRE(t->w13_frag && t->w2_frag && (!fp4_layer || (t->w13_scale_frag && t->w2_scale_frag)) &&
+                       (fp4_layer || (t->w13_scale && t->w2_scale)),
+                   "null pointer: a layer without w13 / w2 needs their packed copies (and scales)");
+        XS_REQUIRE(!p->has_shared || (t->shared_w13_frag && t->shared_w2_frag && t->shared_w13_scale &&
+                                      t->shared_w2_scale),
+                   "null shared expert pointer: a packed-only layer needs the shared expert's packed copies");
+    } else {
+        XS_REQUIRE(t->w13 && t->w13_scale && t->w2 && t->w2_scale, "null pointer");
+        XS_REQUIRE(!p->has_shared || (t->shared_w13 && t->shared_w13_scale && t->shared_w2 && t->shared_w2_scale),
+                   "null shared expert pointer");
+    }
     XS_REQUIRE(!p->has_norm || t->norm_weight, "null norm weight");
     XS_REQUIRE(((uintptr_t)t->x & 15) == 0 && ((uintptr_t)t->out & 15) == 0 &&
                    ((uintptr_t)t->residual & 15) == 0,
@@ -184,8 +199,9 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
                    ((uintptr_t)t->shared_w13 & 15) == 0 && ((uintptr_t)t->shared_w2 & 15) == 0 &&
                    ((uintptr_t)t->router_w & 15) == 0,
                "misaligned operand: weights need 16-byte alignment");
-    XS_REQUIRE(!p->has_shared || (t->shared_w13 && t->shared_w13_scale && t->shared_w2 && t->shared_w2_scale),
-               "null shared expert pointer");
+    XS_REQUIRE(((uintptr_t)t->w13_frag & 15) == 0 && ((uintptr_t)t->w2_frag & 15) == 0 &&
+                   ((uintptr_t)t->shared_w13_frag & 15) == 0 && ((uintptr_t)t->shared_w2_frag & 15) == 0,
+               "misaligned operand: packed weights need 16-byte alignment");
     const WsLayout L = layout(p);
     XS_REQUIRE(ws != nullptr || L.total == 0, "workspace is null");
     if (ws_bytes < L.total) return set_error(XS_ERR_WORKSPACE, "workspace too small: %zu < %zu", ws_bytes, L.total);
@@ -243,26 +259,41 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     // 3. permute: (expert, token)-sorted positions, tile offsets
     if ((rc = prof_mark(3, st))) return rc;
     const bool wide = use_wide(p);
-    const bool fused = fuse_combine(p);
-    // weight-direct tall tiles when the layer gave fragment-packed weights
-    // (XS_WIDE_DIRECT=0 keeps the LDS-ring kernels: measurements, tests)
-    const bool direct = wide && !fused && t->w13_frag && t->w2_frag &&
-                        (!p->has_shared || (t->shared_w13_frag && t->shared_w2_frag)) && wd_supported(H, I) &&
-                        getenv_flag("XS_WIDE_DIRECT", true);
-    const int bm = direct ? wd_tile_rows() : wide ? wide_tile_rows() : pick_bm((double)S / (double)E);
-    // weight-direct decode GEMMs for 16-row tiles, likewise from the packed
-    // weights (XS_DECODE_DIRECT=0 keeps the LDS-ring and stream-K kernels)
-    // weight-direct MXFP4 GEMMs for the routed experts on 64- and 128-row
-    // tiles, from packed weights and scales (XS_FP4_DIRECT=0: the tiled and
-    // stream-K kernels)
-    const bool direct4 = fp4 && (bm == 64 || bm == 128) && t->w13_frag && t->w2_frag && t->w13_scale_frag &&
-                         t->w2_scale_frag && wd4_supported(H, I) && getenv_flag("XS_FP4_DIRECT", true);
-    // ... and their FP8 shared expert on the weight-direct prefill kernel, in
-    // 128-row tiles of its own
+    const bool fused = fuse_combine(p) && !packed_only;
+    // Weight-direct GEMMs (fragment-packed weights loaded straight into
+    // registers) when the layer gives the packed copies: the tall tiles of
+    // prefill (moe_gemm_wd.hip), the 16-row decode tiles (moe_gemm_wdd.hip),
+    // MXFP4 routed experts on 64- and 128-row tiles (moe_gemm_wd4.hip) with
+    // their FP8 shared expert on the prefill kernel in 128-row tiles of its
+    // own.  XS_WIDE_DIRECT / XS_DECODE_DIRECT / XS_FP4_DIRECT = 0 keep the
+    // LDS-ring, tiled and stream-K kernels (measurements, tests).  A
+    // packed-only layer always takes them: FP8 batches that are not 16-row
+    // decode go to the 128-row prefill kernel (the extra rows of short tiles
+    // cost MFMA time that the weight stream hides), MXFP4 batches to 64-row
+    // tiles at least.
+    const bool sh_frag = !p->has_shared || (t->shared_w13_frag && t->shared_w2_frag);
+    const bool frag8 = !fp4 && t->w13_frag && t->w2_frag && sh_frag;
+    const bool frag4 = fp4 && t->w13_frag && t->w2_frag && t->w13_scale_frag && t->w2_scale_frag;
+    int bm = pick_bm((double)S / (double)E);
+    bool direct, ddirect, direct4;
+    if (packed_only) {
+        if (fp4 && bm < 64) bm = 64;
+        ddirect = !fp4 && bm == 16 && wdd_supported(H, I);
+        direct = !fp4 && !ddirect && wd_supported(H, I);
+        direct4 = fp4 && wd4_supported(H, I);
+        if (!direct && !ddirect && !direct4)
+            return set_error(XS_ERR_UNSUPPORTED, "packed-only layer: no weight-direct GEMM for H=%lld I=%lld",
+                             (long long)H, (long long)I);
+    } else {
+        direct = wide && !fused && frag8 && wd_supported(H, I) && getenv_flag("XS_WIDE_DIRECT", true);
+        ddirect = !wide && frag8 && bm == 16 && wdd_supported(H, I) && getenv_flag("XS_DECODE_DIRECT", true);
+        direct4 = frag4 && (bm == 64 || bm == 128) && wd4_supported(H, I) && getenv_flag("XS_FP4_DIRECT", true);
+    }
     const bool sdirect = direct4 && shared_rows && t->shared_w13_frag && t->shared_w2_frag && wd_supported(H, I);
-    const bool ddirect = !wide && !fp4 && bm == 16 && t->w13_frag && t->w2_frag &&
-                         (!p->has_shared || (t->shared_w13_frag && t->shared_w2_frag)) && wdd_supported(H, I) &&
-                         getenv_flag("XS_DECODE_DIRECT", true);
+    if (packed_only && fp4 && shared_rows && !sdirect)
+        return set_error(XS_ERR_UNSUPPORTED, "packed-only layer: no weight-direct GEMM for the shared expert");
+    if (direct) bm = wd_tile_rows();
+    else if (wide && !packed_only) bm = wide_tile_rows();
     PermuteOut po = {};
     po.counts = WS(int32_t, counts);
     po.offsets = offsets;
@@ -284,7 +315,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     // FP8: all tiles in one launch; MXFP4: the routed tiles (the FP8 shared
     // expert runs the tiled kernel)
     const int stream_tiles = fp4 ? routed_tiles : routed_tiles + shared_tiles;
-    const bool stream = !ddirect && !direct4 && stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
+    const bool stream = !direct && !ddirect && !direct4 && stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
                         (sm == 2 || (sm == 1 && stream_items(true, (int)I, stream_tiles) >= 2 * (int64_t)stream_blocks()));
     if (stream) {
         po.zero = WS(int32_t, cnt1);

@@ -52,8 +52,10 @@ MoeLayerWeights load_moe_layer(const std::vector<std::string> &paths, const std:
  * xs_pack_weight_fp8_frag, and for MXFP4 routed experts
  * xs_pack_weight_mxfp4_frag with their scales), which moe_block_ffn then hands
  * to the GEMMs that load weights straight into registers.  The results are the
- * same bits; the expert weights take twice the device memory.  No reference
- * counterpart.  Throws "unsupported device" (host weights) and "unsupported
- * dtype".
+ * same bits.  packed_only = false keeps the row-major weights too (twice the
+ * device memory); true drops them (w13, w2 and the shared expert's become
+ * empty), and every GEMM of the layer is then a weight-direct one.  No
+ * reference counterpart.  Throws "unsupported device" (host weights) and
+ * "unsupported dtype".
  */
-void pack_moe_layer_frag(MoeLayerWeights &w);
+void pack_moe_layer_frag(MoeLayerWeights &w, bool packed_only = false);

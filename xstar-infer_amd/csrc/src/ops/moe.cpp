@@ -33,6 +33,7 @@ namespace {
 struct Frag {
     const Tensor *w13 = nullptr, *w2 = nullptr, *shared_w13 = nullptr, *shared_w2 = nullptr;
     const Tensor *w13_scale = nullptr, *w2_scale = nullptr;   // MXFP4 layers
+    bool only = false;   // packed copies alone: the weight arguments are the packed tensors
 };
 }  // namespace
 
@@ -152,6 +153,12 @@ static Tensor moe_core(const Tensor &x, const Tensor &router_w, const Tensor *ro
             t.shared_w13_frag = frag.shared_w13->data();
             t.shared_w2_frag = frag.shared_w2->data();
         }
+        if (frag.only) {   // no row-major copies: every GEMM reads the packed ones
+            t.w13 = nullptr;
+            t.w2 = nullptr;
+            t.shared_w13 = nullptr;
+            t.shared_w2 = nullptr;
+        }
     }
     t.out = out.data();
     t.norm_weight = norm_weight ? norm_weight->data() : nullptr;
@@ -178,13 +185,20 @@ Tensor moe_block_ffn(const Tensor &h, const Tensor &ln2_w, float eps, const MoeL
                      std::int64_t n_group, std::int64_t topk_group, bool renormalize, float routed_scaling,
                      bool router_exact)
 {
-    if (!w.router_w || !w.w13 || !w.w13_scale || !w.w2 || !w.w2_scale) throw std::runtime_error("shape mismatch");
+    // packed-only layers (pack_moe_layer_frag(w, true)) carry their shapes and
+    // dtypes in the packed tensors
+    const bool only = !w.w13 && !w.w2 && w.w13_frag && w.w2_frag;
+    if (!w.router_w || !w.w13_scale || !w.w2_scale || (!only && (!w.w13 || !w.w2)))
+        throw std::runtime_error("shape mismatch");
     auto p = [](const std::optional<Tensor> &t) { return t ? &*t : nullptr; };
-    const Frag f{p(w.w13_frag), p(w.w2_frag), p(w.shared_w13_frag), p(w.shared_w2_frag), p(w.w13_scale_frag),
-                 p(w.w2_scale_frag)};
-    return moe_core(h, *w.router_w, p(w.router_bias), *w.w13, *w.w13_scale, *w.w2, *w.w2_scale, p(w.shared_w13),
-                    p(w.shared_w13_scale), p(w.shared_w2), p(w.shared_w2_scale), top_k, n_group, topk_group,
-                    renormalize, routed_scaling, router_exact, &ln2_w, eps, &h, f);
+    Frag f{p(w.w13_frag), p(w.w2_frag), p(w.shared_w13_frag), p(w.shared_w2_frag), p(w.w13_scale_frag),
+           p(w.w2_scale_frag)};
+    f.only = only;
+    const Tensor &w13 = only ? *w.w13_frag : *w.w13, &w2 = only ? *w.w2_frag : *w.w2;
+    const Tensor *sw13 = only ? p(w.shared_w13_frag) : p(w.shared_w13), *sw2 = only ? p(w.shared_w2_frag) : p(w.shared_w2);
+    return moe_core(h, *w.router_w, p(w.router_bias), w13, *w.w13_scale, w2, *w.w2_scale, sw13, p(w.shared_w13_scale),
+                    sw2, p(w.shared_w2_scale), top_k, n_group, topk_group, renormalize, routed_scaling, router_exact,
+                    &ln2_w, eps, &h, f);
 }
 
 Tensor moe_router_logits(const Tensor &x, const Tensor &router_w, bool exact)

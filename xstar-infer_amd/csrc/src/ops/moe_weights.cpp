@@ -187,7 +187,7 @@ MoeLayerWeights load_moe_layer(const std::vector<std::string> &paths, const std:
     return L;
 }
 
-void pack_moe_layer_frag(MoeLayerWeights &w)
+void pack_moe_layer_frag(MoeLayerWeights &w, bool packed_only)
 {
     if (!w.w13 || !w.w2) throw std::runtime_error("shape mismatch");
     if (w.w13->device() != Device::CUDA) throw std::runtime_error("unsupported device");
@@ -226,4 +226,10 @@ void pack_moe_layer_frag(MoeLayerWeights &w)
         w.shared_w2_frag = pack(*w.shared_w2, 1, H, I);
     }
     xs_check(xs_stream_synchronize(nullptr));
+    if (packed_only) {
+        w.w13.reset();
+        w.w2.reset();
+        w.shared_w13.reset();
+        w.shared_w2.reset();
+    }
 }

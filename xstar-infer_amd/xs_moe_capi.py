@@ -267,9 +267,12 @@ def pack_weight_mxfp4_frag(w, s):
 
 class MoeLayer:
     """Holds weights (device tensors) and calls xs_moe_forward.  frag=True also
-    keeps fragment-packed copies of the weights (FP8 layers: routed and shared;
-    MXFP4 layers: routed weights and scales), which the GEMMs load straight into
-    registers (same results)."""
+    keeps fragment-packed copies of the weights (routed and shared; MXFP4
+    layers: routed weights with their scales, and the FP8 shared expert), which
+    the GEMMs load straight into registers (same results).  frag="only" keeps
+    the packed copies alone (the row-major expert weights are dropped, so the
+    layer takes no more memory than before), and every GEMM is a weight-direct
+    one."""
 
     def __init__(self, router_w, w13, w13_scale, w2, w2_scale, top_k, router_bias=None,
                  shared=None, routed_format=XS_FP8_E4M3, n_group=1, topk_group=1,
@@ -299,6 +302,10 @@ class MoeLayer:
             if self.shared is not None:
                 sh13p, sh2p = pack_weight_fp8_frag(self.shared[0]), pack_weight_fp8_frag(self.shared[2])
             self.frag = (w13p, w2p, sh13p, sh2p, s13p, s2p)
+        if frag == "only":
+            self.w13 = self.w2 = None
+            if self.shared is not None:
+                self.shared = (None, self.shared[1], None, self.shared[3])
 
     def params(self, T, x_dtype):
         return MoeParams(T, self.H, self.I, self.E, self.top_k, self.n_group, self.topk_group,
