@@ -238,8 +238,12 @@ typedef struct {
      * present), the prefill and decode GEMMs load their weights straight into
      * registers from these copies, with the same results bit for bit.  MXFP4
      * layers: w13_frag / w2_frag and w13_scale_frag / w2_scale_frag from
-     * xs_pack_weight_mxfp4_frag (routed experts; the shared expert stays FP8
-     * and row-major).  NULL = not given. */
+     * xs_pack_weight_mxfp4_frag (routed experts; the shared expert is FP8, its
+     * packed copy from xs_pack_weight_fp8_frag).  NULL = not given.
+     * Packed-only layer: w13 and w2 (and shared_w13 / shared_w2) NULL, the
+     * packed copies given; the block scales (FP8) stay required.  Every GEMM
+     * is then a weight-direct one, and a shape they do not take (K a multiple
+     * of 512, N of 512) is refused with XS_ERR_UNSUPPORTED. */
     const void *w13_frag;
     const void *w2_frag;
     const void *shared_w13_frag;
