@@ -207,13 +207,19 @@ def main():
     return 0
 
 
+def bench_frag():
+    """XS_BENCH_FRAG: 0 (default) row-major weights; 1 also fragment-packed
+    copies (the weight-direct GEMMs); only: packed copies alone."""
+    v = os.environ.get("XS_BENCH_FRAG", "0")
+    return "only" if v == "only" else v == "1"
+
+
 def prefill(a, X, torch):
     from moe_synth import synth_layer, layer_from, expert_bytes, layer_flops
     T = 8192
     g = synth_layer(T, H, I, E, K_TOP, seed=0, zipf=1.1)
-    # XS_BENCH_FRAG=1: the layer also holds fragment-packed FP8 weights, and
-    # the prefill GEMMs take the weight-direct kernels
-    layer = layer_from(g, frag=os.environ.get("XS_BENCH_FRAG", "0") == "1")
+    # XS_BENCH_FRAG=1 / only: fragment-packed weights, weight-direct GEMMs
+    layer = layer_from(g, frag=bench_frag())
     ms, stages = time_forward(layer, g["x"], a.steps, a.warmup, profile=True)
     flops = layer_flops(T, H, I, E, K_TOP)
     counts = routed_counts(layer, g["x"])
@@ -283,8 +289,8 @@ def decode(a, X, torch):
     from moe_synth import synth_layer, layer_from, expert_bytes
     dec = {}
     gd = synth_layer(256, H, I, E, K_TOP, seed=1, bias_std=0.0)
-    # XS_BENCH_FRAG=1: fragment-packed FP8 weights, weight-direct decode GEMMs
-    L = layer_from(gd, frag=os.environ.get("XS_BENCH_FRAG", "0") == "1")
+    # XS_BENCH_FRAG=1 / only: fragment-packed weights, weight-direct GEMMs
+    L = layer_from(gd, frag=bench_frag())
     for Td in (int(t) for t in a.decode_tokens.split(",")):
         xd = gd["x"][:Td].contiguous()
         msd, st = time_forward(L, xd, max(a.steps, 50), a.warmup, profile=True)
@@ -330,8 +336,8 @@ def fp4_layer(a, X, torch):
     """MXFP4 routed experts (FP8 shared), 2048 tokens."""
     from moe_synth import synth_layer, layer_from, expert_bytes, layer_flops
     g4 = synth_layer(2048, H, I, E, K_TOP, seed=3, fp4=True)
-    # XS_BENCH_FRAG=1: packed MXFP4 weights and scales, weight-direct GEMMs
-    L4 = layer_from(g4, frag=os.environ.get("XS_BENCH_FRAG", "0") == "1")
+    # XS_BENCH_FRAG=1 / only: packed MXFP4 weights and scales, weight-direct GEMMs
+    L4 = layer_from(g4, frag=bench_frag())
     ms4, st4 = time_forward(L4, g4["x"], a.steps, a.warmup, profile=True)
     ne4 = routed_expert_count(L4, g4["x"])
     by4 = ne4 * expert_bytes(H, I, True) + expert_bytes(H, I, False) + E * H * 2

@@ -52,3 +52,46 @@ def test_argument_validation_without_gpu():
     rc = L.xs_rmsnorm(ctypes.c_void_p(16), ctypes.c_void_p(16), X.XS_BF16, 4, 96, 1e-6, ctypes.c_void_p(16),
                       ctypes.c_void_p(16), ctypes.c_void_p(16), None)
     assert rc == 1 and b"hidden % 128" in L.xs_last_error()
+
+
+def test_packed_weight_validation_without_gpu():
+    """The forward's checks of packed-only layers and of the packing entry
+    points, which all run before anything touches a GPU."""
+    import xs_moe_capi as X
+    L = X.lib()
+    v = ctypes.c_void_p(4096)   # an aligned stand-in pointer: never dereferenced here
+    p = X.MoeParams(16, 256, 256, 8, 2, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 1, 0)
+    names = [f[0] for f in X.MoeTensors._fields_]
+    def tensors(**given):
+        t = X.MoeTensors()
+        for n in ("x", "router_w", "out", "w13_scale", "w2_scale", "shared_w13_scale", "shared_w2_scale"):
+            setattr(t, n, v)
+        for n, val in given.items():
+            assert n in names
+            setattr(t, n, val)
+        return t
+    # no row-major weights and no packed copies
+    rc = L.xs_moe_forward(ctypes.byref(p), ctypes.byref(tensors()), v, 1 << 30, None)
+    assert rc == 1 and b"packed copies" in L.xs_last_error()
+    # packed routed weights, but the shared expert's missing
+    rc = L.xs_moe_forward(ctypes.byref(p), ctypes.byref(tensors(w13_frag=v, w2_frag=v)), v, 1 << 30, None)
+    assert rc == 1 and b"shared expert's packed" in L.xs_last_error()
+    # MXFP4 packed-only layers also need the packed scales
+    p4 = X.MoeParams(16, 256, 256, 8, 2, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP4_E2M1X2, 0, 0)
+    rc = L.xs_moe_forward(ctypes.byref(p4), ctypes.byref(tensors(w13_frag=v, w2_frag=v)), v, 1 << 30, None)
+    assert rc == 1 and b"packed copies" in L.xs_last_error()
+    # misaligned packed copies
+    rc = L.xs_moe_forward(ctypes.byref(p), ctypes.byref(tensors(w13_frag=ctypes.c_void_p(4104), w2_frag=v,
+                                                                shared_w13_frag=v, shared_w2_frag=v)),
+                          v, 1 << 30, None)
+    assert rc == 1 and b"packed weights need 16-byte alignment" in L.xs_last_error()
+    # the packing entry points
+    rc = L.xs_pack_weight_mxfp4_frag(v, v, 1, 24, 256, ctypes.c_void_p(1 << 20), ctypes.c_void_p(2 << 20), None)
+    assert rc == 1 and b"multiple of 16" in L.xs_last_error()
+    rc = L.xs_pack_weight_mxfp4_frag(ctypes.c_void_p(4100), v, 1, 16, 256, ctypes.c_void_p(1 << 20),
+                                     ctypes.c_void_p(2 << 20), None)
+    assert rc == 1 and b"misaligned" in L.xs_last_error()
+    rc = L.xs_pack_weight_mxfp4_frag(v, v, 1, 16, 256, v, ctypes.c_void_p(2 << 20), None)
+    assert rc == 1 and b"overlap" in L.xs_last_error()
+    rc = L.xs_pack_weight_fp8_frag(v, 1, 16, 200, ctypes.c_void_p(1 << 20), None)
+    assert rc == 1 and b"multiple of 16" in L.xs_last_error()
