@@ -40,6 +40,13 @@ def test_argument_validation_without_gpu():
     assert L.xs_moe_workspace_size(ctypes.byref(p)) == 0          # H % 256 != 0
     p.H = 256
     assert L.xs_moe_workspace_size(ctypes.byref(p)) > 0
+    # 32-bit row offsets in the GEMMs: T x H and T x (k + 1) x I below 2^32
+    big = X.MoeParams(1 << 20, 4096, 2048, 256, 6, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 1, 0)
+    assert L.xs_moe_workspace_size(ctypes.byref(big)) == 0
+    big.T = 299000    # 299000 x 7 x 2048 < 2^32
+    assert L.xs_moe_workspace_size(ctypes.byref(big)) > 0
+    big.T = 300000
+    assert L.xs_moe_workspace_size(ctypes.byref(big)) == 0
     rc = L.xs_moe_route(None, None, 4, 8, 2, 1, 1, 1, 1.0, None, None, None)
     assert rc == 1 and b"null" in L.xs_last_error()
     rc = L.xs_quant_act_fp8(ctypes.c_void_p(16), X.XS_BF16, 4, 100, ctypes.c_void_p(16), ctypes.c_void_p(16), None)

@@ -155,6 +155,10 @@ static int check_params(const xs_moe_params *p)
     XS_REQUIRE(p->routed_format == XS_FP8_E4M3 || p->routed_format == XS_FP4_E2M1X2,
                "unsupported routed expert format");
     XS_REQUIRE(p->T * p->top_k + p->T < ((int64_t)1 << 31), "too many rows");
+    // the GEMMs address gathered activation rows with 32-bit lane offsets:
+    // token x H bytes (gate_up) and position x I bytes (down) stay below 4 GiB
+    XS_REQUIRE(p->T * p->H < ((int64_t)1 << 32) && (p->T * p->top_k + p->T) * p->I < ((int64_t)1 << 32),
+               "too many rows: T x H and T x (top_k + 1) x I must stay below 2^32 (split the batch)");
     XS_REQUIRE(p->has_norm == 0 || p->has_norm == 1, "has_norm must be 0 or 1");
     XS_REQUIRE(p->routed_format != XS_FP4_E2M1X2 || p->I % 256 == 0,
                "shape mismatch: MXFP4 experts need I to be a multiple of 256");
@@ -598,6 +602,8 @@ int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int
     XS_REQUIRE(((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 && ((uintptr_t)C & 15) == 0 &&
                    ((uintptr_t)Bs & 3) == 0,
                "misaligned operand: A, B and C need 16-byte, Bs 4-byte alignment");
+    XS_REQUIRE(M * K < ((int64_t)1 << 32) && N * K < ((int64_t)1 << 32),
+               "shape mismatch: M x K and N x K must stay below 2^32 (32-bit row offsets)");
     XS_REQUIRE(M >= 0 && M < (1 << 24) && N >= 128 && N % 128 == 0 && K >= 128 && K % 128 == 0,
                "shape mismatch: N and K must be multiples of 128");
     size_t o_s, o_part;
