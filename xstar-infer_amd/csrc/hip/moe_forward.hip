@@ -317,7 +317,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     const int sm = use_stream(p);
     const int64_t rows_all = S + shared_rows;
     // FP8: all tiles in one launch; MXFP4: the routed tiles (the FP8 shared
-    // expert runs the tiled kernel)
+    // expert runs a launch of its own: tiled, or weight-direct)
     const int stream_tiles = fp4 ? routed_tiles : routed_tiles + shared_tiles;
     const bool stream = !direct && !ddirect && !direct4 && stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
                         (sm == 2 || (sm == 1 && stream_items(true, (int)I, stream_tiles) >= 2 * (int64_t)stream_blocks()));
