@@ -107,10 +107,13 @@ def test_weight_direct_decode_gemms_emulated(wdd_emu, args):
     assert "identical bytes: yes" in out, out[-2000:]
 
 
-def test_weight_direct_mxfp4_gemms_emulated(wd4_emu):
+@pytest.mark.parametrize("mode", ["0", "1"])
+def test_weight_direct_mxfp4_gemms_emulated(wd4_emu, mode):
     # 64 tokens, 4 experts top-2, Zipf(1.1), 64-row tiles, H=1024, I=512 (the
-    # loop form); MXFP4 weights, MXFP8 activations, e8m0 scales
-    r = subprocess.run([wd4_emu, "64", "4", "2", "1.1", "3", "1024", "512", "4", "0", "1", "64"],
+    # loop form); MXFP4 weights, MXFP8 activations, e8m0 scales.  Mode 0 lands
+    # each DMA at its wait (a read before its wait sees poison), mode 1 at issue
+    # (a refill of a ring slot that a wave still reads corrupts that read).
+    r = subprocess.run([wd4_emu, "64", "4", "2", "1.1", "3", "1024", "512", "4", mode, "1", "64"],
                        capture_output=True, text=True, timeout=900, env=dict(os.environ, EMU_CMP_TILED="1"))
     out = r.stdout + r.stderr
     assert r.returncode == 0 and "errors 0" in out, out[-3000:]
