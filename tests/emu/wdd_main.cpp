@@ -135,12 +135,19 @@ int main(int argc, char **argv)
         const unsigned gx = (unsigned)(a.N / kBN), gy = (unsigned)(tt + nsh);
         const size_t smem = 16 * 1024;   // static arrays only
         printf("pass %s: K=%d grid %ux%u\n", gateup ? "gate_up" : "down", a.K, gx, gy);
-#define XS_EMU_KB(KBV)                                                                               \
-        if (a.K == 128 * KBV) {                                                                      \
-            constexpr int PD = KBV < 4 ? KBV : 4;                                                    \
-            if (gateup) emu_launch([&] { moe_gemm_wdd_kernel<true, KBV, PD>(a); }, gx, gy, kNT, smem, conc); \
-            else emu_launch([&] { moe_gemm_wdd_kernel<false, KBV, PD>(a); }, gx, gy, kNT, smem, conc); \
-            return;                                                                                  \
+        fflush(stdout);
+        // the launcher's prefetch depth (8 for gate_up and for launches of
+        // fewer than 512 blocks, else 4); EMU_WDD_PD=4|8 forces one
+        const char *pf = getenv("EMU_WDD_PD");
+        const bool deep = pf ? atoi(pf) == 8 : (gateup || (int64_t)gx * gy < 512);
+#define XS_EMU_KB(KBV)                                                                                   \
+        if (a.K == 128 * KBV) {                                                                          \
+            constexpr int P4 = KBV < 4 ? KBV : 4, P8 = KBV < 8 ? KBV : 8;                                \
+            if (gateup && deep) emu_launch([&] { moe_gemm_wdd_kernel<true, KBV, P8>(a); }, gx, gy, kNT, smem, conc); \
+            else if (gateup) emu_launch([&] { moe_gemm_wdd_kernel<true, KBV, P4>(a); }, gx, gy, kNT, smem, conc); \
+            else if (deep) emu_launch([&] { moe_gemm_wdd_kernel<false, KBV, P8>(a); }, gx, gy, kNT, smem, conc); \
+            else emu_launch([&] { moe_gemm_wdd_kernel<false, KBV, P4>(a); }, gx, gy, kNT, smem, conc);   \
+            return;                                                                                      \
         }
         XS_EMU_KB(4) XS_EMU_KB(8) XS_EMU_KB(16) XS_EMU_KB(32)
 #undef XS_EMU_KB

@@ -89,17 +89,21 @@ def test_weight_direct_gemms_emulated(wd_emu):
     assert "shared segment alone: errors 0, identical bytes: yes" in out, out[-2000:]
 
 
-@pytest.mark.parametrize("args", [
+@pytest.mark.parametrize("args,pd", [
     # 16 tokens, 32 experts top-4 + shared, H=1024, I=512: one tile per expert
-    ["16", "32", "4", "0", "5", "1024", "512"],
+    # (the launcher's prefetch depth: 8 steps)
+    (["16", "32", "4", "0", "5", "1024", "512"], None),
     # 40 tokens, 8 experts top-2, Zipf(1.1), no shared expert, H=512, I=1024:
-    # experts of several 16-row tiles, ragged last tiles
-    ["40", "8", "2", "1.1", "6", "512", "1024"],
+    # experts of several 16-row tiles, ragged last tiles; 4-step prefetch
+    (["40", "8", "2", "1.1", "6", "512", "1024"], "4"),
 ])
-def test_weight_direct_decode_gemms_emulated(wdd_emu, args):
+def test_weight_direct_decode_gemms_emulated(wdd_emu, args, pd):
     shared = "0" if args[0] == "40" else "1"
+    env = dict(os.environ, EMU_CMP_TILED="1")
+    if pd:
+        env["EMU_WDD_PD"] = pd
     r = subprocess.run([wdd_emu, *args, "8", "0", "1", shared], capture_output=True, text=True, timeout=900,
-                       env=dict(os.environ, EMU_CMP_TILED="1"))
+                       env=env)
     out = r.stdout + r.stderr
     _check(out, r.returncode)
     # the 16-row tiled kernel on the same inputs writes the same bytes: the

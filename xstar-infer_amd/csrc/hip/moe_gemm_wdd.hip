@@ -25,8 +25,8 @@
 //     gate rows n0 + 16 w and the matching 16 up rows, so SwiGLU and the
 //     requantisation's 128-column amax stay inside the block; down, wave w
 //     owns the 16 rows n0 + 16 w;
-//   * each wave keeps PD K steps of loads in flight (8 waves x PD x 4-6 KB per
-//     block), and the K loop is unrolled in full (KB is a template argument),
+//   * each wave keeps PD K steps of loads in flight (4 or 8: 8 waves x PD x 4-6 KB
+//     per block), and the K loop is unrolled in full (KB is a template argument),
 //     so the compiler waits for exactly the step it uses: there is no loop back
 //     edge to make it wait for everything;
 //   * the row scales and block scales are staged in LDS once per block.
@@ -183,12 +183,18 @@ __global__ __launch_bounds__(kNT) void moe_gemm_wdd_kernel(GemmArgs a)
     }
 }
 
+// Prefetch depth: 8 steps where a CU holds one block anyway (gate_up: 136
+// VGPRs at 4 steps, 199-215 at 8) or the launch has fewer blocks than two per
+// CU (decode down at T = 1: 224); 4 steps otherwise, so that the down GEMM's
+// blocks (63-76 VGPRs) can share a CU.
 template <bool GATEUP, int KB>
 int launch_wdd(const GemmArgs &a, int grid_y, hipStream_t st)
 {
-    constexpr int PD = KB < 4 ? KB : 4;
+    constexpr int PD4 = KB < 4 ? KB : 4, PD8 = KB < 8 ? KB : 8;
     const int gx = a.N / kBN;
-    moe_gemm_wdd_kernel<GATEUP, KB, PD><<<dim3((unsigned)gx, (unsigned)grid_y), dim3(kNT), 0, st>>>(a);
+    const bool deep = GATEUP || (int64_t)gx * grid_y < 512;
+    if (deep) moe_gemm_wdd_kernel<GATEUP, KB, PD8><<<dim3((unsigned)gx, (unsigned)grid_y), dim3(kNT), 0, st>>>(a);
+    else moe_gemm_wdd_kernel<GATEUP, KB, PD4><<<dim3((unsigned)gx, (unsigned)grid_y), dim3(kNT), 0, st>>>(a);
     XS_LAUNCH_CHECK();
     return XS_OK;
 }
