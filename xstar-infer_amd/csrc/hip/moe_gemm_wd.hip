@@ -18,9 +18,9 @@
 //   * 128-row tiles; each of the 8 waves (two per SIMD) owns two 16-row weight
 //     tiles (gate_up: 16 gate rows and the matching 16 up rows; down: 32 rows)
 //     over all of the tile's tokens, so every weight byte is loaded once per
-//     block, 4 steps ahead into registers (230 of the 256 a wave gets; the
-//     loop keeps the products of one subtile at a time, folded while the next
-//     subtile's MFMAs run);
+//     block, 4 steps ahead into registers (the loop keeps the products of one
+//     subtile at a time, folded while the next subtile's MFMAs run; 183-190
+//     VGPRs with the K loop unrolled for 4-32 steps, 205-209 for other K);
 //   * activations (gathered token rows) alone use the LDS ring;
 //   * the weight loads are plain loads, so the compiler tracks their registers
 //     and waits itself; the activation DMAs (which write no register) are
