@@ -255,6 +255,26 @@ typedef struct {
 /* Device workspace the forward needs for these params (bytes, 256-aligned). */
 size_t xs_moe_workspace_size(const xs_moe_params *p);
 
+/* The kernels xs_moe_forward chooses for these params and tensors: the same
+ * decision, environment switches included, without launching anything or
+ * touching a GPU.  No reference counterpart: for callers and tests that check
+ * the dispatch.  T >= 1. */
+typedef enum {
+    XS_GEMM_TILED = 0,            /* one block per tile, operands through an LDS ring */
+    XS_GEMM_STREAM = 1,           /* persistent stream-K */
+    XS_GEMM_TALL = 2,             /* tall tiles, operands through LDS rings */
+    XS_GEMM_DIRECT_PREFILL = 3,   /* weight-direct, 128-row tiles */
+    XS_GEMM_DIRECT_DECODE = 4,    /* weight-direct, 16-row tiles */
+    XS_GEMM_DIRECT_MXFP4 = 5      /* weight-direct MXFP4, 64- or 128-row tiles */
+} xs_gemm_kind;
+typedef struct {
+    int tile_rows;       /* rows per tile of the routed GEMMs */
+    int routed_gemm;     /* xs_gemm_kind of the routed experts' gate_up and down */
+    int shared_gemm;     /* xs_gemm_kind of the shared expert (FP8 layers: the routed launch); -1: none */
+    int fused_combine;   /* 1: the down GEMM sums each token's rows itself */
+} xs_moe_plan_t;
+int xs_moe_plan(const xs_moe_params *p, const xs_moe_tensors *t, xs_moe_plan_t *out);
+
 /* [RMSNorm] + activation quant -> router -> top-k -> permute -> grouped gate_up
  * GEMM with SwiGLU and FP8 re-quant -> grouped down GEMM -> weighted combine
  * (+ shared).  With has_norm the layer computes moe(rmsnorm(x, norm_weight,

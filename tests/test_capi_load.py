@@ -102,3 +102,79 @@ def test_packed_weight_validation_without_gpu():
     assert rc == 1 and b"overlap" in L.xs_last_error()
     rc = L.xs_pack_weight_fp8_frag(v, 1, 16, 200, ctypes.c_void_p(1 << 20), None)
     assert rc == 1 and b"multiple of 16" in L.xs_last_error()
+
+
+def _stand_in_tensors(X, row_major=True, frag=False, fp4=False, shared=True):
+    v = ctypes.c_void_p(4096)   # aligned stand-in pointers: xs_moe_plan reads none of them
+    t = X.MoeTensors()
+    for n in ("x", "router_w", "out", "w13_scale", "w2_scale"):
+        setattr(t, n, v)
+    if row_major:
+        t.w13 = t.w2 = v
+    if shared:
+        t.shared_w13_scale = t.shared_w2_scale = v
+        if row_major:
+            t.shared_w13 = t.shared_w2 = v
+    if frag:
+        t.w13_frag = t.w2_frag = v
+        if shared:
+            t.shared_w13_frag = t.shared_w2_frag = v
+        if fp4:
+            t.w13_scale_frag = t.w2_scale_frag = v
+    return t
+
+
+@pytest.mark.parametrize("T,fmt,row_major,frag,want", [
+    # row-major FP8 (V4-Flash shape): tiled decode, stream-K from 16 tokens, tall tiles for prefill
+    (1, "fp8", True, False, (16, "tiled")),
+    (16, "fp8", True, False, (16, "stream")),
+    (8192, "fp8", True, False, (192, "tall")),
+    # with packed copies: the weight-direct kernels where they apply
+    (1, "fp8", True, True, (16, "direct_decode")),
+    (16, "fp8", True, True, (16, "direct_decode")),
+    (1200, "fp8", True, True, (32, "stream")),
+    (1500, "fp8", True, True, (128, "direct_prefill")),   # 9000 rows >= 32 E: tall tiles
+    (8192, "fp8", True, True, (128, "direct_prefill")),
+    # packed-only: every launch weight-direct, mid-size batches on 128-row tiles
+    (16, "fp8", False, True, (16, "direct_decode")),
+    (1200, "fp8", False, True, (128, "direct_prefill")),
+    (8192, "fp8", False, True, (128, "direct_prefill")),
+    # MXFP4
+    (2048, "fp4", True, False, (64, "stream")),
+    (2048, "fp4", True, True, (64, "direct_mxfp4")),
+    (16, "fp4", True, True, (16, "stream")),
+    (16, "fp4", False, True, (64, "direct_mxfp4")),
+])
+def test_kernel_plan_without_gpu(T, fmt, row_major, frag, want, monkeypatch):
+    """The forward's dispatch (xs_moe_plan, the same decision the forward
+    takes): tile height and kernel family per batch size and weight form."""
+    import xs_moe_capi as X
+    for n in ("XS_MOE_STREAM", "XS_WIDE_DIRECT", "XS_DECODE_DIRECT", "XS_FP4_DIRECT", "XS_FUSE_COMBINE"):
+        monkeypatch.delenv(n, raising=False)
+    f = X.XS_FP4_E2M1X2 if fmt == "fp4" else X.XS_FP8_E4M3
+    p = X.MoeParams(T, 4096, 2048, 256, 6, 1, 1, 1, 1.0, X.XS_BF16, f, 1, 0)
+    got = X.plan(p, _stand_in_tensors(X, row_major, frag, fmt == "fp4"))
+    assert (got["tile_rows"], got["routed"]) == want, got
+    if fmt == "fp8":
+        assert got["shared"] == got["routed"]       # one launch for routed and shared tiles
+    else:
+        assert got["shared"] == ("direct_prefill" if frag and got["routed"] == "direct_mxfp4" else "tiled")
+    assert not got["fused_combine"]
+
+
+def test_kernel_plan_switches_and_refusals(monkeypatch):
+    import xs_moe_capi as X
+    p = X.MoeParams(16, 4096, 2048, 256, 6, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 1, 0)
+    monkeypatch.setenv("XS_DECODE_DIRECT", "0")
+    assert X.plan(p, _stand_in_tensors(X, True, True))["routed"] == "stream"
+    monkeypatch.setenv("XS_MOE_STREAM", "0")
+    assert X.plan(p, _stand_in_tensors(X, True, True))["routed"] == "tiled"
+    # the switches do not apply to a packed-only layer: it has no other kernels
+    assert X.plan(p, _stand_in_tensors(X, False, True))["routed"] == "direct_decode"
+    # no shared expert
+    p.has_shared = 0
+    assert X.plan(p, _stand_in_tensors(X, True, False, shared=False))["shared"] is None
+    # a packed-only layer whose shape the weight-direct kernels do not take
+    q = X.MoeParams(16, 256, 256, 8, 2, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 0, 0)
+    with pytest.raises(X.XsError, match="no weight-direct GEMM"):
+        X.plan(q, _stand_in_tensors(X, False, True, shared=False))

@@ -172,12 +172,74 @@ static int check_params(const xs_moe_params *p)
     return XS_OK;
 }
 
-int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_t ws_bytes,
-                hipStream_t st)
+// The kernels of one forward: the tile height and each GEMM's family.
+struct Plan {
+    int bm;
+    bool wide, fused, direct, ddirect, direct4, sdirect, stream;
+};
+
+static int make_plan(const xs_moe_params *p, const xs_moe_tensors *t, Plan &pl)
 {
-    int rc = check_params(p);
-    if (rc) return rc;
-    if (p->T == 0) return XS_OK;   // empty input: nothing is read or written (its tensors may be null)
+    const int64_t T = p->T, H = p->H, I = p->I, E = p->E, k = p->top_k;
+    const int64_t S = T * k;
+    const bool fp4 = p->routed_format == XS_FP4_E2M1X2;
+    const int shared_rows = p->has_shared ? (int)T : 0;
+    const bool packed_only = !t->w13 && !t->w2;
+    const bool wide = use_wide(p);
+    const bool fused = fuse_combine(p) && !packed_only;
+    // Weight-direct GEMMs (fragment-packed weights loaded straight into
+    // registers) when the layer gives the packed copies: the tall tiles of
+    // prefill (moe_gemm_wd.hip), the 16-row decode tiles (moe_gemm_wdd.hip),
+    // MXFP4 routed experts on 64- and 128-row tiles (moe_gemm_wd4.hip) with
+    // their FP8 shared expert on the prefill kernel in 128-row tiles of its
+    // own.  XS_WIDE_DIRECT / XS_DECODE_DIRECT / XS_FP4_DIRECT = 0 keep the
+    // LDS-ring, tiled and stream-K kernels (measurements, tests).  A
+    // packed-only layer always takes them: FP8 batches that are not 16-row
+    // decode go to the 128-row prefill kernel (the extra rows of short tiles
+    // cost MFMA time that the weight stream hides), MXFP4 batches to 64-row
+    // tiles at least.
+    const bool sh_frag = !p->has_shared || (t->shared_w13_frag && t->shared_w2_frag);
+    const bool frag8 = !fp4 && t->w13_frag && t->w2_frag && sh_frag;
+    const bool frag4 = fp4 && t->w13_frag && t->w2_frag && t->w13_scale_frag && t->w2_scale_frag;
+    int bm = pick_bm((double)S / (double)E);
+    bool direct, ddirect, direct4;
+    if (packed_only) {
+        if (fp4 && bm < 64) bm = 64;
+        ddirect = !fp4 && bm == 16 && wdd_supported(H, I);
+        direct = !fp4 && !ddirect && wd_supported(H, I);
+        direct4 = fp4 && wd4_supported(H, I);
+        if (!direct && !ddirect && !direct4)
+            return set_error(XS_ERR_UNSUPPORTED, "packed-only layer: no weight-direct GEMM for H=%lld I=%lld",
+                             (long long)H, (long long)I);
+    } else {
+        direct = wide && !fused && frag8 && wd_supported(H, I) && getenv_flag("XS_WIDE_DIRECT", true);
+        ddirect = !wide && frag8 && bm == 16 && wdd_supported(H, I) && getenv_flag("XS_DECODE_DIRECT", true);
+        direct4 = frag4 && (bm == 64 || bm == 128) && wd4_supported(H, I) && getenv_flag("XS_FP4_DIRECT", true);
+    }
+    const bool sdirect = direct4 && shared_rows && t->shared_w13_frag && t->shared_w2_frag && wd_supported(H, I);
+    if (packed_only && fp4 && shared_rows && !sdirect)
+        return set_error(XS_ERR_UNSUPPORTED, "packed-only layer: no weight-direct GEMM for the shared expert");
+    if (direct) bm = wd_tile_rows();
+    else if (wide && !packed_only) bm = wide_tile_rows();
+    const int routed_tiles = (int)(S / bm + (E < S ? E : S));
+    const int shared_tiles = (int)((shared_rows + bm - 1) / bm);
+    // Persistent GEMMs once the gate_up work (items of one tile x one 256-row
+    // slab) fills every CU twice; below that, whole items per block split
+    // less and the one-block-per-tile kernels are faster.
+    const int sm = use_stream(p);
+    const int64_t rows_all = S + shared_rows;
+    // FP8: all tiles in one launch; MXFP4: the routed tiles (the FP8 shared
+    // expert runs a launch of its own: tiled, or weight-direct)
+    const int stream_tiles = fp4 ? routed_tiles : routed_tiles + shared_tiles;
+    const bool stream = !direct && !ddirect && !direct4 && stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
+                        (sm == 2 || (sm == 1 && stream_items(true, (int)I, stream_tiles) >= 2 * (int64_t)stream_blocks()));
+    pl = Plan{bm, wide, fused, direct, ddirect, direct4, sdirect, stream};
+    return XS_OK;
+}
+
+// The tensors of a forward: present where the params need them, aligned.
+static int check_tensors(const xs_moe_params *p, const xs_moe_tensors *t)
+{
     XS_REQUIRE(t && t->x && t->router_w && t->out, "null pointer");
     // packed-only layer: the routed weights are given only in fragment order
     // (w13 / w2 NULL, w13_frag / w2_frag set; MXFP4: with their packed scales)
@@ -206,6 +268,16 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     XS_REQUIRE(((uintptr_t)t->w13_frag & 15) == 0 && ((uintptr_t)t->w2_frag & 15) == 0 &&
                    ((uintptr_t)t->shared_w13_frag & 15) == 0 && ((uintptr_t)t->shared_w2_frag & 15) == 0,
                "misaligned operand: packed weights need 16-byte alignment");
+    return XS_OK;
+}
+
+int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_t ws_bytes,
+                hipStream_t st)
+{
+    int rc = check_params(p);
+    if (rc) return rc;
+    if (p->T == 0) return XS_OK;   // empty input: nothing is read or written (its tensors may be null)
+    if ((rc = check_tensors(p, t))) return rc;
     const WsLayout L = layout(p);
     XS_REQUIRE(ws != nullptr || L.total == 0, "workspace is null");
     if (ws_bytes < L.total) return set_error(XS_ERR_WORKSPACE, "workspace too small: %zu < %zu", ws_bytes, L.total);
@@ -262,42 +334,11 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     if (rc) return rc;
     // 3. permute: (expert, token)-sorted positions, tile offsets
     if ((rc = prof_mark(3, st))) return rc;
-    const bool wide = use_wide(p);
-    const bool fused = fuse_combine(p) && !packed_only;
-    // Weight-direct GEMMs (fragment-packed weights loaded straight into
-    // registers) when the layer gives the packed copies: the tall tiles of
-    // prefill (moe_gemm_wd.hip), the 16-row decode tiles (moe_gemm_wdd.hip),
-    // MXFP4 routed experts on 64- and 128-row tiles (moe_gemm_wd4.hip) with
-    // their FP8 shared expert on the prefill kernel in 128-row tiles of its
-    // own.  XS_WIDE_DIRECT / XS_DECODE_DIRECT / XS_FP4_DIRECT = 0 keep the
-    // LDS-ring, tiled and stream-K kernels (measurements, tests).  A
-    // packed-only layer always takes them: FP8 batches that are not 16-row
-    // decode go to the 128-row prefill kernel (the extra rows of short tiles
-    // cost MFMA time that the weight stream hides), MXFP4 batches to 64-row
-    // tiles at least.
-    const bool sh_frag = !p->has_shared || (t->shared_w13_frag && t->shared_w2_frag);
-    const bool frag8 = !fp4 && t->w13_frag && t->w2_frag && sh_frag;
-    const bool frag4 = fp4 && t->w13_frag && t->w2_frag && t->w13_scale_frag && t->w2_scale_frag;
-    int bm = pick_bm((double)S / (double)E);
-    bool direct, ddirect, direct4;
-    if (packed_only) {
-        if (fp4 && bm < 64) bm = 64;
-        ddirect = !fp4 && bm == 16 && wdd_supported(H, I);
-        direct = !fp4 && !ddirect && wd_supported(H, I);
-        direct4 = fp4 && wd4_supported(H, I);
-        if (!direct && !ddirect && !direct4)
-            return set_error(XS_ERR_UNSUPPORTED, "packed-only layer: no weight-direct GEMM for H=%lld I=%lld",
-                             (long long)H, (long long)I);
-    } else {
-        direct = wide && !fused && frag8 && wd_supported(H, I) && getenv_flag("XS_WIDE_DIRECT", true);
-        ddirect = !wide && frag8 && bm == 16 && wdd_supported(H, I) && getenv_flag("XS_DECODE_DIRECT", true);
-        direct4 = frag4 && (bm == 64 || bm == 128) && wd4_supported(H, I) && getenv_flag("XS_FP4_DIRECT", true);
-    }
-    const bool sdirect = direct4 && shared_rows && t->shared_w13_frag && t->shared_w2_frag && wd_supported(H, I);
-    if (packed_only && fp4 && shared_rows && !sdirect)
-        return set_error(XS_ERR_UNSUPPORTED, "packed-only layer: no weight-direct GEMM for the shared expert");
-    if (direct) bm = wd_tile_rows();
-    else if (wide && !packed_only) bm = wide_tile_rows();
+    Plan pl;
+    if ((rc = make_plan(p, t, pl))) return rc;
+    const bool wide = pl.wide, fused = pl.fused, direct = pl.direct, ddirect = pl.ddirect, direct4 = pl.direct4,
+               sdirect = pl.sdirect;
+    const int bm = pl.bm;
     PermuteOut po = {};
     po.counts = WS(int32_t, counts);
     po.offsets = offsets;
@@ -311,16 +352,9 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
 
     const int routed_tiles = (int)(S / bm + (E < S ? E : S));
     const int shared_tiles = (int)((shared_rows + bm - 1) / bm);
-    // Persistent GEMMs once the gate_up work (items of one tile x one 256-row
-    // slab) fills every CU twice; below that, whole items per block split
-    // less and the one-block-per-tile kernels are faster.
-    const int sm = use_stream(p);
     const int64_t rows_all = S + shared_rows;
-    // FP8: all tiles in one launch; MXFP4: the routed tiles (the FP8 shared
-    // expert runs a launch of its own: tiled, or weight-direct)
     const int stream_tiles = fp4 ? routed_tiles : routed_tiles + shared_tiles;
-    const bool stream = !direct && !ddirect && !direct4 && stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
-                        (sm == 2 || (sm == 1 && stream_items(true, (int)I, stream_tiles) >= 2 * (int64_t)stream_blocks()));
+    const bool stream = pl.stream;
     if (stream) {
         po.zero = WS(int32_t, cnt1);
         po.zero_n = stream_items(true, (int)I, tiles16_max(p)) + 1;
@@ -557,6 +591,28 @@ size_t xs_moe_workspace_size(const xs_moe_params *p)
 {
     if (check_params(p)) return 0;
     return layout(p).total;
+}
+
+int xs_moe_plan(const xs_moe_params *p, const xs_moe_tensors *t, xs_moe_plan_t *out)
+{
+    XS_REQUIRE(out != nullptr, "null pointer");
+    int rc = check_params(p);
+    if (rc) return rc;
+    XS_REQUIRE(p->T >= 1, "T must be at least 1");
+    if ((rc = check_tensors(p, t))) return rc;
+    Plan pl;
+    if ((rc = make_plan(p, t, pl))) return rc;
+    const bool fp4 = p->routed_format == XS_FP4_E2M1X2;
+    out->tile_rows = pl.bm;
+    out->routed_gemm = pl.stream    ? XS_GEMM_STREAM
+                       : pl.direct  ? XS_GEMM_DIRECT_PREFILL
+                       : pl.ddirect ? XS_GEMM_DIRECT_DECODE
+                       : pl.direct4 ? XS_GEMM_DIRECT_MXFP4
+                       : pl.wide    ? XS_GEMM_TALL
+                                    : XS_GEMM_TILED;
+    out->shared_gemm = !p->has_shared ? -1 : !fp4 ? out->routed_gemm : pl.sdirect ? XS_GEMM_DIRECT_PREFILL : XS_GEMM_TILED;
+    out->fused_combine = pl.fused ? 1 : 0;
+    return XS_OK;
 }
 
 int xs_moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *workspace,

@@ -37,6 +37,14 @@ class MoeTensors(C.Structure):
         "w13_scale_frag", "w2_scale_frag")]
 
 
+class MoePlan(C.Structure):
+    _fields_ = [("tile_rows", C.c_int), ("routed_gemm", C.c_int), ("shared_gemm", C.c_int),
+                ("fused_combine", C.c_int)]
+
+
+GEMM_KINDS = ("tiled", "stream", "tall", "direct_prefill", "direct_decode", "direct_mxfp4")
+
+
 EXPORTS = {
     "xs_last_error": (C.c_char_p, []),
     "xs_device_count": (C.c_int, [P]),
@@ -61,6 +69,7 @@ EXPORTS = {
     "xs_gemm_fp8_blockscale_workspace_size": (C.c_size_t, [I64, I64]),
     "xs_gemm_fp8_blockscale": (C.c_int, [P, P, P, I64, I64, I64, P, P, C.c_size_t, P]),
     "xs_moe_workspace_size": (C.c_size_t, [P]),
+    "xs_moe_plan": (C.c_int, [P, P, P]),
     "xs_moe_forward": (C.c_int, [P, P, P, C.c_size_t, P]),
     "xs_moe_noalloc_scratch_bytes": (C.c_size_t, []),
     "xs_moe_forward_noalloc": (C.c_int, [P, P, P]),
@@ -265,6 +274,17 @@ def pack_weight_mxfp4_frag(w, s):
     return ow, os_
 
 
+def plan(params, tensors):
+    """xs_moe_plan: the kernels xs_moe_forward would launch for these params and
+    tensors (nothing runs; no GPU needed) as a dict: tile_rows, routed, shared
+    (names from GEMM_KINDS; shared None without a shared expert), fused_combine."""
+    out = MoePlan()
+    check(lib().xs_moe_plan(C.byref(params), C.byref(tensors), C.byref(out)))
+    kind = lambda k: None if k < 0 else GEMM_KINDS[k]  # noqa: E731
+    return {"tile_rows": out.tile_rows, "routed": kind(out.routed_gemm), "shared": kind(out.shared_gemm),
+            "fused_combine": bool(out.fused_combine)}
+
+
 class MoeLayer:
     """Holds weights (device tensors) and calls xs_moe_forward.  frag=True also
     keeps fragment-packed copies of the weights (routed and shared; MXFP4
@@ -348,6 +368,16 @@ class MoeLayer:
                        *[_ptr(f) for f in self.frag])
         check(lib().xs_moe_forward(C.byref(p), C.byref(t), _ptr(ws), ws.numel(), _stream()))
         return out
+
+    def plan(self, T, x_dtype=XS_BF16):
+        """The kernels forward() would launch for T tokens (see plan())."""
+        sh = self.shared or (None, None, None, None)
+        stand_in = C.c_void_p(256)   # x and out: checked for presence and alignment, never read
+        t = MoeTensors(stand_in, _ptr(self.router_w), _ptr(self.router_bias), _ptr(self.w13),
+                       _ptr(self.w13_scale), _ptr(self.w2), _ptr(self.w2_scale), _ptr(sh[0]),
+                       _ptr(sh[1]), _ptr(sh[2]), _ptr(sh[3]), stand_in, *([None] * 7),
+                       _ptr(self.norm_weight), None, None, None, None, *[_ptr(f) for f in self.frag])
+        return plan(self.params(T, x_dtype), t)
 
     def forward_noalloc(self, x, out):
         """The same forward through xs_moe_forward_noalloc: the library's static
