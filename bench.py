@@ -214,6 +214,14 @@ GATE_UP_KERNEL = {
 }
 
 
+def safe_plan(layer, T):
+    """layer.plan(T), or the error it raised (the measurement stands either way)."""
+    try:
+        return layer.plan(T)
+    except Exception as e:  # noqa: BLE001
+        return {"error": str(e)}
+
+
 def bench_frag():
     """XS_BENCH_FRAG: 0 (default) row-major weights; 1 also fragment-packed
     copies (the weight-direct GEMMs); only: packed copies alone."""
@@ -265,8 +273,8 @@ def prefill(a, X, torch):
         "layer_frac_fp8_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
         "layer_hbm_gbs": (wbytes + act_bytes) / (ms * 1e-3) / 1e9,
         "stage_ms": stages,
-        "plan": layer.plan(T),   # the kernels that ran (xs_moe_plan)
-        "roofline": {"kernel": GATE_UP_KERNEL.get(layer.plan(T)["routed"], layer.plan(T)["routed"]),
+        "plan": safe_plan(layer, T),   # the kernels that ran (xs_moe_plan)
+        "roofline": {"kernel": GATE_UP_KERNEL.get(safe_plan(layer, T).get("routed"), str(safe_plan(layer, T))),
                      "bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": measured_traffic(),
                      "algorithmic_bytes": gu_bytes, "launch_ms": gu_ms,
@@ -308,7 +316,7 @@ def decode(a, X, torch):
         msx, stx = time_forward(Lx, xd, max(a.steps, 50), a.warmup, profile=True)
         dec[str(Td)] = {"ms": msd, "experts_touched": ned + 1, "hbm_gbs": by / (msd * 1e-3) / 1e9,
                         "frac_hbm_peak": by / (msd * 1e-3) / 1e9 / PEAK_HBM_GBS,
-                        "tokens_per_s": Td / (msd * 1e-3), "stage_ms": st, "plan": L.plan(Td),
+                        "tokens_per_s": Td / (msd * 1e-3), "stage_ms": st, "plan": safe_plan(L, Td),
                         "router_exact": {"ms": msx, "router_logits_ms": stx["router_logits"],
                                          "extra_frac_of_layer": (msx - msd) / msd}}
     del gd
@@ -351,7 +359,7 @@ def fp4_layer(a, X, torch):
     by4 = ne4 * expert_bytes(H, I, True) + expert_bytes(H, I, False) + E * H * 2
     fl4 = layer_flops(2048, H, I, E, K_TOP)
     return {"ms": ms4, "tokens_per_s": 2048 / (ms4 * 1e-3), "tflops": fl4 / (ms4 * 1e-3) / 1e12,
-            "hbm_gbs_weights": by4 / (ms4 * 1e-3) / 1e9, "stage_ms": st4, "plan": L4.plan(2048)}
+            "hbm_gbs_weights": by4 / (ms4 * 1e-3) / 1e9, "stage_ms": st4, "plan": safe_plan(L4, 2048)}
 
 
 
