@@ -178,3 +178,18 @@ def test_kernel_plan_switches_and_refusals(monkeypatch):
     q = X.MoeParams(16, 256, 256, 8, 2, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 0, 0)
     with pytest.raises(X.XsError, match="no weight-direct GEMM"):
         X.plan(q, _stand_in_tensors(X, False, True, shared=False))
+
+
+def test_layer_plan_on_host_tensors():
+    """MoeLayer.plan passes the layer's own pointers (never dereferenced): it
+    runs on CPU tensors too."""
+    import torch
+    import xs_moe_capi as X
+    H, I, E, k = 1024, 512, 32, 4
+    u8 = lambda *s: torch.zeros(s, dtype=torch.uint8)  # noqa: E731
+    f32 = lambda *s: torch.ones(s, dtype=torch.float32)  # noqa: E731
+    layer = X.MoeLayer(torch.zeros((E, H), dtype=torch.bfloat16), u8(E, 2 * I, H), f32(E, 2 * I // 128, H // 128),
+                       u8(E, H, I), f32(E, H // 128, I // 128), k,
+                       shared=(u8(2 * I, H), f32(2 * I // 128, H // 128), u8(H, I), f32(H // 128, I // 128)))
+    assert layer.plan(1)["routed"] == "tiled" and layer.plan(1)["tile_rows"] == 16
+    assert layer.plan(4096)["routed"] == "tall" and layer.plan(4096)["shared"] == "tall"
