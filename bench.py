@@ -333,19 +333,32 @@ def single_gemm(a, X, torch):
     bq, bs = X.quant_weight_fp8_block(Wt)
     C_ = torch.empty((512, 4096), dtype=torch.bfloat16, device="cuda")
     ws = torch.empty(X.lib().xs_gemm_fp8_blockscale_workspace_size(512, 4096), dtype=torch.uint8, device="cuda")
-    for _ in range(a.warmup):
-        X.gemm_fp8_blockscale(A, bq, bs, out=C_, workspace=ws)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    n = 50
-    for _ in range(n):
-        X.gemm_fp8_blockscale(A, bq, bs, out=C_, workspace=ws)
-    e1.record()
-    torch.cuda.synchronize()
-    gms = e0.elapsed_time(e1) / n
     gfl = 2 * 512 * 4096 * 4096
-    return {"ms": gms, "tflops": gfl / (gms * 1e-3) / 1e12, "frac_fp8_peak": gfl / (gms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS}
+
+    def timed(call):
+        for _ in range(a.warmup):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        n = 50
+        for _ in range(n):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        gms = e0.elapsed_time(e1) / n
+        return {"ms": gms, "tflops": gfl / (gms * 1e-3) / 1e12,
+                "frac_fp8_peak": gfl / (gms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS}
+
+    res = timed(lambda: X.gemm_fp8_blockscale(A, bq, bs, out=C_, workspace=ws))
+    res["kernel"] = "gemm_dense_fp8_kernel (row-major B through the LDS ring)"
+    if bench_frag():
+        # XS_BENCH_FRAG=1 / only: B also packed in fragment order, the
+        # weight-direct kernel (the packing is a load-time step, outside the timing)
+        bp = X.pack_weight_fp8_frag(bq)
+        res["packed"] = timed(lambda: X.gemm_fp8_blockscale_packed(A, bp, bs, out=C_, workspace=ws))
+        res["packed"]["kernel"] = "gemm_wd_dense_kernel (packed B straight into registers)"
+    return res
 
 
 def fp4_layer(a, X, torch):

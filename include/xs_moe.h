@@ -141,12 +141,6 @@ int xs_quant_weight_fp8_block(const void *w, int dtype, int64_t batch, int64_t n
 int xs_quant_weight_mxfp4(const void *w, int dtype, int64_t batch, int64_t n, int64_t k,
                           uint8_t *q, uint8_t *s, void *stream);
 
-/* Single FP8 block-scaled GEMM: C = dequant(A) . dequant(B)^T, bf16 out.
- * Replaces gemm_launch(C, A, B, nullptr, m, k, n, transB=true, ...)
- * (xstar_cpp/include/ops/gemm.h:165-176) for FP8 operands.
- * A [M, K] bf16 activations (quantized per 1x128 inside, workspace holds them),
- * B [N, K] e4m3 with Bs [N/128, K/128] f32 block scales, C [M, N] bf16.
- * K % 128 == 0, N % 128 == 0. */
 /* Fragment-order copy of e4m3 weights for the weight-direct prefill GEMMs.
  * No counterpart in the reference (a layout of this library, made once when a
  * layer's weights are loaded).  w [batch, n, k] row-major e4m3 -> out, same
@@ -167,10 +161,29 @@ int xs_pack_weight_fp8_frag(const uint8_t *w, int64_t batch, int64_t n, int64_t 
 int xs_pack_weight_mxfp4_frag(const uint8_t *w, const uint8_t *s, int64_t batch, int64_t n, int64_t k,
                               uint8_t *out_w, uint8_t *out_s, void *stream);
 
+/* Single FP8 block-scaled GEMM: C = dequant(A) . dequant(B)^T, bf16 out.
+ * Replaces gemm_launch(C, A, B, nullptr, m, k, n, transB=true, ...)
+ * (xstar_cpp/include/ops/gemm.h:165-176) for FP8 operands.
+ * A [M, K] bf16 activations (quantized per 1x128 inside, workspace holds them),
+ * B [N, K] e4m3 with Bs [N/128, K/128] f32 block scales, C [M, N] bf16.
+ * K % 128 == 0, N % 128 == 0. */
 size_t xs_gemm_fp8_blockscale_workspace_size(int64_t M, int64_t K);
 int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int64_t M,
                            int64_t N, int64_t K, void *C, void *workspace,
                            size_t workspace_bytes, void *stream);
+
+/* The same GEMM with B given in fragment order (xs_pack_weight_fp8_frag with
+ * batch 1, n = N, k = K), loaded straight into registers by the weight-direct
+ * kernel: 64-row tiles of A x 256-column slabs of B, no K split.  Same
+ * arguments and workspace (xs_gemm_fp8_blockscale_workspace_size) as
+ * xs_gemm_fp8_blockscale otherwise; N % 256 == 0, K % 512 == 0.  No
+ * reference counterpart of its own: it stands in for the same gemm_launch
+ * call when the caller keeps a packed copy of the weights.  Results agree
+ * with xs_gemm_fp8_blockscale within f32 rounding (its K split sums the
+ * partial products in another order). */
+int xs_gemm_fp8_blockscale_packed(const void *A, const uint8_t *Bp, const float *Bs, int64_t M,
+                                  int64_t N, int64_t K, void *C, void *workspace,
+                                  size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------------
  * The whole MoE layer.  Replaces mlp(x, gate_up_weight, down_weight)

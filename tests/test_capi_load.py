@@ -193,3 +193,23 @@ def test_layer_plan_on_host_tensors():
                        shared=(u8(2 * I, H), f32(2 * I // 128, H // 128), u8(H, I), f32(H // 128, I // 128)))
     assert layer.plan(1)["routed"] == "tiled" and layer.plan(1)["tile_rows"] == 16
     assert layer.plan(4096)["routed"] == "tall" and layer.plan(4096)["shared"] == "tall"
+
+
+def test_packed_gemm_validation_without_gpu():
+    """xs_gemm_fp8_blockscale_packed refuses shapes and pointers before any
+    GPU call: N a multiple of 256, K of 512, aligned operands, a workspace."""
+    import xs_moe_capi as X
+    L = X.lib()
+    v = ctypes.c_void_p(4096)
+    ws = L.xs_gemm_fp8_blockscale_workspace_size(512, 4096)
+    rc = L.xs_gemm_fp8_blockscale_packed(v, v, v, 512, 4096, 4096, v, None, 0, None)
+    assert rc != 0 and b"workspace too small" in L.xs_last_error()
+    for N, K in ((384, 4096), (4096, 384), (4096, 1152), (128, 512)):
+        rc = L.xs_gemm_fp8_blockscale_packed(v, v, v, 512, N, K, v, v, ws, None)
+        assert rc == 1 and b"multiple of 256 and K of 512" in L.xs_last_error()
+    rc = L.xs_gemm_fp8_blockscale_packed(v, ctypes.c_void_p(4104), v, 512, 4096, 4096, v, v, ws, None)
+    assert rc == 1 and b"misaligned" in L.xs_last_error()
+    rc = L.xs_gemm_fp8_blockscale_packed(None, v, v, 512, 4096, 4096, v, v, ws, None)
+    assert rc == 1 and b"null" in L.xs_last_error()
+    # M = 0: nothing to do, nothing launched
+    assert L.xs_gemm_fp8_blockscale_packed(v, v, v, 0, 4096, 4096, v, v, ws, None) == 0

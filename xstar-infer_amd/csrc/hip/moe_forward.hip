@@ -680,4 +680,27 @@ int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int
                              cnt, st);
 }
 
+int xs_gemm_fp8_blockscale_packed(const void *A, const uint8_t *Bp, const float *Bs, int64_t M, int64_t N,
+                                  int64_t K, void *C, void *workspace, size_t workspace_bytes, void *stream)
+{
+    XS_REQUIRE(A && Bp && Bs && C, "null pointer");
+    XS_REQUIRE(((uintptr_t)A & 15) == 0 && ((uintptr_t)Bp & 15) == 0 && ((uintptr_t)C & 15) == 0 &&
+                   ((uintptr_t)Bs & 3) == 0,
+               "misaligned operand: A, Bp and C need 16-byte, Bs 4-byte alignment");
+    XS_REQUIRE(M >= 0 && M < (1 << 24) && N >= 256 && N % 256 == 0 && K >= 512 && K % 512 == 0,
+               "shape mismatch: N must be a multiple of 256 and K of 512");
+    XS_REQUIRE(M * K < ((int64_t)1 << 32) && N * K < ((int64_t)1 << 32),
+               "shape mismatch: M x K and N x K must stay below 2^32 (32-bit row offsets)");
+    size_t o_s, o_part;
+    const size_t need = gemm_ws(M, K, &o_s, &o_part);
+    if (!workspace || workspace_bytes < need)
+        return set_error(XS_ERR_WORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, need);
+    if (M == 0) return XS_OK;
+    hipStream_t st = (hipStream_t)stream;
+    char *ws = (char *)workspace;
+    int rc = launch_quant_act(A, XS_BF16, M, K, (uint8_t *)ws, ws + o_s, 0, st);
+    if (rc) return rc;
+    return launch_gemm_wd_dense((const uint8_t *)ws, (const float *)(ws + o_s), Bp, Bs, (uint16_t *)C, M, N, K, st);
+}
+
 }  // extern "C"

@@ -68,6 +68,10 @@ int launch_gemm_wide(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
 // gate_up, or down with f32 rows (a.Cf).
 int launch_gemm_wd(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st);
 int wd_tile_rows();
+// The single FP8 GEMM from fragment-packed B (moe_gemm_wd.hip): C [M, N] bf16 =
+// A . B^T, 64-row tiles x 256-column slabs.  N a multiple of 256, K of 512.
+int launch_gemm_wd_dense(const uint8_t *A, const float *As, const uint8_t *Bp, const float *Bs, uint16_t *C,
+                         int64_t M, int64_t N, int64_t K, hipStream_t st);
 bool wd_supported(int64_t H, int64_t I);   // the layer shapes the weight-direct kernels take
 // Weight-direct decode GEMMs (moe_gemm_wdd.hip): 16-row tiles (a.bm 16), the
 // same results as launch_gemm at that height, from fragment-packed weights;

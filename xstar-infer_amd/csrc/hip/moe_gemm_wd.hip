@@ -93,9 +93,13 @@ __device__ __forceinline__ void barrier_lds()
 // single path keeps the register budget of one loop.
 // KBT > 0: K / 128, known at compile time (the K loop is unrolled in full, so the
 // compiler's waits for the weight registers are exact at every step); 0: any K.
-template <bool GATEUP, int KBT>
+template <bool GATEUP, int KBT, int BM = kBM, bool DENSE = false>
 __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, int rows, int slab, uint8_t *smem)
 {
+    // sizes that follow the tile height (BM = kBM for the expert GEMMs)
+    constexpr int MI = BM / 16, AB = BM * 128, SB = BM * 4, STG = AB + SB;
+    constexpr int NA = BM / 8 / kNW, NSW = SB / 256;
+    static_assert(NA >= 1 && NSW >= 1 && NSW <= kNW && MI % 2 == 0 && kNSA * STG + 8 * 1024 <= 160 * 1024, "tile");
     const int KB = KBT ? KBT : a.K / 128;   // a multiple of kPD (checked at launch)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -112,9 +116,9 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
     };
     const uint8_t *Wexp = shared ? a.Bshp : a.Bp + (size_t)e * Nrows * a.K;
 
-    float *sB = reinterpret_cast<float *>(smem + kNSA * kStage);          // [2][KB] block scales
-    float *red = sB + 2 * KB;                                            // [kNW][kBM] epilogue amax
-    uint8_t *trash = reinterpret_cast<uint8_t *>(red + kNW * kBM);       // [256] scale DMAs of the other waves
+    float *sB = reinterpret_cast<float *>(smem + kNSA * STG);          // [2][KB] block scales
+    float *red = sB + 2 * KB;                                            // [kNW][BM] epilogue amax
+    uint8_t *trash = reinterpret_cast<uint8_t *>(red + kNW * BM);       // [256] scale DMAs of the other waves
     {
         const float *Bsf = shared ? a.Bssh : reinterpret_cast<const float *>(a.Bs) + (size_t)e * (Nrows / 128) * KB;
         for (int q = tid; q < 2 * KB; q += kNT) {
@@ -130,16 +134,16 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
         const int p = pos0 + min(row, rows - 1);
         return a.row_token ? a.row_token[p] : p;
     };
-    uint32_t oA[kNA];
+    uint32_t oA[NA];
 #pragma unroll
-    for (int u = 0; u < kNA; ++u) {
+    for (int u = 0; u < NA; ++u) {
         const int row = 8 * (wave + kNW * u) + (lane >> 3);
         oA[u] = (uint32_t)token_of(row) * (uint32_t)a.K + (uint32_t)(swz8(row, lane & 7) * 16);
     }
-    const bool sw = wave < kNSW;
+    const bool sw = wave < NSW;
     const uint32_t oS = (uint32_t)token_of(sw ? 64 * wave + lane : 0) * (uint32_t)(KB * 4);
     // an expert whose rows fit one tile reads its weights once: stream them
-    const bool stream_w = a.offsets[e + 1] - a.offsets[e] <= kBM;
+    const bool stream_w = !DENSE && a.offsets[e + 1] - a.offsets[e] <= BM;
 
     // loads of step k2 (clamped to the last step: every iteration issues the
     // same loads): activations into ring slot k2 % kNSA, the wave's two weight
@@ -150,12 +154,12 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
     const uint32_t ring = lds_addr(smem), trash_lds = lds_addr(trash);
     auto adma = [&](int k2) __attribute__((always_inline)) {
         const int kk = min(k2, KB - 1);
-        const uint32_t sl = ring + (uint32_t)((k2 % kNSA) * kStage);
+        const uint32_t sl = ring + (uint32_t)((k2 % kNSA) * STG);
 #pragma unroll
-        for (int u = 0; u < kNA; ++u) dma16(uniform(a.A + (size_t)kk * 128), oA[u], sl + 1024 * (wave + kNW * u));
+        for (int u = 0; u < NA; ++u) dma16(uniform(a.A + (size_t)kk * 128), oA[u], sl + 1024 * (wave + kNW * u));
         // every wave issues the scale DMA (the waves past the scales into the
         // trash line), so every wave's counter sees the same loads
-        dma4(uniform(Sb + (size_t)kk * 4), oS, sw ? sl + kAB + 256 * wave : trash_lds);
+        dma4(uniform(Sb + (size_t)kk * 4), oS, sw ? sl + AB + 256 * wave : trash_lds);
     };
     // each fragment is loaded straight into the 8 registers its MFMA reads
     auto wload = [&](int k2, v8i (&w)[2]) __attribute__((always_inline)) {
@@ -174,11 +178,11 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
     // loads per wave per step, in issue order: activation DMAs and the scale
     // DMA after the step's barrier, then the 4 weight loads after its last
     // MFMA (into the registers that MFMA has just read)
-    constexpr int P = kNA + 1 + 4;
+    constexpr int P = NA + 1 + 4;
 
-    v4f acc[kMI][2];
+    v4f acc[MI][2];
 #pragma unroll
-    for (int i = 0; i < kMI; ++i) acc[i][0] = acc[i][1] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < MI; ++i) acc[i][0] = acc[i][1] = v4f{0.f, 0.f, 0.f, 0.f};
     v8i wr[kPD][2];
     __syncthreads();   // sB visible; the ring is free
 #pragma unroll
@@ -189,7 +193,7 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
     const int fb0 = sbl(0), fb1 = sbl(1);   // fold factor blocks of the two tiles
     v4f q[2][2];
     float cl = 0.f, cl1 = 0.f;   // fold factors of the previous subtile (first fold: zeros)
-    q[(kMI - 1) & 1][0] = q[(kMI - 1) & 1][1] = v4f{0.f, 0.f, 0.f, 0.f};
+    q[(MI - 1) & 1][0] = q[(MI - 1) & 1][1] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k0 = 0; k0 < KB; k0 += kPD) {
 #pragma unroll
@@ -201,8 +205,8 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
             wait_vm<(kPD - 1) * P>();
             barrier_lds();   // step k's activations landed everywhere; slot (k-1) % kNSA is free
             adma(k + kPD);
-            const uint8_t *sA = smem + (k % kNSA) * kStage;
-            const float *sS = reinterpret_cast<const float *>(sA + kAB);
+            const uint8_t *sA = smem + (k % kNSA) * STG;
+            const float *sS = reinterpret_cast<const float *>(sA + AB);
             const float sb = sB[fb0 * KB + k], sb1 = sB[fb1 * KB + k];
             v8i bx[2];
             auto rb = [&](int i) __attribute__((always_inline)) {
@@ -215,15 +219,15 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
             // (i = 0: the last subtile of step k-1) while they run
             bx[0] = rb(0);
 #pragma unroll
-            for (int i = 0; i < kMI; ++i) {
-                if (i + 1 < kMI) bx[(i + 1) & 1] = rb(i + 1);
+            for (int i = 0; i < MI; ++i) {
+                if (i + 1 < MI) bx[(i + 1) & 1] = rb(i + 1);
                 const float sa = sS[16 * i + r16];
                 const float ci = sa * sb, ci1 = sa * sb1;
                 q[i & 1][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wr[p][0], bx[i & 1], v4f{0.f, 0.f, 0.f, 0.f},
                                                                                0, 0, 0, 0, 0, 0);
                 q[i & 1][1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wr[p][1], bx[i & 1], v4f{0.f, 0.f, 0.f, 0.f},
                                                                                0, 0, 0, 0, 0, 0);
-                const int fi = i == 0 ? kMI - 1 : i - 1;
+                const int fi = i == 0 ? MI - 1 : i - 1;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     acc[fi][0][e] = __builtin_fmaf(q[fi & 1][0][e], cl, acc[fi][0][e]);
@@ -240,8 +244,8 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        acc[kMI - 1][0][e] = __builtin_fmaf(q[(kMI - 1) & 1][0][e], cl, acc[kMI - 1][0][e]);
-        acc[kMI - 1][1][e] = __builtin_fmaf(q[(kMI - 1) & 1][1][e], cl1, acc[kMI - 1][1][e]);
+        acc[MI - 1][0][e] = __builtin_fmaf(q[(MI - 1) & 1][0][e], cl, acc[MI - 1][0][e]);
+        acc[MI - 1][1][e] = __builtin_fmaf(q[(MI - 1) & 1][1][e], cl1, acc[MI - 1][1][e]);
     }
     wait_vm<0>();   // the clamped loads past the last step land before the ring is reused
     __syncthreads();
@@ -252,9 +256,9 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
     // down: output column n0 + RW wave + 16 j + 4 g + v.
     if (GATEUP) {
         constexpr int JH = kWT / 2;
-        float act[kMI][JH][4];
+        float act[MI][JH][4];
 #pragma unroll
-        for (int i = 0; i < kMI; ++i) {
+        for (int i = 0; i < MI; ++i) {
             float m = 0.f;
 #pragma unroll
             for (int jj = 0; jj < JH; ++jj)
@@ -266,7 +270,7 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
                 }
             m = fmaxf(m, __shfl_xor(m, 16, WAVE));
             m = fmaxf(m, __shfl_xor(m, 32, WAVE));
-            if (g == 0) red[wave * kBM + 16 * i + r16] = m;
+            if (g == 0) red[wave * BM + 16 * i + r16] = m;
         }
         __syncthreads();
         // the FP8 tile is staged in the ring (rows padded to 144 B) and stored
@@ -276,11 +280,11 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
         float *Cs = reinterpret_cast<float *>(a.Cs);
         const int nsc = a.N / 128;
 #pragma unroll
-        for (int i = 0; i < kMI; ++i) {
+        for (int i = 0; i < MI; ++i) {
             const int row = 16 * i + r16;
             float amax = 0.f;
 #pragma unroll
-            for (int w = 0; w < kNW; ++w) amax = fmaxf(amax, red[w * kBM + row]);
+            for (int w = 0; w < kNW; ++w) amax = fmaxf(amax, red[w * BM + row]);
             const float inv = amax == 0.f ? 0.f : __fdiv_rn(448.0f, amax);
 #pragma unroll
             for (int jj = 0; jj < JH; ++jj) {
@@ -295,7 +299,7 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
         }
         __syncthreads();
 #pragma unroll
-        for (int pass = 0; pass < kBM / (kNT / 8); ++pass) {
+        for (int pass = 0; pass < BM / (kNT / 8); ++pass) {
             const int row = (kNT / 8) * pass + (tid >> 3), c = tid & 7;
             if (row < rows)
                 *reinterpret_cast<v4i *>(a.Cq + (size_t)(pos0 + row) * a.N + n0 + 16 * c) =
@@ -304,13 +308,13 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
     } else {
         // f32 rows, staged in two halves (padded to 1040 B) and stored as whole
         // 1 KB rows
-        constexpr int HR = kBM / 2, FS = 260;
-        static_assert(HR * FS * 4 <= kNSA * kStage, "staging tile");
+        constexpr int HR = BM / 2, FS = 260;
+        static_assert(HR * FS * 4 <= kNSA * STG, "staging tile");
         float *fs = reinterpret_cast<float *>(smem);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
-            for (int i = h * (kMI / 2); i < (h + 1) * (kMI / 2); ++i) {
+            for (int i = h * (MI / 2); i < (h + 1) * (MI / 2); ++i) {
                 const int rl = 16 * i + r16 - h * HR;
 #pragma unroll
                 for (int j = 0; j < kWT; ++j) *reinterpret_cast<v4f *>(fs + rl * FS + RW * wave + 16 * j + 4 * g) = acc[i][j];
@@ -319,9 +323,16 @@ __device__ __forceinline__ void run_tile_wd(const GemmArgs &a, int e, int pos0, 
 #pragma unroll 4
             for (int pass = 0; pass < HR / (kNT / 64); ++pass) {
                 const int rl = (kNT / 64) * pass + (tid >> 6), c = 4 * (tid & 63), row = h * HR + rl;
-                if (row < rows)
-                    *reinterpret_cast<v4f *>(a.Cf + (size_t)(pos0 + row) * a.ldc + n0 + c) =
-                        *reinterpret_cast<const v4f *>(fs + rl * FS + c);
+                if (row < rows) {
+                    const v4f v = *reinterpret_cast<const v4f *>(fs + rl * FS + c);
+                    if (DENSE) {   // the single GEMM: bf16 output, one rounding
+                        const uint32_t lo = bf16_from_f32(v[0]) | ((uint32_t)bf16_from_f32(v[1]) << 16);
+                        const uint32_t hi = bf16_from_f32(v[2]) | ((uint32_t)bf16_from_f32(v[3]) << 16);
+                        *reinterpret_cast<v2i *>(a.Cy + (size_t)(pos0 + row) * a.ldc + n0 + c) = v2i{(int)lo, (int)hi};
+                    } else {
+                        *reinterpret_cast<v4f *>(a.Cf + (size_t)(pos0 + row) * a.ldc + n0 + c) = v;
+                    }
+                }
             }
             __syncthreads();
         }
@@ -348,6 +359,30 @@ __global__ __launch_bounds__(kNT) void moe_gemm_wd_kernel(GemmArgs a)
                                         (int)min((int64_t)kBM, a.sh_rows - (int64_t)kBM * tile), 0}
                                  : tab[1 + tile];
     run_tile_wd<GATEUP, KBT>(a, d.x, d.y, min(d.z, kBM), slab, smem);
+}
+
+// The single FP8 block-scaled GEMM C = A . B^T (bf16 C) from fragment-packed
+// B: 64-row tiles of A x 256-column slabs of B, no K split (at 512 x 4096 x
+// 4096 that is 128 blocks of 32 K steps, each at its CU's full MFMA rate,
+// with no partial tiles to exchange).  B is the "shared expert" of the tile
+// routine (e == a.E): a.Bshp packed weights, a.Bssh their block scales.
+// Blocks go to the XCDs in contiguous ranges of (slab, tile) order, tiles
+// fastest, so one XCD runs a few B slabs against every A tile and reads each
+// slab once.
+constexpr int kDenseBM = 64;
+
+template <int KBT>
+__global__ __launch_bounds__(kNT) void gemm_wd_dense_kernel(GemmArgs a)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int TM = (int)((a.sh_rows + kDenseBM - 1) / kDenseBM), gx = a.N / 256;
+    const int total = TM * gx, per = (total + 7) / 8;
+    const int L = (int)blockIdx.x;
+    const int v = (L & 7) * per + (L >> 3);
+    if (v >= total) return;
+    const int slab = v / TM, tile = v - slab * TM;
+    const int rows = (int)min((int64_t)kDenseBM, a.sh_rows - (int64_t)kDenseBM * tile);
+    run_tile_wd<false, KBT, kDenseBM, true>(a, a.E, kDenseBM * tile, rows, slab, smem);
 }
 
 }  // namespace
@@ -390,6 +425,48 @@ int launch_gemm_wd(const GemmArgs &a, bool gateup, int grid_y, hipStream_t st)
     }
     const int64_t groups = (grid_y + 7) / 8 * (gx / 4);   // 8-tile x 4-slab groups
     fn<<<dim3((unsigned)((groups + 7) / 8 * 256)), dim3(kNT), smem, st>>>(a);
+    XS_LAUNCH_CHECK();
+    return XS_OK;
+}
+
+// C [M, N] bf16 = A . B^T: A [M, K] e4m3 with row scales [M, K/128], B packed
+// in fragment order ([N/16][K/128][2][64][16 B]) with block scales
+// [N/128][K/128].  N a multiple of 256, K of 512.
+int launch_gemm_wd_dense(const uint8_t *A, const float *As, const uint8_t *Bp, const float *Bs, uint16_t *C,
+                         int64_t M, int64_t N, int64_t K, hipStream_t st)
+{
+    if (M == 0) return XS_OK;
+    if (N % 256 || K % (128 * kPD) || N <= 0 || K <= 0)
+        return set_error(XS_ERR_UNSUPPORTED, "packed FP8 GEMM shape N=%lld K=%lld (N a multiple of 256, K of %d)",
+                         (long long)N, (long long)K, 128 * kPD);
+    const int64_t total = (M + kDenseBM - 1) / kDenseBM * (N / 256);
+    if (total >= (1ll << 28)) return set_error(XS_ERR_UNSUPPORTED, "packed FP8 GEMM too large");
+    GemmArgs a = {};
+    a.A = A;
+    a.As = As;
+    a.Bshp = Bp;
+    a.Bssh = Bs;
+    a.E = 0;
+    a.K = (int)K;
+    a.N = (int)N;
+    a.bm = kDenseBM;
+    a.Cy = C;
+    a.ldc = N;
+    a.sh_rows = M;
+    constexpr size_t stage = (size_t)kDenseBM * 128 + kDenseBM * 4;
+    const size_t smem = (size_t)kNSA * stage + 8 * (size_t)(K / 128) + 4 * kNW * kDenseBM + 256;
+    if (smem > 160 * 1024) return set_error(XS_ERR_UNSUPPORTED, "K=%lld needs %zu bytes of LDS", (long long)K, smem);
+    const int KB = (int)(K / 128);
+    const int ki = KB == 4 ? 1 : KB == 8 ? 2 : KB == 16 ? 3 : KB == 32 ? 4 : 0;
+    void (*const fns[5])(GemmArgs) = {gemm_wd_dense_kernel<0>, gemm_wd_dense_kernel<4>, gemm_wd_dense_kernel<8>,
+                                      gemm_wd_dense_kernel<16>, gemm_wd_dense_kernel<32>};
+    static bool attr_set[5] = {};
+    if (!attr_set[ki]) {
+        XS_HIP(hipFuncSetAttribute((const void *)fns[ki], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        attr_set[ki] = true;
+    }
+    const int64_t per = (total + 7) / 8;
+    fns[ki]<<<dim3((unsigned)(8 * per)), dim3(kNT), smem, st>>>(a);
     XS_LAUNCH_CHECK();
     return XS_OK;
 }

@@ -68,6 +68,7 @@ EXPORTS = {
     "xs_pack_weight_mxfp4_frag": (C.c_int, [P, P, I64, I64, I64, P, P, P]),
     "xs_gemm_fp8_blockscale_workspace_size": (C.c_size_t, [I64, I64]),
     "xs_gemm_fp8_blockscale": (C.c_int, [P, P, P, I64, I64, I64, P, P, C.c_size_t, P]),
+    "xs_gemm_fp8_blockscale_packed": (C.c_int, [P, P, P, I64, I64, I64, P, P, C.c_size_t, P]),
     "xs_moe_workspace_size": (C.c_size_t, [P]),
     "xs_moe_plan": (C.c_int, [P, P, P]),
     "xs_moe_forward": (C.c_int, [P, P, P, C.c_size_t, P]),
@@ -247,6 +248,21 @@ def gemm_fp8_blockscale(a, bq, bs, out=None, workspace=None):
         workspace = torch.empty(nb, dtype=torch.uint8, device=a.device)
     check(lib().xs_gemm_fp8_blockscale(_ptr(a), _ptr(_u8(bq)), _ptr(bs), M, N, K, _ptr(out),
                                        _ptr(workspace), workspace.numel(), _stream()))
+    return out
+
+
+def gemm_fp8_blockscale_packed(a, bp, bs, out=None, workspace=None):
+    """xs_gemm_fp8_blockscale_packed: bp is pack_weight_fp8_frag(B) of B [N, K]."""
+    import torch
+    M, K = a.shape
+    N = bp.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    nb = lib().xs_gemm_fp8_blockscale_workspace_size(M, K)
+    if workspace is None:
+        workspace = torch.empty(nb, dtype=torch.uint8, device=a.device)
+    check(lib().xs_gemm_fp8_blockscale_packed(_ptr(a), _ptr(_u8(bp)), _ptr(bs), M, N, K, _ptr(out),
+                                              _ptr(workspace), workspace.numel(), _stream()))
     return out
 
 
