@@ -1,6 +1,8 @@
 // moe_gemm_wd.hip -- grouped FP8 block-scaled expert GEMMs with the weights
 // loaded straight into VGPRs (gfx950): the prefill tall-tile path when the
-// layer holds a fragment-packed copy of its FP8 weights.
+// layer holds a fragment-packed copy of its FP8 weights.  The same tile
+// routine, at 64-row tiles with a bf16 output, is the single FP8 GEMM from a
+// packed B (gemm_wd_dense_kernel, xs_gemm_fp8_blockscale_packed).
 //
 // Nearest reference code: gemm_silu_and_mul_kernel (xstar_cpp/src/ops/mlp.cu:52-200)
 // and gemm_kernel (xstar_cpp/src/ops/gemm.cu:41-210).  Numerics are those of the
