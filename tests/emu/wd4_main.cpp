@@ -172,20 +172,27 @@ int main(int argc, char **argv)
     if (g_math) {
         double maxerr = 0, maxref = 0;
         long viol = 0;
-        std::vector<double> act(I);
+        std::vector<double> act(I), acc_slack(I);
         for (int p = 0; p < S; ++p) {
             const int e = (int)(std::upper_bound(offsets, offsets + E + 1, p) - offsets - 1);
             const int tok = row_token[p];
             for (int n = 0; n < I; ++n) {
-                double gs = 0, us = 0;
+                double gs = 0, us = 0, ga = 0, ua = 0;
                 const uint8_t *gr = w13 + ((size_t)e * 2 * I + n) * (H / 2), *ur = w13 + ((size_t)e * 2 * I + I + n) * (H / 2);
                 const uint8_t *gsr = s13 + ((size_t)e * 2 * I + n) * (H / 32), *usr = s13 + ((size_t)e * 2 * I + I + n) * (H / 32);
                 for (int kk = 0; kk < H; ++kk) {
                     const double x = e4m3_dec(xq[(size_t)tok * H + kk]) * e8(xs_[(size_t)tok * (H / 32) + kk / 32]);
                     gs += x * fp4_at(gr, kk) * e8(gsr[kk / 32]);
                     us += x * fp4_at(ur, kk) * e8(usr[kk / 32]);
+                    ga += std::fabs(x * fp4_at(gr, kk) * e8(gsr[kk / 32]));
+                    ua += std::fabs(x * fp4_at(ur, kk) * e8(usr[kk / 32]));
                 }
                 act[n] = gs / (1 + std::exp(-gs)) * us;
+                // the kernel's f32 sums of H products are off by up to about
+                // 16 f32 ulps of the sum of |products|, which moves SwiGLU by
+                // |silu'(g) u| dg + |silu(g)| du
+                const double sg = 1 / (1 + std::exp(-gs));
+                acc_slack[n] = 1e-6 * (std::fabs(sg * (1 + gs * (1 - sg)) * us) * ga + std::fabs(gs * sg) * ua);
             }
             for (int n = 0; n < I; ++n) {
                 const uint8_t sc = acts[(size_t)p * (I / 32) + n / 32];
@@ -195,9 +202,11 @@ int main(int argc, char **argv)
                 maxref = std::max(maxref, a);
                 // given the block's scale 2^se: the clamp at 448 2^se, else half
                 // an e4m3 step (2^-4 relative; 2^-10 2^se below the normals), plus
-                // the f32 accumulation's rounding
-                const double lim = std::max({a - 448 * e8(sc), a / 16, e8(sc) / 1024}) + 1e-5 * a + 1e-30;
-                if (err > lim) ++viol;
+                // the f32 accumulation's rounding (a value within that of a
+                // rounding tie may land on either side of it)
+                const double lim = std::max({a - 448 * e8(sc), a / 16, e8(sc) / 1024}) + acc_slack[n] + 1e-30;
+                if (err > lim && ++viol <= 4)
+                    printf("  act[%d][%d]: ref %.9g got %.9g err %.4g lim %.4g scale 2^%d\n", p, n, act[n], got, err, lim, (int)sc - 127);
             }
         }
         printf("gate_up act: max abs err %.4g, max |ref| %.4g, rel %.4g, outside the MXFP8 bound %ld\n", maxerr, maxref,
