@@ -13,7 +13,8 @@ disassembly (AMD's own llvm-objdump over code objects built here):
           a `v_readfirstlane`/`v_readlane` wrote it;
   vmem    a VGPR read or written while a VMEM load into it is still
           outstanding (no `s_waitcnt vmcnt` has retired it): the load would
-          land late, over a register already reused.
+          land late, over a register already reused.  A later VMEM load into
+          the same register is allowed: loads return in issue order.
 
 Each basic block is scanned in straight-line order; the vmcnt model retires
 all but the N most recent VMEM operations at `s_waitcnt vmcnt(N)` (on gfx9
@@ -121,7 +122,12 @@ def scan(text):
                 pending = pending[len(pending) - n:] if n else []
             continue
         busy = set().union(*pending) if pending else set()
-        touched = set().union(*(_vregs(t) for t in toks)) if toks else set()
+        vm_load = op.startswith(("global_load", "buffer_load", "scratch_load")) and not _is_lds_dma(op, s)
+        # a VMEM load may name a register that an earlier load still targets:
+        # loads return in issue order, so the later one lands last (its
+        # address operands are still checked)
+        toks_chk = toks[1:] if vm_load else toks
+        touched = set().union(*(_vregs(t) for t in toks_chk)) if toks_chk else set()
         if busy & touched:
             found.append(("vmem", ln, s, f"v{min(busy & touched)} has a load in flight"))
         if vmem:

@@ -46,6 +46,10 @@ def test_scanner_flags_planted_hazards():
     assert [f[0] for f in scan(late)] == ["vmem"]
     waited = "\tglobal_load_dwordx4 v[8:11], v[2:3], off\n\ts_waitcnt vmcnt(0)\n\tv_mov_b32_e32 v9, 0\n"
     assert scan(waited) == []
+    # a second load into the same register lands after the first (in-order return)
+    assert scan("\tglobal_load_dword v8, v[2:3], off\n\tglobal_load_dword v8, v[4:5], off\n") == []
+    # but a load whose address register is still being loaded into is flagged
+    assert [f[0] for f in scan("\tglobal_load_dwordx2 v[2:3], v[4:5], off\n\tglobal_load_dword v8, v[2:3], off\n")] == ["vmem"]
     # vmcnt(1) retires the older of two loads only
     two = ("\tglobal_load_dwordx4 v[8:11], v[2:3], off\n\tglobal_load_dwordx4 v[12:15], v[2:3], off\n"
            "\ts_waitcnt vmcnt(1)\n\tv_add_f32_e32 v8, v8, v8\n\tv_add_f32_e32 v12, v12, v12\n")
