@@ -52,6 +52,17 @@ def _scratch_users(remarks: str):
     return bad
 
 
+def _hazards(so_path):
+    """isa_scan over every code object of the library (empty: none found)."""
+    import tempfile
+
+    sys.path.insert(0, HERE)
+    from isa_scan import code_objects, disassemble, scan
+
+    with tempfile.TemporaryDirectory() as d:
+        return [f for co in code_objects(so_path, d) for f in scan(disassemble(co))]
+
+
 def build_hip() -> str:
     os.makedirs(OUT, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(HERE, "csrc", "hip", "*.hip")))
@@ -69,6 +80,11 @@ def build_hip() -> str:
     if bad:
         os.remove(tmp)
         raise RuntimeError("kernels spill to scratch: " + ", ".join(f"{n} ({b} B/lane)" for n, b in bad))
+    # the asm-level wait-state and in-flight-register checks over the machine code
+    found = _hazards(tmp)
+    if found:
+        os.remove(tmp)
+        raise RuntimeError("machine-code hazards: " + "; ".join(map(str, found[:10])))
     os.replace(tmp, out)
     return out
 

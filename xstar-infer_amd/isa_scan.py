@@ -1,4 +1,5 @@
-"""Static checks over the gfx950 machine code of the built libxs_moe.so.
+"""Static checks over the gfx950 machine code of the built libxs_moe.so
+(run by build.py on every build, and by tests/test_isa_hazards.py).
 
 The GEMM kernels issue their LDS DMAs from inline asm, where the compiler's
 hazard recognizer does not look, and the dense kernel loads split-K partials
