@@ -226,6 +226,8 @@ def bench_frag():
     """XS_BENCH_FRAG: 0 (default) row-major weights; 1 also fragment-packed
     copies (the weight-direct GEMMs); only: packed copies alone."""
     v = os.environ.get("XS_BENCH_FRAG", "0")
+    if v != "0":
+        os.environ["XS_WEIGHT_DIRECT"] = "1"   # the weight-direct GEMMs are opt-in
     return "only" if v == "only" else v == "1"
 
 

@@ -180,7 +180,8 @@ int xs_gemm_fp8_blockscale(const void *A, const uint8_t *B, const float *Bs, int
  * reference counterpart of its own: it stands in for the same gemm_launch
  * call when the caller keeps a packed copy of the weights.  Results agree
  * with xs_gemm_fp8_blockscale within f32 rounding (its K split sums the
- * partial products in another order). */
+ * partial products in another order).  Opt-in: without XS_WEIGHT_DIRECT=1
+ * in the environment it returns XS_ERR_UNSUPPORTED. */
 int xs_gemm_fp8_blockscale_packed(const void *A, const uint8_t *Bp, const float *Bs, int64_t M,
                                   int64_t N, int64_t K, void *C, void *workspace,
                                   size_t workspace_bytes, void *stream);
@@ -256,7 +257,11 @@ typedef struct {
      * Packed-only layer: w13 and w2 (and shared_w13 / shared_w2) NULL, the
      * packed copies given; the block scales (FP8) stay required.  Every GEMM
      * is then a weight-direct one, and a shape they do not take (K a multiple
-     * of 512, N of 512) is refused with XS_ERR_UNSUPPORTED. */
+     * of 512, N of 512) is refused with XS_ERR_UNSUPPORTED.
+     * The weight-direct GEMMs are opt-in: they run only when the environment
+     * sets XS_WEIGHT_DIRECT=1 (read per call).  Otherwise the packed copies
+     * are ignored when the row-major weights are given, and a packed-only
+     * layer is refused with XS_ERR_UNSUPPORTED. */
     const void *w13_frag;
     const void *w2_frag;
     const void *shared_w13_frag;
@@ -306,9 +311,13 @@ int xs_moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *worksp
  * for callers that cannot allocate device memory -- code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation.  The layer's
  * scratch lives in a static device array of XS_NOALLOC_SCRATCH_BYTES per GPU
- * (held until the process ends); params whose workspace
- * (xs_moe_workspace_size) exceeds it are rejected with XS_ERR_WORKSPACE (V4-Flash
- * shape: FP8 up to 256 tokens, MXFP4 up to about 200).  Calls nothing that
+ * (held until the process ends, by every process that loads this library,
+ * whether or not it calls this entry); params whose workspace
+ * (xs_moe_workspace_size) exceeds it are rejected with XS_ERR_WORKSPACE.
+ * Callers compare xs_moe_workspace_size(p) with xs_moe_noalloc_scratch_bytes():
+ * the size is not monotonic in T (tile and stream-K regions change with the
+ * kernels chosen), so no token count is a bound.  Examples at the V4-Flash
+ * shape: FP8 T = 256 needs 50.7 MiB, MXFP4 T = 210 about 61 MiB.  Calls nothing that
  * allocates.  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (different streams, or threads) race; calls in one
  * stream order are safe, because each forward re-arms what must start at zero.

@@ -149,8 +149,10 @@ def test_kernel_plan_without_gpu(T, fmt, row_major, frag, want, monkeypatch):
     """The forward's dispatch (xs_moe_plan, the same decision the forward
     takes): tile height and kernel family per batch size and weight form."""
     import xs_moe_capi as X
-    for n in ("XS_MOE_STREAM", "XS_WIDE_DIRECT", "XS_DECODE_DIRECT", "XS_FP4_DIRECT", "XS_FUSE_COMBINE"):
+    for n in ("XS_MOE_STREAM", "XS_WIDE_DIRECT", "XS_DECODE_DIRECT", "XS_FP4_DIRECT", "XS_FUSE_COMBINE",
+              "XS_MOE_GEMM"):
         monkeypatch.delenv(n, raising=False)
+    monkeypatch.setenv("XS_WEIGHT_DIRECT", "1")
     f = X.XS_FP4_E2M1X2 if fmt == "fp4" else X.XS_FP8_E4M3
     p = X.MoeParams(T, 4096, 2048, 256, 6, 1, 1, 1, 1.0, X.XS_BF16, f, 1, 0)
     got = X.plan(p, _stand_in_tensors(X, row_major, frag, fmt == "fp4"))
@@ -162,8 +164,45 @@ def test_kernel_plan_without_gpu(T, fmt, row_major, frag, want, monkeypatch):
     assert not got["fused_combine"]
 
 
+def test_weight_direct_is_opt_in(monkeypatch):
+    """Without XS_WEIGHT_DIRECT=1 the packed copies are ignored, and packed-only
+    layers and the packed single GEMM are refused."""
+    import xs_moe_capi as X
+    for n in ("XS_WEIGHT_DIRECT", "XS_MOE_STREAM", "XS_MOE_GEMM", "XS_DECODE_DIRECT"):
+        monkeypatch.delenv(n, raising=False)
+    p = X.MoeParams(16, 4096, 2048, 256, 6, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 1, 0)
+    assert X.plan(p, _stand_in_tensors(X, True, True))["routed"] == "stream"
+    p.T = 8192
+    assert X.plan(p, _stand_in_tensors(X, True, True))["routed"] == "tall"
+    with pytest.raises(X.XsError, match="weight-direct GEMMs are off"):
+        X.plan(p, _stand_in_tensors(X, False, True))
+    L = X.lib()
+    v = ctypes.c_void_p(4096)
+    ws = L.xs_gemm_fp8_blockscale_workspace_size(512, 4096)
+    assert L.xs_gemm_fp8_blockscale_packed(v, v, v, 512, 4096, 4096, v, v, ws, None) == 3   # XS_ERR_UNSUPPORTED
+    assert b"weight-direct GEMMs are off" in L.xs_last_error()
+    monkeypatch.setenv("XS_WEIGHT_DIRECT", "0")
+    assert X.plan(p, _stand_in_tensors(X, True, True))["routed"] == "tall"
+
+
+def test_wide_switch_is_read_per_call(monkeypatch):
+    """XS_MOE_GEMM is read on every call: a test that forces a family gets it
+    even after an earlier call planned without it."""
+    import xs_moe_capi as X
+    monkeypatch.delenv("XS_MOE_GEMM", raising=False)
+    monkeypatch.setenv("XS_MOE_STREAM", "0")
+    p = X.MoeParams(64, 256, 128, 8, 2, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 1, 0)
+    assert X.plan(p, _stand_in_tensors(X))["routed"] == "tiled"
+    monkeypatch.setenv("XS_MOE_GEMM", "wide")
+    assert X.plan(p, _stand_in_tensors(X))["routed"] == "tall"
+    monkeypatch.setenv("XS_MOE_GEMM", "tiled")
+    p.T = 8192
+    assert X.plan(p, _stand_in_tensors(X))["routed"] == "tiled"
+
+
 def test_kernel_plan_switches_and_refusals(monkeypatch):
     import xs_moe_capi as X
+    monkeypatch.setenv("XS_WEIGHT_DIRECT", "1")
     p = X.MoeParams(16, 4096, 2048, 256, 6, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 1, 0)
     monkeypatch.setenv("XS_DECODE_DIRECT", "0")
     assert X.plan(p, _stand_in_tensors(X, True, True))["routed"] == "stream"
@@ -195,10 +234,11 @@ def test_layer_plan_on_host_tensors():
     assert layer.plan(4096)["routed"] == "tall" and layer.plan(4096)["shared"] == "tall"
 
 
-def test_packed_gemm_validation_without_gpu():
+def test_packed_gemm_validation_without_gpu(monkeypatch):
     """xs_gemm_fp8_blockscale_packed refuses shapes and pointers before any
     GPU call: N a multiple of 256, K of 512, aligned operands, a workspace."""
     import xs_moe_capi as X
+    monkeypatch.setenv("XS_WEIGHT_DIRECT", "1")
     L = X.lib()
     v = ctypes.c_void_p(4096)
     ws = L.xs_gemm_fp8_blockscale_workspace_size(512, 4096)

@@ -135,6 +135,8 @@ def test_moe_c1_tiny_f32(gemm, monkeypatch):
         monkeypatch.setenv("XS_MOE_GEMM", "wide")
     c = make_case(64, 256, 128, 8, 2, seed=11, x_std=0.02, bf16=False, bias_std=0)
     g = to_device(c)
+    if gemm == "wide":
+        assert layer_for(c, g, router_exact=True).plan(64)["routed"] == "tall"
     _run_and_check(c, g, router_exact=True)
     T, E, k, I, H = 64, 8, 2, 128, 256
     R = T * k + T
@@ -156,6 +158,8 @@ def test_moe_f32_stages_bf16_wide(fuse, monkeypatch):
     monkeypatch.setenv("XS_FUSE_COMBINE", fuse)
     c = make_case(300, 256, 256, 4, 2, seed=12, zipf=1.1)
     g = to_device(c)
+    want = {"routed": "tall", "fused_combine": fuse == "1"}
+    assert {n: layer_for(c, g, router_exact=True).plan(300)[n] for n in want} == want
     T, E, k, I, H = 300, 4, 2, 256, 256
     R = T * k + T
     dbg = _debug(T, E, k)
@@ -247,6 +251,7 @@ def test_moe_fused_combine_matches_separate(bf16, monkeypatch):
     outs = {}
     for fuse in ("1", "0"):
         monkeypatch.setenv("XS_FUSE_COMBINE", fuse)
+        assert layer.plan(700)["fused_combine"] == (fuse == "1")
         a = layer.forward(g["x"])
         b = layer.forward(g["x"])
         r = layer.forward(g["x"], residual=res)

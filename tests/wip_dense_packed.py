@@ -15,6 +15,11 @@ torch = pytest.importorskip("torch")
 def _gpu():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
+    # the weight-direct GEMMs are opt-in; these tests are theirs
+    mp = pytest.MonkeyPatch()
+    mp.setenv("XS_WEIGHT_DIRECT", "1")
+    yield
+    mp.undo()
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (1, 256, 512), (100, 512, 1024), (130, 768, 1536),

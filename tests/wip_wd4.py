@@ -15,6 +15,11 @@ pytestmark = pytest.mark.gpu
 def _gpu():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
+    # the weight-direct GEMMs are opt-in; these tests are theirs
+    mp = pytest.MonkeyPatch()
+    mp.setenv("XS_WEIGHT_DIRECT", "1")
+    yield
+    mp.undo()
 
 
 def test_pack_weight_mxfp4_frag():

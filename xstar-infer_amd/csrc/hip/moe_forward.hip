@@ -53,11 +53,12 @@ static int pick_bm(double rows_per_tile_group)
 }
 
 // GEMM family for the FP8 layer: the tall-tile kernels (moe_gemm_wide.hip) once
-// experts average 32+ rows, else the 16..128-row tiles.  XS_MOE_GEMM=wide|tiled overrides (benchmarks, tests).
+// experts average 32+ rows, else the 16..128-row tiles.  XS_MOE_GEMM=wide|tiled
+// overrides (benchmarks, tests); read per call, since tests switch it.
 static bool use_wide(const xs_moe_params *p)
 {
     if (p->routed_format != XS_FP8_E4M3) return false;
-    static const char *force = getenv("XS_MOE_GEMM");
+    const char *force = getenv("XS_MOE_GEMM");
     if (force && !strcmp(force, "wide")) return true;
     if (force && !strcmp(force, "tiled")) return false;
     return p->T * p->top_k >= 32 * p->E;
@@ -77,6 +78,13 @@ static bool getenv_flag(const char *name, bool dflt)
 // (moe_gemm_wide.hip, store_f32_tile) instead of the separate combine launch.
 // Same bits; measured slower at prefill (the block that completes a token
 // holds its CU through the gather), so it is off by default.
+// The weight-direct GEMMs (moe_gemm_wd.hip, moe_gemm_wdd.hip, moe_gemm_wd4.hip
+// and the packed single GEMM) run only when XS_WEIGHT_DIRECT=1: they have not
+// yet passed a run on the card.  Off, a layer that also gives its row-major
+// weights ignores the packed copies, and a packed-only layer or a packed GEMM
+// is refused with XS_ERR_UNSUPPORTED.
+static bool weight_direct_enabled() { return getenv_flag("XS_WEIGHT_DIRECT", false); }
+
 static bool fuse_combine(const xs_moe_params *p)
 {
     return use_wide(p) && getenv_flag("XS_FUSE_COMBINE", false);
@@ -203,6 +211,9 @@ static int make_plan(const xs_moe_params *p, const xs_moe_tensors *t, Plan &pl)
     const bool frag4 = fp4 && t->w13_frag && t->w2_frag && t->w13_scale_frag && t->w2_scale_frag;
     int bm = pick_bm((double)S / (double)E);
     bool direct, ddirect, direct4;
+    if (packed_only && !weight_direct_enabled())
+        return set_error(XS_ERR_UNSUPPORTED,
+                         "packed-only layer: the weight-direct GEMMs are off (XS_WEIGHT_DIRECT=1 enables them)");
     if (packed_only) {
         if (fp4 && bm < 64) bm = 64;
         ddirect = !fp4 && bm == 16 && wdd_supported(H, I);
@@ -212,9 +223,10 @@ static int make_plan(const xs_moe_params *p, const xs_moe_tensors *t, Plan &pl)
             return set_error(XS_ERR_UNSUPPORTED, "packed-only layer: no weight-direct GEMM for H=%lld I=%lld",
                              (long long)H, (long long)I);
     } else {
-        direct = wide && !fused && frag8 && wd_supported(H, I) && getenv_flag("XS_WIDE_DIRECT", true);
-        ddirect = !wide && frag8 && bm == 16 && wdd_supported(H, I) && getenv_flag("XS_DECODE_DIRECT", true);
-        direct4 = frag4 && (bm == 64 || bm == 128) && wd4_supported(H, I) && getenv_flag("XS_FP4_DIRECT", true);
+        const bool wd_on = weight_direct_enabled();
+        direct = wd_on && wide && !fused && frag8 && wd_supported(H, I) && getenv_flag("XS_WIDE_DIRECT", true);
+        ddirect = wd_on && !wide && frag8 && bm == 16 && wdd_supported(H, I) && getenv_flag("XS_DECODE_DIRECT", true);
+        direct4 = wd_on && frag4 && (bm == 64 || bm == 128) && wd4_supported(H, I) && getenv_flag("XS_FP4_DIRECT", true);
     }
     const bool sdirect = direct4 && shared_rows && t->shared_w13_frag && t->shared_w2_frag && wd_supported(H, I);
     if (packed_only && fp4 && shared_rows && !sdirect)
@@ -695,6 +707,8 @@ int xs_gemm_fp8_blockscale_packed(const void *A, const uint8_t *Bp, const float 
     const size_t need = gemm_ws(M, K, &o_s, &o_part);
     if (!workspace || workspace_bytes < need)
         return set_error(XS_ERR_WORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, need);
+    if (!xs::weight_direct_enabled())
+        return set_error(XS_ERR_UNSUPPORTED, "packed GEMM: the weight-direct GEMMs are off (XS_WEIGHT_DIRECT=1 enables them)");
     if (M == 0) return XS_OK;
     hipStream_t st = (hipStream_t)stream;
     char *ws = (char *)workspace;

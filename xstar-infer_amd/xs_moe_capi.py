@@ -308,7 +308,9 @@ class MoeLayer:
     the GEMMs load straight into registers (same results).  frag="only" keeps
     the packed copies alone (the row-major expert weights are dropped, so the
     layer takes no more memory than before), and every GEMM is a weight-direct
-    one."""
+    one.  The weight-direct GEMMs are opt-in (XS_WEIGHT_DIRECT=1 in the
+    environment): without it the packed copies go unused, and a frag="only"
+    layer's forward raises XsError (unsupported)."""
 
     def __init__(self, router_w, w13, w13_scale, w2, w2_scale, top_k, router_bias=None,
                  shared=None, routed_format=XS_FP8_E4M3, n_group=1, topk_group=1,
