@@ -54,3 +54,32 @@ def test_scanner_flags_planted_hazards():
     two = ("\tglobal_load_dwordx4 v[8:11], v[2:3], off\n\tglobal_load_dwordx4 v[12:15], v[2:3], off\n"
            "\ts_waitcnt vmcnt(1)\n\tv_add_f32_e32 v8, v8, v8\n\tv_add_f32_e32 v12, v12, v12\n")
     assert [(f[0], f[2].split()[1]) for f in scan(two)] == [("vmem", "v12,")]
+
+
+def test_scanner_follows_branches_and_back_edges():
+    """A load in flight is followed over the control-flow graph: into a branch
+    target, and around a loop's back edge into the next iteration."""
+    branch = ("\tglobal_load_dwordx4 v[8:11], v[2:3], off\n\ts_cbranch_scc1 L1\n"
+              "\ts_waitcnt vmcnt(0)\n\ts_branch L2\n"
+              "L1:\n\tv_add_f32_e32 v9, v9, v9\n"
+              "L2:\n\ts_endpgm\n")
+    assert [(f[0], f[2].split()[0]) for f in scan(branch)] == [("vmem", "v_add_f32_e32")]
+    # both paths wait before the join: nothing in flight there
+    joined = branch.replace("L1:\n\tv_add", "L1:\n\ts_waitcnt vmcnt(0)\n\tv_add")
+    assert scan(joined) == []
+    # the load of one iteration is still in flight at the top of the next
+    loop = ("L0:\n\tv_mov_b32_e32 v12, 0\n\tglobal_load_dword v12, v[2:3], off\n"
+            "\ts_cbranch_scc1 L0\n\ts_waitcnt vmcnt(0)\n\ts_endpgm\n")
+    assert [f[0] for f in scan(loop)] == ["vmem"]
+    assert scan(loop.replace("\ts_cbranch_scc1 L0\n", "\ts_waitcnt vmcnt(0)\n\ts_cbranch_scc1 L0\n")) == []
+    # the paths are aligned from the newest load: vmcnt(1) on the join retires
+    # the older load of the longer path only
+    two = ("\tglobal_load_dword v8, v[2:3], off\n\ts_cbranch_scc1 L1\n"
+           "\tglobal_load_dword v9, v[2:3], off\n"
+           "L1:\n\ts_waitcnt vmcnt(1)\n\tv_mov_b32_e32 v8, 0\n\tv_mov_b32_e32 v9, 0\n")
+    assert [(f[0], f[2].split()[1]) for f in scan(two)] == [("vmem", "v8,"), ("vmem", "v9,")]
+    # an M0 write at the end of the fall-through predecessor counts for a DMA
+    # at a branch target
+    m0 = "\ts_cbranch_scc1 L1\n\ts_mov_b32 m0, s4\nL1:\n\tglobal_load_lds_dwordx4 v1, s[2:3]\n"
+    assert [f[0] for f in scan(m0)] == ["m0"]
+    assert scan(m0.replace("s4\n", "s4\n\ts_nop 0\n")) == []

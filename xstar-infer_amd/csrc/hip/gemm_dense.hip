@@ -94,17 +94,20 @@ __device__ __forceinline__ void wait_vm()
 // 16-byte store and load with the sc1 cache policy, the one agent-scope
 // atomics carry: the store writes through this XCD's L2 and the load misses
 // in the reader's, so partial tiles pass between XCDs without a cache-wide
-// write-back or invalidation.  The load's destination is valid after
-// s_waitcnt vmcnt.
+// write-back or invalidation.  The load is the compiler's own buffer load
+// (cache-policy operand 16 = sc1), so the compiler tracks its destination
+// registers and places the vmcnt wait before their first use.  The resource
+// is raw (stride 0): num_records bounds the byte offset; word 3 is gfx9's
+// 32-bit data format, which untyped buffer loads need.
 __device__ __forceinline__ void store16_coh(float *p, v4f v)
 {
     asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
-__device__ __forceinline__ v4f load16_coh(const float *p)
+__device__ __forceinline__ v4f load16_coh(const float *base, uint32_t byte_off)
 {
-    v4f v;
-    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
-    return v;
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, 0x7fffffff, 0x00020000);
+    return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16));
 }
 
 // NW waves: NW/2 along the A rows (MI 16-row subtiles each) x 2 along the
@@ -340,8 +343,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_dense_fp8_kernel(DenseArgs a)
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) o[i][j] = load16_coh(pp + ((i * 4 + j) * NT + tid) * 4);
-                wait_vm<0>();
+                    for (int j = 0; j < 4; ++j) o[i][j] = load16_coh(pp, (uint32_t)(((i * 4 + j) * NT + tid) * 16));
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
 #pragma unroll
