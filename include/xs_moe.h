@@ -75,7 +75,7 @@ int xs_stream_synchronize(void *stream);
 /* Router logits = x . router_w^T in f32 (replaces linear(x, router_w, nullptr),
  * xstar_cpp/src/ops/linear.cpp:9-66 over gemm_launch, xstar_cpp/include/ops/gemm.h:165-176).
  * x [T, H], router_w [E, H], dtype XS_F32 or XS_BF16 (both the same);
- * logits [T, E] f32.  exact = 1: sequential-k f32 accumulation with separately
+ * logits [T, E] f32.  exact != 0: sequential-k f32 accumulation with separately
  * rounded products, bit-identical to gemm_cpu (gemm.h:57-83).  exact = 0 (bf16
  * only): bf16 MFMA with f32 accumulation.  H % 128 == 0. */
 int xs_moe_router_logits(const void *x, const void *router_w, int dtype, int64_t T, int64_t E,
@@ -186,6 +186,23 @@ int xs_gemm_fp8_blockscale_packed(const void *A, const uint8_t *Bp, const float 
                                   int64_t N, int64_t K, void *C, void *workspace,
                                   size_t workspace_bytes, void *stream);
 
+/* Router of the MoE layer (xs_moe_params.router_exact).  The reference's
+ * router logits are gemm_cpu's sequential f32 sums (gemm.h:57-83); the
+ * routing contract asks for its top-k indices bit for bit.
+ *   XS_ROUTER_MFMA: bf16 MFMA logits, f32 accumulate.  Fast, not bit-exact:
+ *     a token whose top-k keys lie within rounding of each other may route
+ *     differently.
+ *   XS_ROUTER_CERTIFIED: bit-exact routing.  The MFMA logits come with a
+ *     proven bound on their distance from the gemm_cpu sums; tokens whose
+ *     top-k the bound settles are routed on them, and for the others the
+ *     logits whose key interval meets another's (the undecided experts) are
+ *     recomputed in gemm_cpu order before routing.  Indices, order, counts
+ *     and the permutation are the reference's; logits (and so the routing
+ *     weights) of settled experts are the MFMA's.  f32 inputs take the chain
+ *     router.
+ *   XS_ROUTER_CHAIN: every logit in gemm_cpu order (bit-exact logits too). */
+enum { XS_ROUTER_MFMA = 0, XS_ROUTER_CERTIFIED = 1, XS_ROUTER_CHAIN = 2 };
+
 /* ---------------------------------------------------------------------------
  * The whole MoE layer.  Replaces mlp(x, gate_up_weight, down_weight)
  * (xstar_cpp/include/ops/mlp.h:51) at its call sites in transformer_block
@@ -204,7 +221,7 @@ typedef struct {
     int x_dtype;          /* XS_BF16 or XS_F32: x, router_w and out */
     int routed_format;    /* XS_FP8_E4M3 (128x128 f32 scales) or XS_FP4_E2M1X2 (MXFP4) */
     int has_shared;       /* 1: shared expert weights present (FP8 128x128) */
-    int router_exact;     /* 1: bit-exact sequential f32 router logits */
+    int router_exact;     /* XS_ROUTER_MFMA (0), XS_ROUTER_CERTIFIED (1) or XS_ROUTER_CHAIN (2) */
     int has_norm;         /* 1: RMSNorm x with norm_weight first (the block's pre-norm) */
     float norm_eps;       /* RMSNorm epsilon when has_norm */
 } xs_moe_params;

@@ -1,0 +1,157 @@
+// Additions to emu.hpp for the router kernels of moe_router.hip: the wave
+// exchanges they use (shuffles of ints, shfl_up, readlane, DPP row patterns,
+// __any), device atomics, the bf16 16x16x32 MFMA (exact products, the sum
+// rounded once to f32), and a launcher with a z grid dimension.
+#pragma once
+#include "emu.hpp"
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+inline float __fadd_rn(float a, float b) { return a + b; }
+inline float __fmul_rn(float a, float b) { return a * b; }
+inline float __int_as_float(int i) { float f; memcpy(&f, &i, 4); return f; }
+inline int atomicOr(uint32_t *p, uint32_t v) { return (int)__atomic_fetch_or(p, v, __ATOMIC_RELAXED); }
+
+// every lane posts v; returns the value lane src posted
+inline uint64_t emu_xchg(uint64_t v, int src)
+{
+    const int w = wave_id(), l = lane_id();
+    tb->xch[w][l] = v;
+    tb->wbar[w]->arrive_and_wait();
+    const uint64_t r = tb->xch[w][src & 63];
+    tb->wbar[w]->arrive_and_wait();
+    return r;
+}
+inline int __shfl_xor(int v, int m, int) { return (int)(uint32_t)emu_xchg((uint32_t)v, lane_id() ^ m); }
+inline int __shfl_up(int v, int d, int)
+{
+    const int l = lane_id();
+    return (int)(uint32_t)emu_xchg((uint32_t)v, l >= d ? l - d : l);
+}
+inline int emu_readlane(int v, int src) { return (int)(uint32_t)emu_xchg((uint32_t)v, src); }
+#define __builtin_amdgcn_readlane(v, l) emu_readlane((v), (l))
+inline int __any(int pred)
+{
+    const int w = wave_id(), l = lane_id();
+    tb->xch[w][l] = pred != 0;
+    tb->wbar[w]->arrive_and_wait();
+    int r = 0;
+    for (int i = 0; i < 64; ++i) r |= (int)tb->xch[w][i];
+    tb->wbar[w]->arrive_and_wait();
+    return r;
+}
+// DPP row patterns used by the route kernel: quad_perm (0x00-0xff),
+// row_mirror (0x140), row_half_mirror (0x141); all rows and banks enabled
+inline int emu_dpp(int old, int src, int ctrl, int, int, bool)
+{
+    (void)old;
+    const int l = lane_id();
+    int from;
+    if (ctrl < 0x100) from = (l & ~3) + ((ctrl >> (2 * (l & 3))) & 3);
+    else if (ctrl == 0x140) from = (l & ~15) + 15 - (l & 15);
+    else if (ctrl == 0x141) from = (l & ~7) + 7 - (l & 7);
+    else { EMU_ERR("DPP control %#x not modelled", ctrl); from = l; }
+    return (int)(uint32_t)emu_xchg((uint32_t)src, from);
+}
+#define __builtin_amdgcn_update_dpp(o, s, c, r, b, bc) emu_dpp((o), (s), (c), (r), (b), (bc))
+
+// bf16 16x16x32: lane 16g + r gives row r, K elements [8g, 8g + 8) of A and
+// B; lane 16g + r receives C[4g + v][r] += sum_k A[4g + v][k] B[r][k].  The
+// hardware's internal order and rounding are not specified, so the model is
+// selectable (EMU_MFMA_MODEL): 0 the exact products summed in double and
+// rounded once with C; 1 C plus the products in k order, each add rounded to
+// f32; 2 the same with every add truncated toward zero (the coarsest
+// behaviour the certified router's bound allows for).
+inline int g_mfma_model = 0;
+inline float emu_add_rz(float a, float b)
+{
+    const double s = (double)a + (double)b;   // exact: both are floats of close exponent or one dominates
+    float r = (float)s;
+    if ((double)r != s && std::fabs((double)r) > std::fabs(s)) r = std::nextafter(r, 0.0f);
+    return r;
+}
+inline float bf16v(__bf16 b) { uint16_t u; memcpy(&u, &b, 2); return __uint_as_float((uint32_t)u << 16); }
+inline v4f emu_mfma_bf16(v8bf a, v8bf b, v4f c, int, int, int)
+{
+    const int w = wave_id(), l = lane_id();
+    memcpy(tb->wx[w][l], &a, 16);
+    memcpy(tb->wx[w][l] + 16, &b, 16);
+    tb->wbar[w]->arrive_and_wait();
+    const int r = l & 15, g = l >> 4;
+    v4f out;
+    auto el = [&](int row, int k, int off) {
+        __bf16 v;
+        memcpy(&v, tb->wx[w][16 * (k / 8) + row] + off + 2 * (k % 8), 2);
+        return (double)bf16v(v);
+    };
+    for (int v = 0; v < 4; ++v) {
+        if (g_mfma_model == 0) {
+            double s = c[v];
+            for (int k = 0; k < 32; ++k) s += el(4 * g + v, k, 0) * el(r, k, 16);
+            out[v] = (float)s;
+        } else {
+            float s = c[v];
+            for (int k = 0; k < 32; ++k) {
+                const float p = (float)(el(4 * g + v, k, 0) * el(r, k, 16));   // exact: bf16 x bf16
+                s = g_mfma_model == 1 ? s + p : emu_add_rz(s, p);
+            }
+            out[v] = s;
+        }
+    }
+    tb->wbar[w]->arrive_and_wait();
+    return out;
+}
+#define __builtin_amdgcn_mfma_f32_16x16x32_bf16 emu_mfma_bf16
+
+// the tile kernel's DMA: a per-lane source, a wave-uniform LDS base
+inline void dma16x(const void *g, uint32_t lds)
+{
+    lds = (uint32_t)wave_first(lds, "rt_dma16 lds");
+    dma_lane((const uint8_t *)g, lds, 16, "rt_dma16");
+}
+
+template <typename F>
+inline void emu_launch3(F fn, unsigned gx, unsigned gy, unsigned gz, unsigned nt, size_t smem, unsigned conc)
+{
+    gridDim = {gx, gy, gz};
+    blockDim = {nt, 1, 1};
+    std::vector<EmuDim> blocks;
+    for (unsigned z = 0; z < gz; ++z)
+        for (unsigned y = 0; y < gy; ++y)
+            for (unsigned x = 0; x < gx; ++x) blocks.push_back({x, y, z});
+    for (size_t b0 = 0; b0 < blocks.size(); b0 += conc) {
+        const size_t nb = std::min<size_t>(conc, blocks.size() - b0);
+        std::vector<Blk *> bk(nb);
+        std::vector<std::thread> th;
+        for (size_t i = 0; i < nb; ++i) {
+            Blk *B = new Blk();
+            B->smem_size = smem ? smem : 16;
+            B->smem = (uint8_t *)aligned_alloc(256, (B->smem_size + 255) / 256 * 256 + 256);
+            memset(B->smem, 0x5A, B->smem_size);
+            B->bar = new std::barrier<>(nt);
+            for (unsigned w = 0; w < nt / 64; ++w) B->wbar[w] = new std::barrier<>(64);
+            bk[i] = B;
+            const EmuDim bid = blocks[b0 + i];
+            for (unsigned t = 0; t < nt; ++t)
+                th.emplace_back([=] {
+                    threadIdx = {t, 0, 0};
+                    blockIdx = bid;
+                    tb = B;
+                    tq.clear();
+                    t_m0 = 0; t_sbase = nullptr; t_ndma = 0; t_shoff = 0;
+                    fn();
+                    if (!tq.empty()) EMU_ERR("lane exits with %zu DMA ops outstanding", tq.size());
+                    emu_wait(0);
+                    B->wbar[t / 64]->arrive_and_drop();
+                    B->bar->arrive_and_drop();
+                });
+        }
+        for (auto &t : th) t.join();
+        for (auto *B : bk) {
+            free(B->smem);
+            delete B->bar;
+            for (unsigned w = 0; w < nt / 64; ++w) delete B->wbar[w];
+            delete B;
+        }
+    }
+}

@@ -49,12 +49,12 @@ static const Tensor *opt(py::object o) { return o.is_none() ? nullptr : &o.cast<
 Tensor moe_py(Tensor &x, Tensor &router_w, py::object router_bias, Tensor &w13, Tensor &w13_scale,
               Tensor &w2, Tensor &w2_scale, py::object shared_w13, py::object shared_w13_scale,
               py::object shared_w2, py::object shared_w2_scale, std::int64_t top_k, std::int64_t n_group,
-              std::int64_t topk_group, bool renormalize, float routed_scaling, bool router_exact,
+              std::int64_t topk_group, bool renormalize, float routed_scaling, int router,
               py::object norm_weight, float norm_eps, py::object residual)
 {
     return moe(x, router_w, opt(router_bias), w13, w13_scale, w2, w2_scale, opt(shared_w13),
                opt(shared_w13_scale), opt(shared_w2), opt(shared_w2_scale), top_k, n_group, topk_group,
-               renormalize, routed_scaling, router_exact, opt(norm_weight), norm_eps, opt(residual));
+               renormalize, routed_scaling, router, opt(norm_weight), norm_eps, opt(residual));
 }
 
 py::tuple rmsnorm_quant_fp8_py(Tensor &x, Tensor &weight, float eps)
@@ -129,11 +129,11 @@ PYBIND11_MODULE(xstar_cpp, m)
           py::arg("shared_w13_scale") = py::none(), py::arg("shared_w2") = py::none(),
           py::arg("shared_w2_scale") = py::none(), py::arg("top_k") = 6, py::arg("n_group") = 1,
           py::arg("topk_group") = 1, py::arg("renormalize") = true, py::arg("routed_scaling") = 1.0f,
-          py::arg("router_exact") = false, py::arg("norm_weight") = py::none(), py::arg("norm_eps") = 1e-6f,
+          py::arg("router") = 1, py::arg("norm_weight") = py::none(), py::arg("norm_eps") = 1e-6f,
           py::arg("residual") = py::none());
     m.def("moe_block_ffn", &moe_block_ffn, py::arg("h"), py::arg("ln2_w"), py::arg("eps"), py::arg("w"),
           py::arg("top_k") = 6, py::arg("n_group") = 1, py::arg("topk_group") = 1, py::arg("renormalize") = true,
-          py::arg("routed_scaling") = 1.0f, py::arg("router_exact") = false);
+          py::arg("routed_scaling") = 1.0f, py::arg("router") = 1);
     m.def("rmsnorm", &rmsnorm, py::arg("x"), py::arg("weight"), py::arg("eps"));
     m.def("rmsnorm_quant_fp8", &rmsnorm_quant_fp8_py, py::arg("x"), py::arg("weight"), py::arg("eps"));
     // safetensors reading (the reference's names and signatures, bindings/python_bindings.cpp:412-424,519-522)

@@ -39,7 +39,7 @@ static int prof_mark(int stage, hipStream_t st)
 }
 
 struct WsLayout {
-    size_t logits, idx, w, mask, wordprefix, counts, offsets, perm, inv, row_token, tiles, tiletab, part, cnt1, cnt2;
+    size_t logits, dpart, flog, pairs, ccert, flagged, idx, w, mask, wordprefix, counts, offsets, perm, inv, row_token, tiles, tiletab, part, cnt1, cnt2;
     size_t xn, xq, xs, xmq, xms, actq, acts, actms, y, ccnt;
     size_t total;
 };
@@ -85,6 +85,15 @@ static bool getenv_flag(const char *name, bool dflt)
 // is refused with XS_ERR_UNSUPPORTED.
 static bool weight_direct_enabled() { return getenv_flag("XS_WEIGHT_DIRECT", false); }
 
+// XS_ROUTER_MARGIN=<f>: scales the certified router's key margins (tests of
+// the exact pass: a large value sends every token through it).  Default 1.
+static float router_margin_scale()
+{
+    const char *v = getenv("XS_ROUTER_MARGIN");
+    const float f = v ? strtof(v, nullptr) : 1.0f;
+    return f >= 1.0f ? f : 1.0f;
+}
+
 static bool fuse_combine(const xs_moe_params *p)
 {
     return use_wide(p) && getenv_flag("XS_FUSE_COMBINE", false);
@@ -115,7 +124,16 @@ static WsLayout layout(const xs_moe_params *p)
     WsLayout L = {};
     size_t o = 0;
     auto take = [&](size_t &field, size_t bytes) { field = o; o += al(bytes); };
-    take(L.logits, 4 * T * E * (size_t)router_logits_splits(p->T, p->H, p->router_exact, p->x_dtype));
+    const size_t nsplit = (size_t)router_logits_splits(p->T, p->H, p->router_exact, p->x_dtype);
+    take(L.logits, 4 * T * E * nsplit);
+    // the certified router: bound terms, logit rows and pairs of the tokens it
+    // lists (at most every logit), its two counters
+    const bool cert = router_kind(p->router_exact, p->x_dtype) == XS_ROUTER_CERTIFIED;
+    take(L.dpart, cert ? 4 * T * E * nsplit : 0);
+    take(L.flog, cert ? 4 * T * E : 0);
+    take(L.pairs, cert ? 8 * T * E : 0);
+    take(L.ccert, cert ? 8 : 0);
+    take(L.flagged, cert ? 4 * T : 0);
     take(L.idx, 4 * S);
     take(L.w, 4 * S);
     take(L.mask, 4 * W * E);
@@ -168,6 +186,8 @@ static int check_params(const xs_moe_params *p)
     XS_REQUIRE(p->T * p->H < ((int64_t)1 << 32) && (p->T * p->top_k + p->T) * p->I < ((int64_t)1 << 32),
                "too many rows: T x H and T x (top_k + 1) x I must stay below 2^32 (split the batch)");
     XS_REQUIRE(p->has_norm == 0 || p->has_norm == 1, "has_norm must be 0 or 1");
+    XS_REQUIRE(p->router_exact >= XS_ROUTER_MFMA && p->router_exact <= XS_ROUTER_CHAIN,
+               "router_exact must be XS_ROUTER_MFMA, XS_ROUTER_CERTIFIED or XS_ROUTER_CHAIN");
     XS_REQUIRE(p->routed_format != XS_FP4_E2M1X2 || p->I % 256 == 0,
                "shape mismatch: MXFP4 experts need I to be a multiple of 256");
     if (p->n_group > 1) {
@@ -336,14 +356,34 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     // 2. router: logits -> top-k + per-expert token masks
     if ((rc = prof_mark(1, st))) return rc;
     const int nsplit = router_logits_splits(T, H, p->router_exact, p->x_dtype);
+    const bool certified = router_kind(p->router_exact, p->x_dtype) == XS_ROUTER_CERTIFIED;
+    CertState cs = {};
+    if (certified) {
+        cs.dpart = WS(float, dpart);
+        cs.kblocks = (int)(H / nsplit / 32);
+        cs.flog = WS(float, flog);
+        cs.pairs = WS(int32_t, pairs);
+        cs.cnt = WS(int32_t, ccert);
+        cs.flagged = WS(int32_t, flagged);
+        cs.margin_scale = router_margin_scale();
+    }
     rc = launch_router_logits(xin, t->router_w, p->x_dtype, T, E, H, p->router_exact, logits, nsplit, st, mask,
                               (int64_t)Wd * E, fold_quant ? WS(uint8_t, xq) : nullptr,
-                              fold_quant ? WS(float, xs) : nullptr);
+                              fold_quant ? WS(float, xs) : nullptr, certified ? &cs : nullptr);
     if (rc) return rc;
     if ((rc = prof_mark(2, st))) return rc;
     rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
-                      p->routed_scaling, idx, w, mask, Wd, nsplit, t->logits, st);
+                      p->routed_scaling, idx, w, mask, Wd, nsplit, t->logits, st, certified ? &cs : nullptr,
+                      certified ? 1 : 0);
     if (rc) return rc;
+    if (certified) {
+        // the pairs the bound left undecided, in gemm_cpu order, then the
+        // listed tokens' routing on their patched logit rows
+        if ((rc = launch_router_fix(xin, t->router_w, p->x_dtype, T, E, H, cs, st))) return rc;
+        rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
+                          p->routed_scaling, idx, w, mask, Wd, 1, t->logits, st, &cs, 2);
+        if (rc) return rc;
+    }
     // 3. permute: (expert, token)-sorted positions, tile offsets
     if ((rc = prof_mark(3, st))) return rc;
     Plan pl;

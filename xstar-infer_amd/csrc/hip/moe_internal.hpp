@@ -84,7 +84,10 @@ __device__ __forceinline__ void quant8_fp8(const float *v, uint8_t *__restrict__
     if (s) *s = amax == 0.0f ? 1.0f : __fdiv_rn(amax, 448.0f);
 }
 
+struct CertState;
 // ---- launchers (stream-ordered, no synchronisation) ----
+// Router kind (XS_ROUTER_*) for params.router_exact and the input dtype.
+int router_kind(int exact, int dtype);
 // Number of K slices the bf16 MFMA router uses for T tokens (1 = no split).
 int router_logits_splits(int64_t T, int64_t H, int exact, int dtype);
 // Writes nsplit partial logit slices [nsplit][T][E] (nsplit = 1: the logits).
@@ -92,16 +95,36 @@ int router_logits_splits(int64_t T, int64_t H, int exact, int dtype);
 // q/qs (optional, decode path only: router_quantizes()): the FP8 1x128
 // quantization of x, written by the same launch.
 bool router_quantizes(int64_t T, int exact, int dtype);
+// cert (certified router only): its dpart is written and its counters zeroed.
 int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
                          int exact, float *logits, int nsplit, hipStream_t st,
                          uint32_t *mask_clear = nullptr, int64_t mask_words = 0, uint8_t *q = nullptr,
-                         float *qs = nullptr);
+                         float *qs = nullptr, const CertState *cert = nullptr);
+// The certified router's device state for one forward (moe_router.hip):
+// dpart [nsplit][T][E] error-bound terms of the MFMA logit slices, flog [T][E]
+// logit rows of the tokens it could not settle, pairs [T*E][2] the (token,
+// expert) logits to recompute exactly, cnt[2] {pairs, flagged tokens}
+// (zeroed by the logits launch), flagged [T].
+struct CertState {
+    float *dpart;
+    int kblocks;          // 32-wide K blocks per logit slice (H / nsplit / 32)
+    float *flog;
+    int32_t *pairs;
+    int32_t *cnt;
+    int32_t *flagged;
+    float margin_scale;   // 1 (XS_ROUTER_MARGIN scales it: tests of the exact path)
+};
 // Routes on the sum (in slice order) of nsplit partial logit slices; writes the
-// summed logits to logits_out when it is not NULL.
+// summed logits to logits_out when it is not NULL.  mode 0: plain; 1:
+// certified (with cert: tokens it cannot settle are listed for the exact
+// pass and left unrouted); 2: routes the listed tokens on cert->flog.
 int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,
                  int64_t n_group, int64_t topk_group, int renorm, float scaling, int32_t *idx,
                  float *w, uint32_t *mask, int mask_words, int nsplit, float *logits_out,
-                 hipStream_t st);
+                 hipStream_t st, const CertState *cert = nullptr, int mode = 0);
+// The exact (gemm_cpu order) logits of the listed pairs into cert->flog.
+int launch_router_fix(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
+                      const CertState &cert, hipStream_t st);
 // zero[0 .. zero_n) is cleared by the same launch (counters of a following kernel).
 int launch_quant_act(const void *x, int dtype, int64_t rows, int64_t cols, uint8_t *q, void *s,
                      int mx, hipStream_t st, int32_t *zero = nullptr, int zero_n = 0);

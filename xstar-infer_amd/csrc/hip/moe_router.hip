@@ -26,134 +26,190 @@ __device__ __forceinline__ void clear_mask(uint32_t *mask, int64_t words)
 }
 
 // ------------------------------------------------------------ exact logits
-// gemm_cpu order: each logit is one sequential f32 chain over k (a separately
-// rounded product added to the running sum, no contraction), so the work is
-// latency-bound chains.  A lane owns TB chains: one expert, TB tokens (one
-// token for small batches, where the chains' latency is the cost; four for
-// large ones, where the LDS reads shared by the four chains are).  The block
-// holds 64 experts x 4 TB tokens (TB per wave).  K moves in chunks of 256: the
-// chunk of the 64 router rows is converted to f32 into LDS (rows padded to
-// 260 floats, so a lane's 16-byte reads of its own row hit distinct banks),
-// the token rows too (read as broadcasts), and the next chunk's loads are in
-// flight while the chains run over the current one.
-constexpr int kXC = 256;                 // K chunk
-constexpr int kXR = kXC + 4;             // padded LDS row (floats)
+// gemm_cpu order: each logit is one sequential f32 chain over k, a separately
+// rounded product added to the running sum (no contraction).  The chains are
+// latency-bound, so a block splits each chain's work between waves: wave 0
+// runs 64 chains (one (token, expert) pair per lane), and waves 1..4 compute
+// the rounded products x[t][k] * w[e][k] of the next K chunk into LDS
+// (double-buffered), so the chain wave issues one LDS read per 4 adds and
+// nothing else.  A product computed by a helper is the same f32 value the
+// reference rounds (the helpers only multiply, the chain only adds), so the
+// bits are gemm_cpu's for f32 and bf16 operands alike.
+// Pairs: implicit (pair p = token p / E, expert p % E: every logit) or a list
+// of (token, expert) int32 pairs with its count in device memory (the pairs
+// the certified router could not settle).  Blocks loop over groups of 64
+// pairs, so the grid is sized without knowing the count.
+constexpr int kCK = 128;                 // K chunk per buffer
+constexpr int kCR = kCK + 4;             // padded LDS row (floats): a lane's 16-byte reads of its own row hit distinct banks
+constexpr int kChainThreads = 320;       // 1 chain wave + 4 product waves
 
 template <typename T>
-struct ChainLoad;
-template <>
-struct ChainLoad<uint16_t> {
-    static constexpr int N = 8;          // 16-byte loads per thread per chunk (64 bf16)
-    v4i r[N];
-};
-template <>
-struct ChainLoad<float> {
-    static constexpr int N = 16;         // 64 f32
-    v4i r[N];
+struct ChainUnit {
+    // one unit = 8 consecutive k of one pair: x and w, 16 bytes (bf16) or 32 (f32) each
+    static constexpr int V = sizeof(T) == 2 ? 1 : 2;
+    v4i x[V], w[V];
 };
 
-template <typename T, int TB>
-__global__ __launch_bounds__(256) void router_logits_exact_kernel(const T *__restrict__ x,
-                                                                  const T *__restrict__ wr,
-                                                                  int Tn, int E, int H,
-                                                                  float *__restrict__ logits,
-                                                                  uint32_t *__restrict__ mask, int64_t mask_words)
+template <typename T>
+__device__ __forceinline__ void chain_unit_load(ChainUnit<T> &u, const T *xr, const T *wr)
+{
+#pragma unroll
+    for (int i = 0; i < ChainUnit<T>::V; ++i) {
+        u.x[i] = *reinterpret_cast<const v4i *>(xr + i * (16 / sizeof(T)));
+        u.w[i] = *reinterpret_cast<const v4i *>(wr + i * (16 / sizeof(T)));
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void chain_unit_products(const ChainUnit<T> &u, float *dst)
+{
+#pragma clang fp contract(off)
+    float xv[8], wv[8];
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            xv[2 * j] = __uint_as_float((uint32_t)u.x[0][j] << 16);
+            xv[2 * j + 1] = __uint_as_float((uint32_t)u.x[0][j] & 0xFFFF0000u);
+            wv[2 * j] = __uint_as_float((uint32_t)u.w[0][j] << 16);
+            wv[2 * j + 1] = __uint_as_float((uint32_t)u.w[0][j] & 0xFFFF0000u);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                xv[4 * i + j] = __int_as_float(u.x[i][j]);
+                wv[4 * i + j] = __int_as_float(u.w[i][j]);
+            }
+    }
+    v4f lo, hi;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        lo[j] = __fmul_rn(xv[j], wv[j]);
+        hi[j] = __fmul_rn(xv[4 + j], wv[4 + j]);
+    }
+    *reinterpret_cast<v4f *>(dst) = lo;
+    *reinterpret_cast<v4f *>(dst + 4) = hi;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kChainThreads) void router_chain_kernel(const T *__restrict__ x,
+                                                                     const T *__restrict__ wr, int E, int H,
+                                                                     const int32_t *__restrict__ pairs,
+                                                                     const int32_t *__restrict__ npairs_dev,
+                                                                     int64_t npairs, float *__restrict__ out,
+                                                                     uint32_t *__restrict__ mask, int64_t mask_words)
 {
 #pragma clang fp contract(off)
     clear_mask(mask, mask_words);
-    extern __shared__ __attribute__((aligned(16))) float xsm[];
-    float *Ws = xsm;                      // [64][kXR]
-    float *Xs = xsm + 64 * kXR;           // [4 TB][kXC]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int e0 = blockIdx.x * 64, t0 = blockIdx.y * 4 * TB + wave * TB;
-    // loader mapping: router row lr (4 threads per row, 64 consecutive k each);
-    // this wave's TB token rows, 4 consecutive k per lane.  H is a multiple of
-    // 128: a last chunk of 128 loads (and runs) half.
-    const int lr = tid >> 2, lc = (tid & 3) * 64;
-    const T *wrow = wr + (size_t)min(e0 + lr, E - 1) * H + lc;
-    ChainLoad<T> ld;
-    float xv[TB][4];
-    auto fetch = [&](int k0) {
-        const int rem = min(kXC, H - k0);
-        if (lc < rem) {
+    extern __shared__ __attribute__((aligned(16))) float prod[];   // [2][64][kCR]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t n = pairs ? (int64_t)*npairs_dev : npairs;
+    const int nc = H / kCK;
+    // product waves: 256 threads x 4 units = 64 pairs x 16 units of 8 k per chunk;
+    // 16 consecutive threads cover one pair's 128 k (256 contiguous bytes of bf16)
+    const int htid = tid - 64;
+    for (int64_t base = (int64_t)blockIdx.x * 64; base < n; base += (int64_t)gridDim.x * 64) {
+        const int cnt = (int)min((int64_t)64, n - base);
+        if (wave == 0) {
+            float acc = 0.0f;
+            for (int c = 0; c < nc; ++c) {
+                __syncthreads();              // chunk c's products are in buffer c & 1
+                const float *row = prod + (c & 1) * 64 * kCR + lane * kCR;
 #pragma unroll
-            for (int i = 0; i < ChainLoad<T>::N; ++i)
-                ld.r[i] = *reinterpret_cast<const v4i *>(wrow + k0 + i * (16 / sizeof(T)));
-        }
-        if (lane * 4 < rem) {
-#pragma unroll
-            for (int j = 0; j < TB; ++j) load4(x + (size_t)min(t0 + j, Tn - 1) * H + k0 + lane * 4, xv[j]);
-        }
-    };
-    auto store = [&]() {
-        float *dst = Ws + lr * kXR + lc;
-        if constexpr (sizeof(T) == 2) {
-#pragma unroll
-            for (int i = 0; i < ChainLoad<T>::N; ++i) {
-                v4f lo, hi;
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    lo[2 * j] = __uint_as_float((uint32_t)ld.r[i][j] << 16);
-                    lo[2 * j + 1] = __uint_as_float((uint32_t)ld.r[i][j] & 0xFFFF0000u);
-                    hi[2 * j] = __uint_as_float((uint32_t)ld.r[i][j + 2] << 16);
-                    hi[2 * j + 1] = __uint_as_float((uint32_t)ld.r[i][j + 2] & 0xFFFF0000u);
+                for (int k = 0; k < kCK; k += 4) {
+                    const v4f pv = *reinterpret_cast<const v4f *>(row + k);
+                    acc = acc + pv[0];
+                    acc = acc + pv[1];
+                    acc = acc + pv[2];
+                    acc = acc + pv[3];
                 }
-                *reinterpret_cast<v4f *>(dst + 8 * i) = lo;
-                *reinterpret_cast<v4f *>(dst + 8 * i + 4) = hi;
+            }
+            __syncthreads();                  // the last chunk: the product waves' final barrier
+            if (lane < cnt) {
+                int t, e;
+                if (pairs) {
+                    t = pairs[2 * (base + lane)];
+                    e = pairs[2 * (base + lane) + 1];
+                } else {
+                    t = (int)((base + lane) / E);
+                    e = (int)((base + lane) % E);
+                }
+                out[(size_t)t * E + e] = acc;
             }
         } else {
+            const T *xr[4], *wrow[4];
+            int l[4], k8[4];
 #pragma unroll
-            for (int i = 0; i < ChainLoad<T>::N; ++i)
-                *reinterpret_cast<v4i *>(dst + 4 * i) = ld.r[i];
-        }
+            for (int i = 0; i < 4; ++i) {
+                const int u = i * 256 + htid;
+                l[i] = u >> 4;
+                k8[i] = u & 15;
+                const int64_t pp = base + (l[i] < cnt ? l[i] : 0);
+                int t, e;
+                if (pairs) {
+                    t = pairs[2 * pp];
+                    e = pairs[2 * pp + 1];
+                } else {
+                    t = (int)(pp / E);
+                    e = (int)(pp % E);
+                }
+                xr[i] = x + (size_t)t * H + 8 * k8[i];
+                wrow[i] = wr + (size_t)e * H + 8 * k8[i];
+            }
+            ChainUnit<T> ua[4], ub[4];
+            // chunk 0 into buffer 0 and chunk 1's loads in flight, then per
+            // iteration c: products of chunk c + 1 (loaded one iteration ago)
+            // into buffer (c + 1) & 1 and chunk c + 2's loads issued
 #pragma unroll
-        for (int j = 0; j < TB; ++j)
-            *reinterpret_cast<v4f *>(Xs + (wave * TB + j) * kXC + lane * 4) = v4f{xv[j][0], xv[j][1], xv[j][2], xv[j][3]};
-    };
-    float acc[TB];
+            for (int i = 0; i < 4; ++i) chain_unit_load(ua[i], xr[i], wrow[i]);
+            if (nc > 1) {
 #pragma unroll
-    for (int j = 0; j < TB; ++j) acc[j] = 0.0f;
-    fetch(0);
-    for (int k0 = 0; k0 < H; k0 += kXC) {
-        __syncthreads();                  // the previous chunk's chains are done with LDS
-        store();
-        if (k0 + kXC < H) fetch(k0 + kXC);
-        __syncthreads();
-        const float *wl = Ws + lane * kXR;
-        const float *xl = Xs + wave * TB * kXC;
-        const int rem = min(kXC, H - k0);
-#pragma unroll 4
-        for (int k = 0; k < rem; k += 4) {
-            const v4f w4 = *reinterpret_cast<const v4f *>(wl + k);
-            v4f x4[TB];
+                for (int i = 0; i < 4; ++i) chain_unit_load(ub[i], xr[i] + kCK, wrow[i] + kCK);
+            }
 #pragma unroll
-            for (int j = 0; j < TB; ++j) x4[j] = *reinterpret_cast<const v4f *>(xl + j * kXC + k);
+            for (int i = 0; i < 4; ++i) chain_unit_products(ua[i], prod + l[i] * kCR + 8 * k8[i]);
+            for (int c = 0; c < nc; ++c) {
+                __syncthreads();
+                if (c + 1 < nc) {
+                    ChainUnit<T> *cur = (c & 1) ? ua : ub;   // chunk c + 1
+                    ChainUnit<T> *nxt = (c & 1) ? ub : ua;   // chunk c + 2 goes where chunk c was
+                    float *dst = prod + ((c + 1) & 1) * 64 * kCR;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+                    for (int i = 0; i < 4; ++i) chain_unit_products(cur[i], dst + l[i] * kCR + 8 * k8[i]);
+                    if (c + 2 < nc) {
 #pragma unroll
-                for (int j = 0; j < TB; ++j) acc[j] = acc[j] + x4[j][i] * w4[i];   // no contraction (pragma above)
+                        for (int i = 0; i < 4; ++i)
+                            chain_unit_load(nxt[i], xr[i] + (size_t)(c + 2) * kCK, wrow[i] + (size_t)(c + 2) * kCK);
+                    }
+                }
+            }
+            __syncthreads();
         }
     }
-    const int e = e0 + lane;
-#pragma unroll
-    for (int j = 0; j < TB; ++j)
-        if (t0 + j < Tn && e < E) logits[(size_t)(t0 + j) * E + e] = acc[j];
 }
 
-template <typename T, int TB>
-static int launch_exact(const T *x, const T *wr, int64_t T_, int64_t E, int64_t H, float *logits, uint32_t *mask,
+// Chain launch: every logit of [T, E] (pairs == NULL) or the listed pairs.
+template <typename T>
+static int launch_chain(const T *x, const T *wr, int64_t T_, int64_t E, int64_t H, const int32_t *pairs,
+                        const int32_t *npairs_dev, int64_t max_pairs, float *out, uint32_t *mask,
                         int64_t mask_words, hipStream_t st)
 {
-    const size_t smem = sizeof(float) * (64 * kXR + 4 * TB * kXC);
+    const size_t smem = sizeof(float) * 2 * 64 * kCR;
     static bool attr_set = false;
     if (!attr_set) {
-        XS_HIP(hipFuncSetAttribute((const void *)router_logits_exact_kernel<T, TB>,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        XS_HIP(hipFuncSetAttribute((const void *)router_chain_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)smem));
         attr_set = true;
     }
-    dim3 grid((unsigned)((E + 63) / 64), (unsigned)((T_ + 4 * TB - 1) / (4 * TB))), block(256);
-    router_logits_exact_kernel<T, TB><<<grid, block, smem, st>>>(x, wr, (int)T_, (int)E, (int)H, logits, mask,
-                                                                 mask_words);
+    const int64_t groups = (max_pairs + 63) / 64;
+    // two blocks per CU fit (67.6 KB of LDS each); a list launch is sized for
+    // its worst case and loops, so it stays small
+    const int64_t cap = pairs ? 512 : 4096;
+    dim3 grid((unsigned)std::max((int64_t)1, std::min(groups, cap))), block(kChainThreads);
+    router_chain_kernel<T><<<grid, block, smem, st>>>(x, wr, (int)E, (int)H, pairs, npairs_dev,
+                                                      pairs ? 0 : T_ * E, out, mask, mask_words);
     XS_LAUNCH_CHECK();
     return XS_OK;
 }
@@ -178,15 +234,43 @@ __device__ __forceinline__ void quant_chunk_fp8(const T *__restrict__ xr, int co
 // weight is 2 MB and stays L2-resident).  MFMA 16x16x32 bf16: lane l supplies
 // row (l % 16) and k-slice (l / 16) of 8 elements for both A and B, so the
 // k-pairing is consistent whatever the hardware's internal k order.
-template <int MT, int NT>
+// The certified router's error bound (CERT): besides each logit L, the kernel
+// tracks R = sum over the 32-wide K blocks of |acc| after the block's MFMA, and
+// A = sum |x_k| |w_k| (the same MFMA over the operands' magnitudes, exact
+// bf16 values), and writes D = 98 R + 101 A per (slice, token, expert) into
+// dpart.  The route kernel turns D into a bound on |L - L_ref|, L_ref the
+// sequential gemm_cpu sum (see route_token).
+__device__ __forceinline__ v8bf bf16_abs8(v8bf v)
+{
+    v4i u = __builtin_bit_cast(v4i, v);
+    u &= 0x7fff7fff;
+    return __builtin_bit_cast(v8bf, u);
+}
+__device__ __forceinline__ v4f abs4(v4f v)
+{
+    return v4f{__builtin_fabsf(v[0]), __builtin_fabsf(v[1]), __builtin_fabsf(v[2]), __builtin_fabsf(v[3])};
+}
+__device__ __forceinline__ v4f cert_d(v4f r, v4f a) { return 98.0f * r + 101.0f * a; }
+
+// Zeroes n int32 words (the certified router's counters) from the first
+// block's first threads.
+__device__ __forceinline__ void clear_words(int32_t *z, int n)
+{
+    if (z && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && (int)threadIdx.x < n) z[threadIdx.x] = 0;
+}
+
+template <int MT, int NT, bool CERT>
 __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t *__restrict__ x,
                                                                  const uint16_t *__restrict__ wr,
                                                                  int Tn, int E, int H, int klen,
                                                                  float *__restrict__ part,
                                                                  uint32_t *__restrict__ mask, int64_t mask_words,
-                                                                 uint8_t *__restrict__ q, float *__restrict__ qs)
+                                                                 uint8_t *__restrict__ q, float *__restrict__ qs,
+                                                                 float *__restrict__ dpart, int32_t *__restrict__ zero,
+                                                                 int zero_n)
 {
     clear_mask(mask, mask_words);
+    clear_words(zero, zero_n);
     if (q && blockIdx.x == 0) {
         // the FP8 1x128 activation quant of this block's tokens and K slice
         // (klen % 128 == 0, so each aligned 16-lane group is one 128-column group)
@@ -212,6 +296,7 @@ __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t 
     for (int j = 0; j < NT; ++j)
         wb[j] = reinterpret_cast<const v8bf *>(wr + (size_t)min(e0 + 16 * j + r, E - 1) * H + kbeg + g * 8);
     v4f acc[MT][NT] = {};
+    v4f aacc[MT][NT] = {}, rr[MT][NT] = {};
     for (int k = 0; k < klen; k += 128) {
         v8bf a[MT][4], b[NT][4];
 #pragma unroll
@@ -227,20 +312,31 @@ __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t 
 #pragma unroll
             for (int i = 0; i < MT; ++i)
 #pragma unroll
-                for (int j = 0; j < NT; ++j)
+                for (int j = 0; j < NT; ++j) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i][u], b[j][u], acc[i][j], 0, 0, 0);
+                    if constexpr (CERT) {
+                        aacc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf16_abs8(a[i][u]), bf16_abs8(b[j][u]),
+                                                                            aacc[i][j], 0, 0, 0);
+                        rr[i][j] += abs4(acc[i][j]);
+                    }
+                }
     }
     // output layout: lane holds column (l % 16), rows 4*(l/16) + v
     float *out = part + (size_t)blockIdx.z * Tn * E;
+    float *dout = CERT ? dpart + (size_t)blockIdx.z * Tn * E : nullptr;
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
             int e = e0 + 16 * j + r;
+            const v4f d = cert_d(rr[i][j], aacc[i][j]);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 int t = t0 + 16 * i + 4 * g + v;
-                if (t < Tn && e < E) out[(size_t)t * E + e] = acc[i][j][v];
+                if (t < Tn && e < E) {
+                    out[(size_t)t * E + e] = acc[i][j][v];
+                    if constexpr (CERT) dout[(size_t)t * E + e] = d[v];
+                }
             }
         }
 }
@@ -280,13 +376,17 @@ __device__ __forceinline__ void rt_wait_vm()
 }
 }  // namespace
 
+template <bool CERT>
 __global__ __launch_bounds__(256) void router_logits_tile_kernel(const uint16_t *__restrict__ x,
                                                                  const uint16_t *__restrict__ wr,
                                                                  int Tn, int E, int H, int klen,
                                                                  float *__restrict__ part,
-                                                                 uint32_t *__restrict__ mask, int64_t mask_words)
+                                                                 uint32_t *__restrict__ mask, int64_t mask_words,
+                                                                 float *__restrict__ dpart, int32_t *__restrict__ zero,
+                                                                 int zero_n)
 {
     clear_mask(mask, mask_words);
+    clear_words(zero, zero_n);
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -314,6 +414,7 @@ __global__ __launch_bounds__(256) void router_logits_tile_kernel(const uint16_t 
     };
 
     v4f acc[4][4] = {};        // [expert subtile j][token subtile i]
+    v4f aacc[4][4] = {}, rr[4][4] = {};   // CERT: magnitude sums and |partial| sums
 #pragma unroll
     for (int s = 0; s < kRtNST - 1; ++s) issue(s);
     for (int ks = 0; ks < KS; ++ks) {
@@ -341,11 +442,25 @@ __global__ __launch_bounds__(256) void router_logits_tile_kernel(const uint16_t 
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+            if constexpr (CERT) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wf[j] = bf16_abs8(wf[j]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xf[i] = bf16_abs8(xf[i]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        aacc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], xf[i], aacc[j][i], 0, 0, 0);
+                        rr[j][i] += abs4(acc[j][i]);
+                    }
+            }
         }
     }
     rt_wait_vm<0>();
     // result layout: lane 16g + r holds token r and experts 4g..4g+3 of the subtile
     float *out = part + (size_t)blockIdx.z * Tn * E;
+    float *dout = CERT ? dpart + (size_t)blockIdx.z * Tn * E : nullptr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int t = t0 + wm * 64 + 16 * i + l16;
@@ -353,12 +468,17 @@ __global__ __launch_bounds__(256) void router_logits_tile_kernel(const uint16_t 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int e = e0 + wn * 64 + 16 * j + 4 * g;
+            const v4f d = cert_d(rr[j][i], aacc[j][i]);
             if (e + 3 < E && (E & 3) == 0) {
                 *reinterpret_cast<v4f *>(out + (size_t)t * E + e) = acc[j][i];
+                if constexpr (CERT) *reinterpret_cast<v4f *>(dout + (size_t)t * E + e) = d;
             } else {
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    if (e + v < E) out[(size_t)t * E + e + v] = acc[j][i][v];
+                    if (e + v < E) {
+                        out[(size_t)t * E + e + v] = acc[j][i][v];
+                        if constexpr (CERT) dout[(size_t)t * E + e + v] = d[v];
+                    }
             }
         }
     }
@@ -432,65 +552,167 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
     return r;
 }
 
-// One wave per token.  Lane l holds experts l + 64*i, i < NV.
-template <int NV>
-__global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ logits,
-                                                    const float *__restrict__ bias, int Tn, int E,
-                                                    int k, int n_group, int topk_group, int renorm,
-                                                    float scaling, int32_t *__restrict__ idx,
-                                                    float *__restrict__ wout,
-                                                    uint32_t *__restrict__ mask, int mask_words,
-                                                    int nsplit, float *__restrict__ logits_out)
+// Inclusive prefix sum over the wave's lanes.
+__device__ __forceinline__ int wave_prefix(int v, int lane)
 {
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= Tn) return;
-    float s[NV], key[NV];
-    bool ok[NV];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o, WAVE);
+        if (lane >= o) v += u;
+    }
+    return v;
+}
+__device__ __forceinline__ float wave_minf(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+// The certified router's state for one forward (route_token MODE 1 and 2).
+struct CertArgs {
+    const float *dpart;   // [nsplit][T][E]: D = 98 R + 101 A of each logit slice (MODE 1)
+    int kblocks;          // 32-wide K blocks per slice
+    float *flog;          // [T][E]: the logit rows of flagged tokens (MODE 1 writes, MODE 2 reads)
+    int32_t *pairs;       // [T * E][2]: (token, expert) pairs to recompute in gemm_cpu order
+    int32_t *cnt;         // [0] pairs, [1] flagged tokens (zeroed by the logits launch)
+    int32_t *flagged;     // [T]: tokens whose routing waits for their exact logits
+    float margin_scale;   // 1; larger values widen every interval (tests of the exact path)
+};
+
+// Routing of token t by one wave; lane l holds experts l + 64 i, i < NV.
+//   MODE 0: route on the sum (in slice order) of the nsplit logit slices.
+//   MODE 1 (certified): the slices are the bf16 MFMA router's.  With
+//     u = 2^-24, the gemm_cpu sum L_ref of exact bf16 products p_k differs
+//     from the exact sum by at most u sum_k |S_k| (S_k its partial sums,
+//     each add rounding by at most u |S_k|).  For k in the 32-wide block
+//     starting at j0, |S_k| <= |S_j0| + a_j (a_j the block's sum of |p|),
+//     so sum_k |S_k| <= 32 sum_j |S_j0| + 32 A.  The MFMA's own result is
+//     allowed 66 u (|acc| + a_j) per instruction: 33 additions of at most
+//     one unit in the last place of a magnitude below |acc| + a_j, whatever
+//     the hardware's internal order and rounding (truncation included).
+//     Slice s starts its accumulator at 0 while L_ref's partial sums carry
+//     P_s (the slices before it), which adds 32 n_s |P_s| for its n_s
+//     blocks; summing the slices rounds by at most u |P_s+1| per add.  Hence
+//       |L - L_ref| <= delta = u (1 + 2^-4) (sum_s D_s + (32 n_s + 1) sum_s |P_s|
+//                                            + |L|),
+//     the factor absorbing second-order terms (errors of the tracked |acc|,
+//     of A's own MFMA, f32 rounding of the bound).  The sigmoid is
+//     1/4-Lipschitz and xs_sigmoid is within 2^-22 of it over all floats, and
+//     the bias add rounds by at most 2^-24 (|key| + 1), so the reference's
+//     key lies in [key - m, key + m] with
+//       m = (delta / 4)(1 + 2^-8) + 2^-20 + 2^-22 |bias|.
+//     Let T be the top-k on these keys and U the experts whose interval
+//     meets the interval of another expert where either is in T.  Every
+//     expert outside T and U lies below all of T under the reference's keys
+//     too, and every pair in T + U with a member outside U is ordered the
+//     same by both keys, so recomputing the logits of U in gemm_cpu order and
+//     routing again on the mixed keys gives the reference's top-k, order and
+//     ties included.  A token with U empty is routed here; otherwise its
+//     pairs (t, e in U) and the token are listed, its logit row goes to flog,
+//     and routing waits for MODE 2.  Group-limited routing is certified at the
+//     group step the same way (group scores bounded by the top-2 sums of the
+//     interval ends); when that step is not settled, or a logit or bound is
+//     not finite, every expert of the token is recomputed.
+//   MODE 2: route on flog (the exact logits of U patched in).
+template <int NV, int MODE>
+__device__ __forceinline__ void route_token(int t, int lane, const float *__restrict__ logits,
+                                            const float *__restrict__ bias, int Tn, int E, int k, int n_group,
+                                            int topk_group, int renorm, float scaling, int32_t *__restrict__ idx,
+                                            float *__restrict__ wout, uint32_t *__restrict__ mask, int mask_words,
+                                            int nsplit, float *__restrict__ logits_out, const CertArgs &ca)
+{
+    float s[NV], key[NV], lgv[NV];
+    float lo[NV], hi[NV];   // MODE 1: the interval of the reference's key
+    bool ok[NV], valid[NV];
+    bool bad = false;       // MODE 1: a non-finite logit or bound, or an unsettled group step
     const size_t TE = (size_t)Tn * E;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         int e = lane + 64 * i;
-        ok[i] = e < E;
-        // split-K partials of the router GEMM, summed in slice order
-        float lg = 0.0f;
+        ok[i] = valid[i] = e < E;
+        float lg = 0.0f, mm = 0.0f;
         if (ok[i]) {
-            float part[kMaxSplits];
+            if constexpr (MODE == 2) {
+                lg = ca.flog[(size_t)t * E + e];
+            } else {
+                // split-K partials of the router GEMM, summed in slice order
+                float part[kMaxSplits], dp[kMaxSplits];
 #pragma unroll
-            for (int sp = 0; sp < kMaxSplits; ++sp)
-                if (sp < nsplit) part[sp] = logits[sp * TE + (size_t)t * E + e];
-            lg = part[0];
+                for (int sp = 0; sp < kMaxSplits; ++sp)
+                    if (sp < nsplit) {
+                        part[sp] = logits[sp * TE + (size_t)t * E + e];
+                        if constexpr (MODE == 1) dp[sp] = ca.dpart[sp * TE + (size_t)t * E + e];
+                    }
+                lg = part[0];
+                float dsum = 0.0f, carry = 0.0f;
+                if constexpr (MODE == 1) dsum = dp[0];
 #pragma unroll
-            for (int sp = 1; sp < kMaxSplits; ++sp)
-                if (sp < nsplit) lg = __fadd_rn(lg, part[sp]);
-            if (logits_out) logits_out[(size_t)t * E + e] = lg;
+                for (int sp = 1; sp < kMaxSplits; ++sp)
+                    if (sp < nsplit) {
+                        if constexpr (MODE == 1) {
+                            carry += __builtin_fabsf(lg);
+                            dsum += dp[sp];
+                        }
+                        lg = __fadd_rn(lg, part[sp]);
+                    }
+                if constexpr (MODE == 1) {
+                    const float delta = 0x1.1p-24f * (dsum + 32.0f * (float)ca.kblocks * carry + carry +
+                                                      __builtin_fabsf(lg)) + 0x1p-100f;
+                    mm = 0.25f * delta * 1.00390625f * ca.margin_scale + 0x1p-20f +
+                         (bias ? 0x1p-22f * __builtin_fabsf(bias[e]) : 0.0f);
+                    if (!__builtin_isfinite(lg) || !__builtin_isfinite(mm)) bad = true;
+                }
+            }
         }
+        lgv[i] = lg;
         s[i] = xs_sigmoid(lg);
         key[i] = (ok[i] && bias) ? __fadd_rn(s[i], bias[e]) : s[i];
+        lo[i] = key[i] - mm;
+        hi[i] = key[i] + mm;
     }
     if (n_group > 1) {
         const int gs = E / n_group;
-        float my_score = -__builtin_inff();
+        float my_score = -__builtin_inff(), my_lo = -__builtin_inff(), my_hi = -__builtin_inff();
         for (int gidx = 0; gidx < n_group; ++gidx) {
-            // top-2 keys of the group: lane-local, then a wave merge of pairs
-            float b1 = -__builtin_inff(), b2 = -__builtin_inff();
+            // top-2 keys of the group (MODE 1: also of the interval ends):
+            // lane-local, then a wave merge of pairs
+            float b[3][2];
+#pragma unroll
+            for (int q = 0; q < 3; ++q) b[q][0] = b[q][1] = -__builtin_inff();
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
                 int e = lane + 64 * i;
                 if (ok[i] && e / gs == gidx) {
-                    if (key[i] > b1) { b2 = b1; b1 = key[i]; }
-                    else if (key[i] > b2) b2 = key[i];
+#pragma unroll
+                    for (int q = 0; q < (MODE == 1 ? 3 : 1); ++q) {
+                        const float v = q == 0 ? key[i] : (q == 1 ? lo[i] : hi[i]);
+                        if (v > b[q][0]) { b[q][1] = b[q][0]; b[q][0] = v; }
+                        else if (v > b[q][1]) b[q][1] = v;
+                    }
                 }
             }
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                float c1 = __shfl_xor(b1, o, WAVE), c2 = __shfl_xor(b2, o, WAVE);
-                float n1 = fmaxf(b1, c1);
-                float n2 = fmaxf(fminf(b1, c1), fmaxf(b2, c2));
-                b1 = n1;
-                b2 = n2;
+            for (int q = 0; q < (MODE == 1 ? 3 : 1); ++q) {
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) {
+                    float c1 = __shfl_xor(b[q][0], o, WAVE), c2 = __shfl_xor(b[q][1], o, WAVE);
+                    float n1 = fmaxf(b[q][0], c1);
+                    float n2 = fmaxf(fminf(b[q][0], c1), fmaxf(b[q][1], c2));
+                    b[q][0] = n1;
+                    b[q][1] = n2;
+                }
             }
-            if (lane == gidx) my_score = __fadd_rn(b1, b2);
+            if (lane == gidx) {
+                my_score = __fadd_rn(b[0][0], b[0][1]);
+                if constexpr (MODE == 1) {
+                    // the top-2 sum is increasing in every key; its rounding is
+                    // below 2^-22 (1 + |sum|)
+                    const float l2 = b[1][0] + b[1][1], h2 = b[2][0] + b[2][1];
+                    my_lo = l2 - 0x1p-22f * (1.0f + __builtin_fabsf(l2));
+                    my_hi = h2 + 0x1p-22f * (1.0f + __builtin_fabsf(h2));
+                }
+            }
         }
         // keep the topk_group best groups (ties -> lower group index)
         uint64_t keep = 0;
@@ -502,12 +724,20 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ lo
             c = wave_best(c);
             keep |= 1ull << c.e;
         }
+        if constexpr (MODE == 1) {
+            // settled when every kept group's score is surely above every other's
+            const bool kept = lane < n_group && ((keep >> lane) & 1ull);
+            const float kl = wave_minf(kept ? my_lo : __builtin_inff());
+            const float nh = wave_max((lane < n_group && !kept) ? my_hi : -__builtin_inff());
+            if (!(kl > nh)) bad = true;
+        }
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             int e = lane + 64 * i;
             if (ok[i]) ok[i] = (keep >> (e / gs)) & 1ull;
         }
     }
+    if constexpr (MODE == 1) bad = __builtin_amdgcn_readfirstlane((int)__any(bad)) != 0;
     // top-k: k rounds of a wave arg-max over 64-bit ranks (order-preserving
     // key bits, then the complement of the expert index: ties go to the lower
     // index, as in the reference's comparison); empty candidates rank 0
@@ -516,7 +746,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ lo
     for (int i = 0; i < NV; ++i) rk[i] = ok[i] ? route_rank(key[i], lane + 64 * i) : 0ull;
     // lane j keeps pick j; the weight denominator is summed in pick order
     int my_e = -1;
-    float my_s = 0.0f, denom = 0.0f;
+    float my_s = 0.0f, denom = 0.0f, my_lo = 0.0f, my_hi = 0.0f, min_lo = __builtin_inff();
 #pragma unroll 1
     for (int j = 0; j < k; ++j) {
         uint64_t b = rk[0];
@@ -524,17 +754,86 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ lo
         for (int i = 1; i < NV; ++i) b = rk[i] > b ? rk[i] : b;
         b = wave_max_u64(b);
         const int e = b ? (int)(0xffffffffu - (uint32_t)b) : -1;
-        // the winner's score, from its lane
-        float sv = 0.0f;
+        // the winner's score (and interval), from its lane
+        float sv = 0.0f, lv = 0.0f, hv = 0.0f;
 #pragma unroll
         for (int i = 0; i < NV; ++i)
-            if ((e >> 6) == i) sv = s[i];
+            if ((e >> 6) == i) {
+                sv = s[i];
+                lv = lo[i];
+                hv = hi[i];
+            }
         sv = e >= 0 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), e & 63)) : 0.0f;
+        if constexpr (MODE == 1) {
+            lv = e >= 0 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lv), e & 63)) : 0.0f;
+            hv = e >= 0 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, hv), e & 63)) : 0.0f;
+            min_lo = fminf(min_lo, lv);
+        }
         denom = __fadd_rn(denom, sv);
-        if (lane == j) { my_e = e; my_s = sv; }
+        if (lane == j) { my_e = e; my_s = sv; my_lo = lv; my_hi = hv; }
 #pragma unroll
         for (int i = 0; i < NV; ++i)
             if (lane + 64 * i == e) rk[i] = 0ull;
+    }
+    if constexpr (MODE == 1) {
+        // U: non-picks whose interval reaches the lowest pick's, picks that
+        // reach a non-pick's or another pick's
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            if (rk[i]) mx = fmaxf(mx, hi[i]);
+        const float max_hi = wave_max(mx);
+        int n_amb = 0;
+        uint32_t amb_bits = 0;   // bit i: expert lane + 64 i is in U (non-picks, or all when bad)
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            if (bad ? valid[i] : (rk[i] && hi[i] >= min_lo)) {
+                amb_bits |= 1u << i;
+                ++n_amb;
+            }
+        bool pick_amb = false;
+        if (!bad) {   // wave-uniform: every lane takes part in the readlanes
+            const bool mine = lane < k && my_e >= 0;
+            if (mine && my_lo <= max_hi) pick_amb = true;
+            for (int jj = 0; jj < k; ++jj) {
+                const float l2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_lo), jj));
+                const float h2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_hi), jj));
+                const int e2 = __builtin_amdgcn_readlane(my_e, jj);
+                if (mine && jj != lane && e2 >= 0 && my_lo <= h2 && l2 <= my_hi) pick_amb = true;
+            }
+        }
+        n_amb += pick_amb ? 1 : 0;
+        const int incl = wave_prefix(n_amb, lane);
+        const int total = __builtin_amdgcn_readlane(incl, 63);
+        if (total > 0) {
+            int pbase = 0;
+            if (lane == 0) {
+                pbase = atomicAdd(&ca.cnt[0], total);
+                ca.flagged[atomicAdd(&ca.cnt[1], 1)] = t;
+            }
+            pbase = __builtin_amdgcn_readlane(pbase, 0);
+            int o = pbase + incl - n_amb;
+#pragma unroll
+            for (int i = 0; i < NV; ++i)
+                if ((amb_bits >> i) & 1u) {
+                    ca.pairs[2 * (size_t)o] = t;
+                    ca.pairs[2 * (size_t)o + 1] = lane + 64 * i;
+                    ++o;
+                }
+            if (pick_amb) {
+                ca.pairs[2 * (size_t)o] = t;
+                ca.pairs[2 * (size_t)o + 1] = my_e;
+            }
+#pragma unroll
+            for (int i = 0; i < NV; ++i)
+                if (valid[i]) ca.flog[(size_t)t * E + lane + 64 * i] = lgv[i];
+            return;   // routed by MODE 2 once the pairs are exact
+        }
+    }
+    if (logits_out) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            if (valid[i]) logits_out[(size_t)t * E + lane + 64 * i] = lgv[i];
     }
     if (lane < k) {
         const float wv = renorm ? __fmul_rn(__fdiv_rn(my_s, denom), scaling) : __fmul_rn(my_s, scaling);
@@ -544,31 +843,86 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ lo
     }
 }
 
+// One wave per token (MODE 0, 1), or per listed token (MODE 2: the flagged
+// tokens, a grid-stride loop over their count).
+template <int NV, int MODE>
+__global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ logits,
+                                                    const float *__restrict__ bias, int Tn, int E,
+                                                    int k, int n_group, int topk_group, int renorm,
+                                                    float scaling, int32_t *__restrict__ idx,
+                                                    float *__restrict__ wout,
+                                                    uint32_t *__restrict__ mask, int mask_words,
+                                                    int nsplit, float *__restrict__ logits_out, CertArgs ca)
+{
+    const int lane = threadIdx.x & 63;
+    const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if constexpr (MODE == 2) {
+        const int n = ca.cnt[1];
+        for (int j = w; j < n; j += gridDim.x * 4)
+            route_token<NV, 2>(ca.flagged[j], lane, logits, bias, Tn, E, k, n_group, topk_group, renorm, scaling,
+                               idx, wout, mask, mask_words, 1, logits_out, ca);
+    } else {
+        if (w >= Tn) return;
+        route_token<NV, MODE>(w, lane, logits, bias, Tn, E, k, n_group, topk_group, renorm, scaling, idx, wout,
+                              mask, mask_words, nsplit, logits_out, ca);
+    }
+}
+
 int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,
                  int64_t n_group, int64_t topk_group, int renorm, float scaling, int32_t *idx,
                  float *w, uint32_t *mask, int mask_words, int nsplit, float *logits_out,
-                 hipStream_t st)
+                 hipStream_t st, const CertState *cert, int mode)
 {
     if (T == 0) return XS_OK;
-    dim3 grid((unsigned)((T + 3) / 4)), block(256);
+    CertArgs ca = {};
+    if (cert) {
+        ca.dpart = cert->dpart;
+        ca.kblocks = cert->kblocks;
+        ca.flog = cert->flog;
+        ca.pairs = cert->pairs;
+        ca.cnt = cert->cnt;
+        ca.flagged = cert->flagged;
+        ca.margin_scale = cert->margin_scale;
+    }
+    // MODE 2 loops over the flagged tokens: a grid for a quarter of them at most
+    dim3 grid((unsigned)(mode == 2 ? std::min((T + 3) / 4, (int64_t)256) : (T + 3) / 4)), block(256);
     int nv = (int)((E + 63) / 64);
-#define XS_ROUTE(NVV)                                                                       \
-    route_kernel<NVV><<<grid, block, 0, st>>>(logits, bias, (int)T, (int)E, (int)k,         \
-                                              (int)n_group, (int)topk_group, renorm, scaling, \
-                                              idx, w, mask, mask_words, nsplit, logits_out)
-    if (nv <= 1) XS_ROUTE(1);
-    else if (nv <= 2) XS_ROUTE(2);
-    else if (nv <= 4) XS_ROUTE(4);
-    else if (nv <= 8) XS_ROUTE(8);
-    else XS_ROUTE(16);
+#define XS_ROUTE(NVV, M)                                                                         \
+    route_kernel<NVV, M><<<grid, block, 0, st>>>(logits, bias, (int)T, (int)E, (int)k,           \
+                                                 (int)n_group, (int)topk_group, renorm, scaling, \
+                                                 idx, w, mask, mask_words, nsplit, logits_out, ca)
+#define XS_ROUTE_NV(M)                       \
+    if (nv <= 1) XS_ROUTE(1, M);             \
+    else if (nv <= 2) XS_ROUTE(2, M);        \
+    else if (nv <= 4) XS_ROUTE(4, M);        \
+    else if (nv <= 8) XS_ROUTE(8, M);        \
+    else XS_ROUTE(16, M);
+    if (mode == 1) {
+        XS_ROUTE_NV(1)
+    } else if (mode == 2) {
+        XS_ROUTE_NV(2)
+    } else {
+        XS_ROUTE_NV(0)
+    }
+#undef XS_ROUTE_NV
 #undef XS_ROUTE
     XS_LAUNCH_CHECK();
     return XS_OK;
 }
 
+// Router kinds by params.router_exact and the input dtype: 0 the bf16 MFMA
+// router (approximate); 1 exact routing: bf16 inputs take the certified MFMA
+// router (route_token MODE 1) plus the chain kernel for the pairs it lists;
+// 2, and f32 inputs, the chain kernel for every logit.
+int router_kind(int exact, int dtype)
+{
+    if (dtype == XS_F32 || exact >= 2) return XS_ROUTER_CHAIN;
+    return exact == 1 ? XS_ROUTER_CERTIFIED : XS_ROUTER_MFMA;
+}
+
 int router_logits_splits(int64_t T, int64_t H, int exact, int dtype)
 {
-    if (exact || dtype == XS_F32) return 1;
+    if (router_kind(exact, dtype) == XS_ROUTER_CHAIN) return 1;
     // decode: enough K slices to fill the GPU; prefill (tiled kernel, 64-wide
     // K steps): 2 slices from 2048 tokens, 4 below
     int ns = T <= 64 ? 16 : (T <= 256 ? 8 : (T < 2048 ? 4 : 2));
@@ -578,49 +932,73 @@ int router_logits_splits(int64_t T, int64_t H, int exact, int dtype)
 
 bool router_quantizes(int64_t T, int exact, int dtype)
 {
-    return !exact && dtype == XS_BF16 && T <= 256;   // the decode (router_logits_mfma_kernel) path
+    // the decode (router_logits_mfma_kernel) path
+    return router_kind(exact, dtype) != XS_ROUTER_CHAIN && T <= 256;
 }
 
 int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
                          int exact, float *logits, int nsplit, hipStream_t st, uint32_t *mask_clear,
-                         int64_t mask_words, uint8_t *q, float *qs)
+                         int64_t mask_words, uint8_t *q, float *qs, const CertState *cert)
 {
     if (q && !router_quantizes(T, exact, dtype))
         return set_error(XS_ERR_INVALID, "router: the activation quant is folded into the decode path only");
     if (T == 0) return XS_OK;
-    if (exact || dtype == XS_F32) {
-        // one token per lane while the chains' latency is the cost (measured up to
-        // 256 tokens: 4 per lane was 2.5x slower there), four for large batches
+    const int kind = router_kind(exact, dtype);
+    if (kind == XS_ROUTER_CHAIN || (kind == XS_ROUTER_CERTIFIED && !cert)) {
+        // every logit in gemm_cpu order (a certified router needs the routing
+        // stage: without it, the logits alone are computed exactly)
         if (dtype == XS_F32)
-            return T <= 2048 ? launch_exact<float, 1>((const float *)x, (const float *)wr, T, E, H, logits, mask_clear,
-                                                    mask_words, st)
-                           : launch_exact<float, 4>((const float *)x, (const float *)wr, T, E, H, logits, mask_clear,
-                                                    mask_words, st);
-        return T <= 2048 ? launch_exact<uint16_t, 1>((const uint16_t *)x, (const uint16_t *)wr, T, E, H, logits,
-                                                   mask_clear, mask_words, st)
-                       : launch_exact<uint16_t, 4>((const uint16_t *)x, (const uint16_t *)wr, T, E, H, logits,
-                                                   mask_clear, mask_words, st);
-    } else if (T > 256) {
+            return launch_chain<float>((const float *)x, (const float *)wr, T, E, H, nullptr, nullptr, T * E, logits,
+                                       mask_clear, mask_words, st);
+        return launch_chain<uint16_t>((const uint16_t *)x, (const uint16_t *)wr, T, E, H, nullptr, nullptr, T * E,
+                                      logits, mask_clear, mask_words, st);
+    }
+    const bool c = kind == XS_ROUTER_CERTIFIED;
+    float *dpart = c ? cert->dpart : nullptr;
+    int32_t *zero = c ? cert->cnt : nullptr;
+    const int zero_n = c ? 2 : 0;
+    if (T > 256) {
         // prefill: 128 tokens x 128 experts per block through an LDS ring, K split nsplit ways
-        static bool attr_set = false;
-        if (!attr_set) {
-            XS_HIP(hipFuncSetAttribute((const void *)router_logits_tile_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kRtNST * kRtStage));
-            attr_set = true;
+        static bool attr_set[2] = {false, false};
+        const void *fn = c ? (const void *)router_logits_tile_kernel<true> : (const void *)router_logits_tile_kernel<false>;
+        if (!attr_set[c]) {
+            XS_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kRtNST * kRtStage));
+            attr_set[c] = true;
         }
         dim3 grid((unsigned)((E + kRtBE - 1) / kRtBE), (unsigned)((T + kRtBT - 1) / kRtBT), (unsigned)nsplit), block(256);
-        router_logits_tile_kernel<<<grid, block, kRtNST * kRtStage, st>>>((const uint16_t *)x, (const uint16_t *)wr,
-                                                                          (int)T, (int)E, (int)H, (int)(H / nsplit),
-                                                                          logits, mask_clear, mask_words);
+        if (c)
+            router_logits_tile_kernel<true><<<grid, block, kRtNST * kRtStage, st>>>(
+                (const uint16_t *)x, (const uint16_t *)wr, (int)T, (int)E, (int)H, (int)(H / nsplit), logits,
+                mask_clear, mask_words, dpart, zero, zero_n);
+        else
+            router_logits_tile_kernel<false><<<grid, block, kRtNST * kRtStage, st>>>(
+                (const uint16_t *)x, (const uint16_t *)wr, (int)T, (int)E, (int)H, (int)(H / nsplit), logits,
+                mask_clear, mask_words, nullptr, nullptr, 0);
     } else {
         // decode: 32 tokens x 64 experts per block, K split nsplit ways
         dim3 grid((unsigned)((E + 63) / 64), (unsigned)((T + 31) / 32), (unsigned)nsplit), block(256);
-        router_logits_mfma_kernel<1, 2><<<grid, block, 0, st>>>((const uint16_t *)x, (const uint16_t *)wr,
-                                                                (int)T, (int)E, (int)H, (int)(H / nsplit), logits,
-                                                                mask_clear, mask_words, q, qs);
+        if (c)
+            router_logits_mfma_kernel<1, 2, true><<<grid, block, 0, st>>>(
+                (const uint16_t *)x, (const uint16_t *)wr, (int)T, (int)E, (int)H, (int)(H / nsplit), logits,
+                mask_clear, mask_words, q, qs, dpart, zero, zero_n);
+        else
+            router_logits_mfma_kernel<1, 2, false><<<grid, block, 0, st>>>(
+                (const uint16_t *)x, (const uint16_t *)wr, (int)T, (int)E, (int)H, (int)(H / nsplit), logits,
+                mask_clear, mask_words, q, qs, nullptr, nullptr, 0);
     }
     XS_LAUNCH_CHECK();
     return XS_OK;
+}
+
+int launch_router_fix(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
+                      const CertState &cert, hipStream_t st)
+{
+    if (T == 0) return XS_OK;
+    if (dtype == XS_F32)
+        return launch_chain<float>((const float *)x, (const float *)wr, T, E, H, cert.pairs, cert.cnt, T * E,
+                                   cert.flog, nullptr, 0, st);
+    return launch_chain<uint16_t>((const uint16_t *)x, (const uint16_t *)wr, T, E, H, cert.pairs, cert.cnt, T * E,
+                                  cert.flog, nullptr, 0, st);
 }
 
 // ---------------------------------------------------- activation quantizers

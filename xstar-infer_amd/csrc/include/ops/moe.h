@@ -29,7 +29,12 @@
  *                    into the activation quantization (ops/rmsnorm.h numerics)
  *   returns          [..., H], dtype of x, device CUDA
  *
- * Numerics: routing bit-exact with the CPU restatement given the logits;
+ *   router           0 bf16 MFMA logits (approximate routing); 1 (default)
+ *                    certified: top-k indices, order and counts bit-exact with
+ *                    the reference's gemm_cpu logits; 2 every logit in
+ *                    gemm_cpu order (xs_moe.h, XS_ROUTER_*)
+ *
+ * Numerics: routing bit-exact with the CPU restatement (router 1 or 2);
  * expert GEMMs in FP8 (or MXFP4 x MXFP8) with f32 accumulation; SwiGLU in f32
  * (branched sigmoid, xstar_cpp/src/ops/mlp.cpp:10-26); combine in f32 with one
  * cast to the output dtype.
@@ -44,7 +49,7 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
            const Tensor *shared_w13, const Tensor *shared_w13_scale,
            const Tensor *shared_w2, const Tensor *shared_w2_scale,
            std::int64_t top_k, std::int64_t n_group = 1, std::int64_t topk_group = 1,
-           bool renormalize = true, float routed_scaling = 1.0f, bool router_exact = false,
+           bool renormalize = true, float routed_scaling = 1.0f, int router = 1,
            const Tensor *norm_weight = nullptr, float norm_eps = 1e-6f, const Tensor *residual = nullptr);
 
 /**
@@ -59,7 +64,7 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
  */
 Tensor moe_block_ffn(const Tensor &h, const Tensor &ln2_w, float eps, const MoeLayerWeights &w, std::int64_t top_k,
                      std::int64_t n_group = 1, std::int64_t topk_group = 1, bool renormalize = true,
-                     float routed_scaling = 1.0f, bool router_exact = false);
+                     float routed_scaling = 1.0f, int router = 1);
 
 /** Router logits x . router_w^T in f32 ([T, E]); exact: bit-identical to
  * gemm_cpu's sequential accumulation (xstar_cpp/include/ops/gemm.h:57-83). */

@@ -42,7 +42,7 @@ static Tensor moe_core(const Tensor &x, const Tensor &router_w, const Tensor *ro
                        const Tensor *shared_w13, const Tensor *shared_w13_scale,
                        const Tensor *shared_w2, const Tensor *shared_w2_scale,
                        std::int64_t top_k, std::int64_t n_group, std::int64_t topk_group,
-                       bool renormalize, float routed_scaling, bool router_exact,
+                       bool renormalize, float routed_scaling, int router,
                        const Tensor *norm_weight, float norm_eps, const Tensor *residual, const Frag &frag)
 {
     // ---- dtype ----
@@ -115,7 +115,8 @@ static Tensor moe_core(const Tensor &x, const Tensor &router_w, const Tensor *ro
     p.x_dtype = code(x.dtype());
     p.routed_format = fp4 ? XS_FP4_E2M1X2 : XS_FP8_E4M3;
     p.has_shared = has_shared ? 1 : 0;
-    p.router_exact = router_exact ? 1 : 0;
+    if (router < XS_ROUTER_MFMA || router > XS_ROUTER_CHAIN) throw std::runtime_error("unsupported router");
+    p.router_exact = router;
     p.has_norm = norm_weight ? 1 : 0;
     p.norm_eps = norm_eps;
     std::size_t wsb = xs_moe_workspace_size(&p);
@@ -173,17 +174,17 @@ Tensor moe(const Tensor &x, const Tensor &router_w, const Tensor *router_bias,
            const Tensor *shared_w13, const Tensor *shared_w13_scale,
            const Tensor *shared_w2, const Tensor *shared_w2_scale,
            std::int64_t top_k, std::int64_t n_group, std::int64_t topk_group,
-           bool renormalize, float routed_scaling, bool router_exact,
+           bool renormalize, float routed_scaling, int router,
            const Tensor *norm_weight, float norm_eps, const Tensor *residual)
 {
     return moe_core(x, router_w, router_bias, w13, w13_scale, w2, w2_scale, shared_w13, shared_w13_scale, shared_w2,
-                    shared_w2_scale, top_k, n_group, topk_group, renormalize, routed_scaling, router_exact, norm_weight,
+                    shared_w2_scale, top_k, n_group, topk_group, renormalize, routed_scaling, router, norm_weight,
                     norm_eps, residual, Frag{});
 }
 
 Tensor moe_block_ffn(const Tensor &h, const Tensor &ln2_w, float eps, const MoeLayerWeights &w, std::int64_t top_k,
                      std::int64_t n_group, std::int64_t topk_group, bool renormalize, float routed_scaling,
-                     bool router_exact)
+                     int router)
 {
     // packed-only layers (pack_moe_layer_frag(w, true)) carry their shapes and
     // dtypes in the packed tensors
@@ -197,7 +198,7 @@ Tensor moe_block_ffn(const Tensor &h, const Tensor &ln2_w, float eps, const MoeL
     const Tensor &w13 = only ? *w.w13_frag : *w.w13, &w2 = only ? *w.w2_frag : *w.w2;
     const Tensor *sw13 = only ? p(w.shared_w13_frag) : p(w.shared_w13), *sw2 = only ? p(w.shared_w2_frag) : p(w.shared_w2);
     return moe_core(h, *w.router_w, p(w.router_bias), w13, *w.w13_scale, w2, *w.w2_scale, sw13, p(w.shared_w13_scale),
-                    sw2, p(w.shared_w2_scale), top_k, n_group, topk_group, renormalize, routed_scaling, router_exact,
+                    sw2, p(w.shared_w2_scale), top_k, n_group, topk_group, renormalize, routed_scaling, router,
                     &ln2_w, eps, &h, f);
 }
 

@@ -15,6 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "xstar_cpp_py", "libxs_moe.so")
 
 XS_F32, XS_BF16, XS_FP8_E4M3, XS_FP4_E2M1X2, XS_E8M0, XS_I32 = range(6)
+XS_ROUTER_MFMA, XS_ROUTER_CERTIFIED, XS_ROUTER_CHAIN = range(3)
 
 P = C.c_void_p
 I64 = C.c_int64
@@ -314,15 +315,21 @@ class MoeLayer:
 
     def __init__(self, router_w, w13, w13_scale, w2, w2_scale, top_k, router_bias=None,
                  shared=None, routed_format=XS_FP8_E4M3, n_group=1, topk_group=1,
-                 renormalize=True, routed_scaling=1.0, router_exact=False, norm_weight=None,
-                 norm_eps=1e-6, frag=False):
+                 renormalize=True, routed_scaling=1.0, router_exact=None, norm_weight=None,
+                 norm_eps=1e-6, frag=False, router=None):
         self.router_w, self.router_bias = router_w, router_bias
         self.norm_weight, self.norm_eps = norm_weight, norm_eps
         self.w13, self.w13_scale, self.w2, self.w2_scale = _u8(w13), w13_scale, _u8(w2), w2_scale
         self.shared = None if shared is None else (_u8(shared[0]), shared[1], _u8(shared[2]), shared[3])
         self.top_k, self.routed_format = top_k, routed_format
         self.n_group, self.topk_group = n_group, topk_group
-        self.renormalize, self.routed_scaling, self.router_exact = renormalize, routed_scaling, router_exact
+        # router: XS_ROUTER_MFMA / _CERTIFIED / _CHAIN (default certified: the
+        # reference's top-k bit for bit).  router_exact=True / False, the older
+        # switch, picks the chain router (gemm_cpu logits) / the MFMA router.
+        if router is None:
+            router = XS_ROUTER_CERTIFIED if router_exact is None else (
+                XS_ROUTER_CHAIN if router_exact else XS_ROUTER_MFMA)
+        self.renormalize, self.routed_scaling, self.router_exact = renormalize, routed_scaling, int(router)
         self.E, self.H = router_w.shape
         self.I = w2.shape[-1] * (2 if routed_format == XS_FP4_E2M1X2 else 1)
         self._ws = None
