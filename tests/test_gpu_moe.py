@@ -31,15 +31,23 @@ def _debug(T, E, k):
 
 
 def _run_and_check(c, g, router_exact, tol=TOL, rows=None):
+    """router_exact: True the chain router (logits bit-exact), False the MFMA
+    router (routing checked given its logits), "certified" the default router
+    (routing checked against the oracle's from x, weights given the logits it
+    routed on)."""
     T, E, k = c["T"], c["E"], c["k"]
-    layer = layer_for(c, g, router_exact=router_exact)
+    cert = router_exact == "certified"
+    layer = layer_for(c, g, router_exact=None, router=1) if cert else layer_for(c, g, router_exact=router_exact)
     dbg = _debug(T, E, k)
     out = layer.forward(g["x"], debug=dbg)
     torch.cuda.synchronize()
     d = {n: t.cpu().numpy() for n, t in dbg.items()}
-    r = oracle_forward(c, logits_in=None if router_exact else d["logits"])
-    if router_exact:
+    r = oracle_forward(c, logits_in=None if router_exact is True else d["logits"])
+    if router_exact is True:
         assert np.array_equal(d["logits"], r["logits"])
+    if cert:
+        xidx, _ = oracle.route(oracle.router_logits(c["x"], c["router_w"], c["x"].dtype == np.uint16), c["bias"], k)
+        assert np.array_equal(d["topk_idx"], xidx)     # the reference's top-k from x, bit for bit
     assert np.array_equal(d["topk_idx"], r["idx"])
     assert np.array_equal(d["topk_w"], r["w"])
     assert np.array_equal(d["counts"], r["counts"])
@@ -296,19 +304,61 @@ def test_moe_fp4_small(T, mode, monkeypatch):
 def test_moe_v4_decode_full_shape(T):
     """C4 at full V4-Flash shape: H=4096, I=2048, 256 experts top-6 + shared."""
     c, g = make_case_gpu(T, 4096, 2048, 256, 6, seed=40 + T)
+    _run_and_check(c, g, router_exact="certified")
     _run_and_check(c, g, router_exact=False)
 
 
 def test_moe_v4_decode_zero_bias():
     """C4 as specified: uniform routing with zero router bias, 16 tokens."""
     c, g = make_case_gpu(16, 4096, 2048, 256, 6, seed=44, bias_std=0)
-    _run_and_check(c, g, router_exact=False)
+    _run_and_check(c, g, router_exact="certified")
 
 
 def test_moe_fp4_full_shape():
     """C5 shape (H=4096, I=2048, 256 MXFP4 experts top-6 + FP8 shared) at 32 tokens."""
     c, g = make_case_gpu(32, 4096, 2048, 256, 6, seed=7, fp4=True)
-    _run_and_check(c, g, router_exact=False)
+    _run_and_check(c, g, router_exact="certified")
+
+
+@pytest.mark.parametrize("T", [16, 700])
+def test_certified_router_exact_pass_everywhere(T, monkeypatch):
+    """XS_ROUTER_MARGIN widens every key interval, so every token takes the
+    certified router's exact pass (the chain kernel over all its pairs, then
+    routing on the patched rows): the logits it routed on are the oracle's
+    gemm_cpu logits bit for bit, and routing and output follow; decode (split-K
+    MFMA kernel) and prefill (tile kernel) logits."""
+    monkeypatch.setenv("XS_ROUTER_MARGIN", "1e30")
+    c = make_case(T, 1024, 256, 64, 6, seed=60 + T)
+    g = to_device(c)
+    T_, E, k = c["T"], c["E"], c["k"]
+    layer = layer_for(c, g, router_exact=None, router=1)
+    dbg = _debug(T_, E, k)
+    out = layer.forward(g["x"], debug=dbg)
+    torch.cuda.synchronize()
+    r = oracle_forward(c)
+    assert np.array_equal(dbg["logits"].cpu().numpy(), r["logits"])
+    assert np.array_equal(dbg["topk_idx"].cpu().numpy(), r["idx"])
+    assert np.array_equal(dbg["topk_w"].cpu().numpy(), r["w"])
+    assert max_abs_rel(out.float().cpu().numpy(), r["out_f32"]) <= TOL
+
+
+@pytest.mark.parametrize("T", [1, 64, 1000])
+def test_certified_router_small_layers(T):
+    """The default router on small layers, with ties (duplicated router rows
+    and biases) that always need the exact pass, and group-limited routing."""
+    c = make_case(T, 512, 256, 64, 6, seed=70 + T)
+    c["router_w"][48:] = c["router_w"][:16]
+    c["bias"][48:] = c["bias"][:16]
+    g = to_device(c)
+    _run_and_check(c, g, router_exact="certified")
+    import xs_moe_capi as X
+    layer = X.MoeLayer(g["router_w"], g["w13"], g["s13"], g["w2"], g["s2"], 6, router_bias=g["bias"],
+                       shared=g["shared"], n_group=8, topk_group=3)
+    dbg = _debug(T, 64, 6)
+    layer.forward(g["x"], debug=dbg)
+    torch.cuda.synchronize()
+    xidx, _ = oracle.route(oracle.router_logits(c["x"], c["router_w"], True), c["bias"], 6, n_group=8, topk_group=3)
+    assert np.array_equal(dbg["topk_idx"].cpu().numpy(), xidx)
 
 
 def _full_size_check(c, g, T, E, k, bm, exact=False):
@@ -371,14 +421,13 @@ def test_moe_prefill_full_size_properties():
     assert max_abs_rel(got, r["out_f32"]) <= TOL
     # sum of the routed weights per token is 1 (renormalised)
     assert np.allclose(d["topk_w"].sum(1), 1.0, rtol=1e-5)
-    # the bf16 MFMA router against the reference's routing from x: tokens whose
-    # top-6 set or order differs (the MFMA accumulation order moves logits by
-    # a few ulps, which flips near-ties)
+    # the default (certified) router against the reference's routing from x:
+    # no token routes differently
     xlog = oracle.router_logits(c["x"], c["router_w"], True)
     xidx, _ = oracle.route(xlog, c["bias"], k)
     flips = int((xidx != d["topk_idx"]).any(1).sum())
-    print(f"C3 MFMA router: {flips} of {T} tokens route differently from the reference logits")
-    assert flips <= T // 100
+    print(f"C3 certified router: {flips} of {T} tokens route differently from the reference logits")
+    assert flips == 0
 
 
 def test_moe_prefill_exact_router_full_size():
