@@ -334,7 +334,7 @@ int xs_moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *worksp
  * Callers compare xs_moe_workspace_size(p) with xs_moe_noalloc_scratch_bytes():
  * the size is not monotonic in T (tile and stream-K regions change with the
  * kernels chosen), so no token count is a bound.  Examples at the V4-Flash
- * shape: FP8 T = 256 needs 50.7 MiB, MXFP4 T = 210 about 61 MiB.  Calls nothing that
+ * shape with the default router: FP8 T = 256 needs 53.5 MiB, MXFP4 T = 200 62.2 MiB.  Calls nothing that
  * allocates.  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (different streams, or threads) race; calls in one
  * stream order are safe, because each forward re-arms what must start at zero.

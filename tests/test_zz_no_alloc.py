@@ -55,3 +55,29 @@ def test_noalloc_rejects_params_beyond_the_scratch():
     out = torch.empty_like(x)
     with pytest.raises(X.XsError, match="static scratch"):
         layer.forward_noalloc(x, out)
+
+
+@pytest.mark.parametrize("env,T1,T2,H,I,E,k", [
+    # stream-K counters and partial tiles (zeroed by the preceding launches)
+    ({"XS_MOE_STREAM": "1", "XS_STREAM_GROUPED": "0"}, 256, 40, 1024, 1024, 32, 6),
+    # the fused combine's per-(token, slab) counters on the tall tiles
+    ({"XS_MOE_GEMM": "wide", "XS_FUSE_COMBINE": "1"}, 700, 300, 1024, 1024, 16, 4),
+    # the certified router's pair and token counters, every token through the exact pass
+    ({"XS_ROUTER_MARGIN": "1e30"}, 200, 20, 1024, 512, 32, 6),
+])
+def test_noalloc_counters_are_rearmed(env, T1, T2, H, I, E, k, monkeypatch):
+    """State that must start at zero in every forward (stream-K counters, the
+    fused combine's counters, the certified router's list counters) lives in
+    the shared scratch: a larger forward and then a smaller one through the
+    scratch equal the workspace forward bit for bit."""
+    for n, v in env.items():
+        monkeypatch.setenv(n, v)
+    c = make_case(T1, H, I, E, k, seed=74, zipf=1.1)
+    g = to_device(c)
+    layer = layer_for(c, g, router_exact=None)
+    x1 = g["x"]
+    x2 = x1[:T2].clone()
+    a1, b1 = _both(layer, x1)
+    a2, b2 = _both(layer, x2)
+    assert torch.equal(a1, b1)
+    assert torch.equal(a2, b2)
