@@ -59,7 +59,7 @@ def test_noalloc_rejects_params_beyond_the_scratch():
 
 @pytest.mark.parametrize("env,T1,T2,H,I,E,k", [
     # stream-K counters and partial tiles (zeroed by the preceding launches)
-    ({"XS_MOE_STREAM": "1", "XS_STREAM_GROUPED": "0"}, 256, 40, 1024, 1024, 32, 6),
+    ({"XS_MOE_GEMM": "tiled", "XS_MOE_STREAM": "1", "XS_STREAM_GROUPED": "0"}, 256, 40, 1024, 1024, 32, 6),
     # the fused combine's per-(token, slab) counters on the tall tiles
     ({"XS_MOE_GEMM": "wide", "XS_FUSE_COMBINE": "1"}, 700, 300, 1024, 1024, 16, 4),
     # the certified router's pair and token counters, every token through the exact pass
@@ -75,6 +75,11 @@ def test_noalloc_counters_are_rearmed(env, T1, T2, H, I, E, k, monkeypatch):
     c = make_case(T1, H, I, E, k, seed=74, zipf=1.1)
     g = to_device(c)
     layer = layer_for(c, g, router_exact=None)
+    plan = layer.plan(T1)
+    if "XS_MOE_STREAM" in env:
+        assert plan["routed"] == "stream"
+    if "XS_FUSE_COMBINE" in env:
+        assert plan["fused_combine"]
     x1 = g["x"]
     x2 = x1[:T2].clone()
     a1, b1 = _both(layer, x1)
