@@ -59,7 +59,7 @@ def test_noalloc_rejects_params_beyond_the_scratch():
 
 @pytest.mark.parametrize("env,T1,T2,H,I,E,k", [
     # stream-K counters and partial tiles (zeroed by the preceding launches)
-    ({"XS_MOE_GEMM": "tiled", "XS_MOE_STREAM": "1", "XS_STREAM_GROUPED": "0"}, 256, 40, 1024, 1024, 32, 6),
+    ({"XS_MOE_GEMM": "tiled", "XS_MOE_STREAM": "1", "XS_STREAM_GROUPED": "0"}, 256, 40, 1024, 1024, 64, 4),
     # the fused combine's per-(token, slab) counters on the tall tiles
     ({"XS_MOE_GEMM": "wide", "XS_FUSE_COMBINE": "1"}, 700, 300, 1024, 1024, 16, 4),
     # the certified router's pair and token counters, every token through the exact pass
