@@ -84,11 +84,24 @@ struct Blk {
     std::barrier<> *wbar[16];
     uint64_t xch[16][64];
     uint8_t wx[16][64][64];
+    uint64_t xseq[16][64];   // per lane: how many wave exchanges it has entered
+    bool gone[16][64];       // lane has returned from the kernel
 };
 inline thread_local Blk *tb;
 inline thread_local std::deque<Op> tq;
 inline thread_local int32_t t_claims[64];
 inline thread_local int t_nclaim;
+inline thread_local uint64_t t_xseq = 0;
+// Wave exchanges (shuffles, readfirstlane, MFMA operand exchange) need every
+// live lane of the wave: on the card they are wave-wide, here each is a
+// barrier of the wave's lane threads.  A lane that skips one (divergent
+// control flow around a shuffle) would pair later exchanges wrongly, so each
+// lane counts the exchanges it enters and the first live lane checks that
+// all live lanes are at the same one, of the same kind (1 readfirstlane,
+// 2 shuffle, 3 MFMA, 4 first-lane read, 5 readlane / DPP / int shuffle, 6 any,
+// 7 ballot).
+inline void emu_xpost(int w, int l, int kind) { tb->xseq[w][l] = (++t_xseq << 8) | (uint64_t)kind; }
+inline void emu_xcheck(int w, int l);
 
 inline uint8_t *emu_smem() { return tb->smem; }
 // static __shared__ arrays: carved from the block's LDS in declaration order
@@ -106,6 +119,19 @@ inline T *emu_shared(size_t n)
 inline uint32_t lds_addr(const void *p) { return (uint32_t)((const uint8_t *)p - tb->smem); }
 
 inline void __syncthreads() { tb->bar->arrive_and_wait(); }
+inline void emu_xcheck(int w, int l)
+{
+    for (int i = 0; i < 64; ++i) {
+        if (tb->gone[w][i]) continue;
+        if (i != l) return;   // only the first live lane checks
+        break;
+    }
+    for (int i = 0; i < 64; ++i)
+        if (!tb->gone[w][i] && tb->xseq[w][i] != tb->xseq[w][l])
+            EMU_ERR("wave %d: lane %d is at exchange %llu (kind %d), lane %d at %llu (kind %d): a wave exchange under divergent control flow",
+                    w, i, (unsigned long long)(tb->xseq[w][i] >> 8), (int)(tb->xseq[w][i] & 255), l,
+                    (unsigned long long)(tb->xseq[w][l] >> 8), (int)(tb->xseq[w][l] & 255));
+}
 inline int wave_id() { return threadIdx.x / 64; }
 inline int lane_id() { return threadIdx.x % 64; }
 
@@ -114,7 +140,9 @@ inline uint64_t wave_first(uint64_t v, const char *what)
 {
     const int w = wave_id(), l = lane_id();
     tb->xch[w][l] = v;
+    emu_xpost(w, l, 1);
     tb->wbar[w]->arrive_and_wait();
+    emu_xcheck(w, l);
     const uint64_t r = tb->xch[w][0];
     if (r != v) EMU_ERR("non-uniform %s: lane %d has %llx, lane 0 %llx", what, l, (unsigned long long)v, (unsigned long long)r);
     tb->wbar[w]->arrive_and_wait();
@@ -140,7 +168,9 @@ inline float __shfl_xor(float v, int m, int)
     uint32_t u;
     memcpy(&u, &v, 4);
     tb->xch[w][l] = u;
+    emu_xpost(w, l, 2);
     tb->wbar[w]->arrive_and_wait();
+    emu_xcheck(w, l);
     uint32_t o = (uint32_t)tb->xch[w][l ^ m];
     tb->wbar[w]->arrive_and_wait();
     float r;
@@ -340,7 +370,9 @@ inline v4f emu_mfma(v8i a, v8i b, v4f c, int cbsz, int blgp, int opa, int sa, in
     memcpy(tb->wx[w][l], &a, 32);
     memcpy(tb->wx[w][l] + 32, &b, 32);
     tb->xch[w][l] = ((uint64_t)(uint8_t)(sa >> (8 * opa)) << 8) | (uint8_t)(sb >> (8 * opb));
+    emu_xpost(w, l, 3);
     tb->wbar[w]->arrive_and_wait();
+    emu_xcheck(w, l);
     const int r = l & 15, g = l >> 4;
     v4f out = c;
     auto elem = [&](int lane_row, int k, int off, bool fp4) -> float {   // element k of row lane_row
@@ -396,10 +428,11 @@ inline void emu_launch(F fn, unsigned gx, unsigned gy, unsigned nt, size_t smem,
                     blockIdx = {blocks[b0 + i].first, blocks[b0 + i].second, 0};
                     tb = B;
                     tq.clear();
-                    t_m0 = 0; t_sbase = nullptr; t_ndma = 0; t_shoff = 0;
+                    t_m0 = 0; t_sbase = nullptr; t_ndma = 0; t_shoff = 0; t_xseq = 0;
                     fn();
                     if (!tq.empty()) EMU_ERR("lane exits with %zu DMA ops outstanding", tq.size());
                     emu_wait(0);
+                    B->gone[t / 64][t % 64] = true;
                     B->wbar[t / 64]->arrive_and_drop();
                     B->bar->arrive_and_drop();
                 });
@@ -417,7 +450,9 @@ inline uint32_t emu_first_lane(uint32_t v)
 {
     const int w = wave_id(), l = lane_id();
     tb->xch[w][l] = v;
+    emu_xpost(w, l, 4);
     tb->wbar[w]->arrive_and_wait();
+    emu_xcheck(w, l);
     const uint32_t r = (uint32_t)tb->xch[w][0];
     tb->wbar[w]->arrive_and_wait();
     return r;

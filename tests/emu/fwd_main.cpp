@@ -1,0 +1,160 @@
+// Whole-forward host emulation: the library's own C ABI (xs_moe_forward,
+// xs_moe_forward_noalloc, xs_moe_plan), dispatch and launchers, with every
+// kernel run from its source on the CPU (gen_fwd.py, hip_emu.hpp), against
+// the CPU oracle on the same inputs.
+// usage: fwd_emu T H I E k seed fp4 shared router x_f32 zipf norm residual noalloc
+// Prints the plan, then "idx mismatches N" etc. (routing, weights, counts,
+// offsets, permutation and inverse against the oracle's routing of the logits
+// the forward routed on), "ref idx mismatches N" (against the oracle's routing
+// from x; required 0 for the certified and chain routers), "logit mismatches
+// N" (chain router: required 0), and "max-abs-rel E" of the output against the
+// oracle's dequantize-then-f32 layer.
+#include "hip_emu.hpp"
+#include <cmath>
+#include <random>
+
+#include "moe_oracle.h"
+#include "xs_moe.h"
+
+int main(int argc, char **argv)
+{
+    auto arg = [&](int i, double d) { return argc > i ? atof(argv[i]) : d; };
+    const int T = (int)arg(1, 64), H = (int)arg(2, 256), I = (int)arg(3, 256), E = (int)arg(4, 8), k = (int)arg(5, 2);
+    const int seed = (int)arg(6, 1), fp4 = (int)arg(7, 0), shared = (int)arg(8, 1), router = (int)arg(9, 1);
+    const int xf32 = (int)arg(10, 0);
+    const double zipf = arg(11, 0);
+    const int norm = (int)arg(12, 0), resid = (int)arg(13, 0), noalloc = (int)arg(14, 0);
+    g_math = true;
+    std::mt19937 rng(seed);
+    std::normal_distribution<float> nd(0.f, 1.f);
+    const size_t el = xf32 ? 4 : 2;
+    auto fill_act = [&](void *p, size_t n, float sd) {
+        for (size_t i = 0; i < n; ++i) {
+            const float v = sd * nd(rng);
+            if (xf32) ((float *)p)[i] = v; else ((uint16_t *)p)[i] = xo_bf16_from_f32(v);
+        }
+    };
+    void *x = emu_alloc((size_t)T * H * el, "x");
+    void *wr = emu_alloc((size_t)E * H * el, "router_w");
+    float *bias = (float *)emu_alloc(4 * (size_t)E, "bias");
+    fill_act(x, (size_t)T * H, 1.0f);
+    fill_act(wr, (size_t)E * H, 0.02f);
+    for (int e = 0; e < E; ++e) bias[e] = 0.1f * nd(rng) + (zipf > 0 ? (float)(-zipf * std::log(1.0 + (e * 7919) % E)) : 0.f);
+    void *nw = nullptr, *res = nullptr;
+    if (norm) { nw = emu_alloc((size_t)H * el, "norm_w"); fill_act(nw, H, 1.0f); }
+    if (resid) { res = emu_alloc((size_t)T * H * el, "residual"); fill_act(res, (size_t)T * H, 1.0f); }
+    // weights: N(0, 0.02) quantized by the oracle's quantizers
+    std::vector<float> w13f((size_t)2 * I * H), w2f((size_t)H * I);
+    uint8_t *w13, *w2;
+    void *s13, *s2;
+    if (fp4) {
+        w13 = (uint8_t *)emu_alloc((size_t)E * 2 * I * H / 2, "w13");
+        s13 = emu_alloc((size_t)E * 2 * I * H / 32, "s13");
+        w2 = (uint8_t *)emu_alloc((size_t)E * H * I / 2, "w2");
+        s2 = emu_alloc((size_t)E * H * I / 32, "s2");
+    } else {
+        w13 = (uint8_t *)emu_alloc((size_t)E * 2 * I * H, "w13");
+        s13 = emu_alloc(4 * (size_t)E * (2 * I / 128) * (H / 128), "s13");
+        w2 = (uint8_t *)emu_alloc((size_t)E * H * I, "w2");
+        s2 = emu_alloc(4 * (size_t)E * (H / 128) * (I / 128), "s2");
+    }
+    for (int e = 0; e < E; ++e) {
+        for (auto &v : w13f) v = 0.02f * nd(rng);
+        for (auto &v : w2f) v = 0.02f * nd(rng);
+        if (fp4) {
+            xo_quant_weight_mxfp4(w13f.data(), 2 * I, H, w13 + (size_t)e * 2 * I * H / 2, (uint8_t *)s13 + (size_t)e * 2 * I * H / 32);
+            xo_quant_weight_mxfp4(w2f.data(), H, I, w2 + (size_t)e * H * I / 2, (uint8_t *)s2 + (size_t)e * H * I / 32);
+        } else {
+            xo_quant_weight_fp8_block(w13f.data(), 2 * I, H, w13 + (size_t)e * 2 * I * H, (float *)s13 + (size_t)e * (2 * I / 128) * (H / 128));
+            xo_quant_weight_fp8_block(w2f.data(), H, I, w2 + (size_t)e * H * I, (float *)s2 + (size_t)e * (H / 128) * (I / 128));
+        }
+    }
+    uint8_t *sw13 = nullptr, *sw2 = nullptr;
+    float *ss13 = nullptr, *ss2 = nullptr;
+    if (shared) {
+        sw13 = (uint8_t *)emu_alloc((size_t)2 * I * H, "shared_w13");
+        ss13 = (float *)emu_alloc(4 * (size_t)(2 * I / 128) * (H / 128), "shared_s13");
+        sw2 = (uint8_t *)emu_alloc((size_t)H * I, "shared_w2");
+        ss2 = (float *)emu_alloc(4 * (size_t)(H / 128) * (I / 128), "shared_s2");
+        for (auto &v : w13f) v = 0.02f * nd(rng);
+        for (auto &v : w2f) v = 0.02f * nd(rng);
+        xo_quant_weight_fp8_block(w13f.data(), 2 * I, H, sw13, ss13);
+        xo_quant_weight_fp8_block(w2f.data(), H, I, sw2, ss2);
+    }
+
+    xs_moe_params p = {};
+    p.T = T; p.H = H; p.I = I; p.E = E; p.top_k = k; p.n_group = 1; p.topk_group = 1;
+    p.renormalize = 1; p.routed_scaling = 1.0f; p.x_dtype = xf32 ? XS_F32 : XS_BF16;
+    p.routed_format = fp4 ? XS_FP4_E2M1X2 : XS_FP8_E4M3; p.has_shared = shared; p.router_exact = router;
+    p.has_norm = norm; p.norm_eps = 1e-6f;
+    void *out = emu_alloc((size_t)T * H * el, "out");
+    float *lg = (float *)emu_alloc(4 * (size_t)T * E, "dbg logits");
+    int32_t *idx = (int32_t *)emu_alloc(4 * (size_t)T * k, "dbg idx");
+    float *w = (float *)emu_alloc(4 * (size_t)T * k, "dbg w");
+    int32_t *counts = (int32_t *)emu_alloc(4 * (size_t)E, "dbg counts");
+    int32_t *offsets = (int32_t *)emu_alloc(4 * (size_t)(E + 1), "dbg offsets");
+    int32_t *perm = (int32_t *)emu_alloc(4 * (size_t)T * k, "dbg perm");
+    int32_t *inv = (int32_t *)emu_alloc(4 * (size_t)T * k, "dbg inv");
+    xs_moe_tensors t = {};
+    t.x = x; t.router_w = wr; t.router_bias = bias;
+    t.w13 = w13; t.w13_scale = s13; t.w2 = w2; t.w2_scale = s2;
+    t.shared_w13 = sw13; t.shared_w13_scale = ss13; t.shared_w2 = sw2; t.shared_w2_scale = ss2;
+    t.norm_weight = nw; t.residual = res; t.out = out;
+    t.logits = lg; t.topk_idx = idx; t.topk_w = w; t.counts = counts; t.offsets = offsets; t.perm = perm; t.inv = inv;
+    xs_moe_plan_t pl;
+    if (xs_moe_plan(&p, &t, &pl)) { printf("plan failed: %s\n", xs_last_error()); return 1; }
+    printf("plan tile_rows %d routed %d shared %d fused %d\n", pl.tile_rows, pl.routed_gemm, pl.shared_gemm, pl.fused_combine);
+    int rc;
+    if (noalloc) {
+        rc = xs_moe_forward_noalloc(&p, &t, nullptr);
+    } else {
+        const size_t wsb = xs_moe_workspace_size(&p);
+        void *ws = emu_alloc(wsb, "workspace");
+        memset(ws, 0xA7, wsb);   // the forward must not rely on a zeroed workspace
+        rc = xs_moe_forward(&p, &t, ws, wsb, nullptr);
+    }
+    if (rc) { printf("forward failed: %d %s\n", rc, xs_last_error()); return 1; }
+
+    // the oracle on the (normalized) x the router read
+    std::vector<uint8_t> xin((size_t)T * H * el);
+    if (norm) xo_rmsnorm(x, nw, xf32 ? 0 : 1, T, H, 1e-6f, xin.data());
+    else memcpy(xin.data(), x, xin.size());
+    xo_moe_cfg cfg = {T, H, I, E, k, 1, 1, 1, 1.0f, xf32 ? 0 : 1, fp4, shared, 1};
+    xo_moe_inputs in = {xin.data(), wr, bias, lg, w13, s13, w2, s2, sw13, ss13, sw2, ss2};
+    std::vector<int32_t> ridx((size_t)T * k), rc_((size_t)E), ro((size_t)E + 1), rp((size_t)T * k), ri((size_t)T * k);
+    std::vector<float> rw((size_t)T * k), rout((size_t)T * H);
+    std::vector<uint8_t> rob((size_t)T * H * el);
+    xo_moe_outputs o = {nullptr, ridx.data(), rw.data(), rc_.data(), ro.data(), rp.data(), ri.data(), rout.data(), rob.data()};
+    xo_moe_forward(&cfg, &in, &o);
+    long b_idx = 0, b_w = 0, b_c = 0, b_o = 0, b_p = 0, b_i = 0;
+    for (size_t i = 0; i < (size_t)T * k; ++i) {
+        b_idx += idx[i] != ridx[i];
+        b_w += memcmp(&w[i], &rw[i], 4) != 0;
+        b_p += perm[i] != rp[i];
+        b_i += inv[i] != ri[i];
+    }
+    for (int e = 0; e < E; ++e) b_c += counts[e] != rc_[e];
+    for (int e = 0; e <= E; ++e) b_o += offsets[e] != ro[e];
+    // routing from x (the reference's gemm_cpu logits)
+    std::vector<float> xl((size_t)T * E);
+    xo_router_logits(xin.data(), wr, xf32 ? 0 : 1, T, E, H, xl.data());
+    std::vector<int32_t> xidx((size_t)T * k);
+    std::vector<float> xw((size_t)T * k);
+    xo_route(xl.data(), bias, T, E, k, 1, 1, 1, 1.0f, xidx.data(), xw.data());
+    long b_xidx = 0, b_lg = 0;
+    for (size_t i = 0; i < (size_t)T * k; ++i) b_xidx += idx[i] != xidx[i];
+    for (size_t i = 0; i < (size_t)T * E; ++i) b_lg += memcmp(&lg[i], &xl[i], 4) != 0;
+    double amax = 0, dmax = 0;
+    for (size_t i = 0; i < (size_t)T * H; ++i) {
+        double r = rout[i], g;
+        if (resid) r += xf32 ? ((float *)res)[i] : xo_f32_from_bf16(((uint16_t *)res)[i]);
+        g = xf32 ? ((float *)out)[i] : xo_f32_from_bf16(((uint16_t *)out)[i]);
+        amax = std::max(amax, std::fabs(r));
+        dmax = std::max(dmax, std::fabs(g - r));
+    }
+    printf("idx mismatches %ld\nw mismatches %ld\ncounts mismatches %ld\noffsets mismatches %ld\n"
+           "perm mismatches %ld\ninv mismatches %ld\nref idx mismatches %ld\nlogit mismatches %ld\n",
+           b_idx, b_w, b_c, b_o, b_p, b_i, b_xidx, b_lg);
+    printf("max-abs-rel %.4g\nerrors %ld\n", dmax / (amax > 0 ? amax : 1), (long)g_errors);
+    return 0;
+}

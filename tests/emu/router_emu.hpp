@@ -17,7 +17,9 @@ inline uint64_t emu_xchg(uint64_t v, int src)
 {
     const int w = wave_id(), l = lane_id();
     tb->xch[w][l] = v;
+    emu_xpost(w, l, 5);
     tb->wbar[w]->arrive_and_wait();
+    emu_xcheck(w, l);
     const uint64_t r = tb->xch[w][src & 63];
     tb->wbar[w]->arrive_and_wait();
     return r;
@@ -34,7 +36,9 @@ inline int __any(int pred)
 {
     const int w = wave_id(), l = lane_id();
     tb->xch[w][l] = pred != 0;
+    emu_xpost(w, l, 6);
     tb->wbar[w]->arrive_and_wait();
+    emu_xcheck(w, l);
     int r = 0;
     for (int i = 0; i < 64; ++i) r |= (int)tb->xch[w][i];
     tb->wbar[w]->arrive_and_wait();
@@ -76,7 +80,9 @@ inline v4f emu_mfma_bf16(v8bf a, v8bf b, v4f c, int, int, int)
     const int w = wave_id(), l = lane_id();
     memcpy(tb->wx[w][l], &a, 16);
     memcpy(tb->wx[w][l] + 16, &b, 16);
+    emu_xpost(w, l, 3);
     tb->wbar[w]->arrive_and_wait();
+    emu_xcheck(w, l);
     const int r = l & 15, g = l >> 4;
     v4f out;
     auto el = [&](int row, int k, int off) {
@@ -138,10 +144,11 @@ inline void emu_launch3(F fn, unsigned gx, unsigned gy, unsigned gz, unsigned nt
                     blockIdx = bid;
                     tb = B;
                     tq.clear();
-                    t_m0 = 0; t_sbase = nullptr; t_ndma = 0; t_shoff = 0;
+                    t_m0 = 0; t_sbase = nullptr; t_ndma = 0; t_shoff = 0; t_xseq = 0;
                     fn();
                     if (!tq.empty()) EMU_ERR("lane exits with %zu DMA ops outstanding", tq.size());
                     emu_wait(0);
+                    B->gone[t / 64][t % 64] = true;
                     B->wbar[t / 64]->arrive_and_drop();
                     B->bar->arrive_and_drop();
                 });

@@ -1,0 +1,91 @@
+"""Host emulation of the whole default forward: the library's own C ABI
+(xs_moe_forward, xs_moe_forward_noalloc, xs_moe_plan), dispatch, workspace
+layout and launchers compiled for the host, with every kernel launch running
+the kernel's source on the CPU (tests/emu/gen_fwd.py, hip_emu.hpp; one thread
+per lane, DMAs landing at their waits, addresses checked against their
+buffers, every wave exchange checked to be reached by all live lanes).
+
+Each case runs one forward on a poisoned workspace and compares against the
+CPU oracle: routing, weights, counts, offsets, permutation and inverse bit
+for bit against the oracle's routing of the logits the forward routed on;
+the top-k against the oracle's routing from x for the certified and chain
+routers (and the logits bit for bit for the chain router); the output within
+the layer's 2e-2 bound of the oracle's dequantize-then-f32 layer.  The cases
+cover each GEMM family of the default dispatch: one-block-per-tile, the
+persistent stream-K kernels, the tall tiles with the separate and the fused
+combine, MXFP4 routed experts, the pre-norm with a residual, the
+no-allocation entry point, f32 inputs, and E = 1024 with top-16."""
+import os
+import re
+import shutil
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EMU = os.path.join(ROOT, "tests", "emu")
+HIP = os.path.join(ROOT, "xstar-infer_amd", "csrc", "hip")
+CLANG = "/opt/rocm/llvm/bin/clang++"
+FLAGS = ["-O1", "-std=c++20", "-pthread", "-Wno-psabi", "-ffp-contract=off"]
+
+
+@pytest.fixture(scope="module")
+def fwd_emu(tmp_path_factory):
+    if not os.path.exists(CLANG):
+        pytest.skip("clang++ not found")
+    import oracle
+    oracle.lib()
+    d = tmp_path_factory.mktemp("fwd_emu")
+    subprocess.run([sys.executable, os.path.join(EMU, "gen_fwd.py"), HIP, str(d)], check=True, cwd=EMU)
+    inc = ["-I", str(d), "-I", EMU, "-I", os.path.join(ROOT, "include")]
+    srcs = sorted(f for f in os.listdir(d) if f.endswith(".cpp"))
+    procs = [subprocess.Popen([CLANG, *FLAGS, *inc, "-c", str(d / f), "-o", str(d / (f[:-4] + ".o"))])
+             for f in srcs]
+    assert all(p.wait() == 0 for p in procs)
+    build = os.path.join(ROOT, "oracle", "_build")
+    exe = d / "fwd_emu"
+    subprocess.run([CLANG, *FLAGS, *inc, "-I", os.path.join(ROOT, "oracle"), os.path.join(EMU, "fwd_main.cpp"),
+                    *[str(d / (f[:-4] + ".o")) for f in srcs], "-o", str(exe), "-L", build, "-loracle",
+                    f"-Wl,-rpath,{build}"], check=True)
+    yield str(exe)
+    shutil.rmtree(d, ignore_errors=True)
+
+
+# name, env, (T H I E k seed fp4 shared router x_f32 zipf norm residual noalloc), expected routed GEMM
+CASES = [
+    ("tiled", {"XS_MOE_STREAM": "0"}, (64, 256, 256, 8, 2, 1, 0, 1, 1, 0, 0, 0, 0, 0), 0),
+    ("stream", {}, (64, 256, 256, 8, 2, 1, 0, 1, 1, 0, 0, 0, 0, 0), 1),
+    ("tall", {}, (300, 256, 256, 4, 2, 2, 0, 1, 1, 0, 1.1, 0, 0, 0), 2),
+    ("tall_fused_combine", {"XS_FUSE_COMBINE": "1"}, (300, 256, 256, 4, 2, 2, 0, 1, 1, 0, 1.1, 0, 0, 0), 2),
+    ("c1_f32_chain", {}, (64, 256, 128, 8, 2, 11, 0, 1, 2, 1, 0, 0, 0, 0), 0),
+    ("mxfp4_stream", {}, (48, 512, 512, 16, 6, 3, 1, 1, 1, 0, 0, 0, 0, 0), 1),
+    ("mxfp4_tiled64", {"XS_MOE_STREAM": "0"}, (160, 512, 512, 16, 6, 4, 1, 1, 1, 0, 0, 0, 0, 0), 0),
+    ("norm_residual", {}, (100, 512, 256, 16, 4, 5, 0, 1, 1, 0, 0, 1, 1, 0), 1),
+    ("noalloc", {}, (40, 512, 256, 16, 4, 6, 0, 1, 1, 0, 0, 0, 0, 1), 1),
+    ("decode_t1", {}, (1, 1024, 512, 64, 6, 8, 0, 1, 1, 0, 0, 0, 0, 0), 0),
+    ("mfma_router", {}, (64, 256, 256, 8, 2, 7, 0, 1, 0, 0, 0, 0, 0, 0), 1),
+    ("e1024_top16", {}, (48, 256, 128, 1024, 16, 10, 0, 1, 1, 0, 0, 0, 0, 0), 1),
+    ("f32_norm_residual", {}, (64, 256, 128, 8, 2, 12, 0, 1, 1, 1, 0, 1, 1, 0), 0),
+]
+
+
+@pytest.mark.parametrize("name,env,args,routed", CASES, ids=[c[0] for c in CASES])
+def test_forward_emulated(fwd_emu, name, env, args, routed):
+    r = subprocess.run([fwd_emu, *map(str, args)], capture_output=True, text=True, timeout=900,
+                       env=dict(os.environ, **env))
+    out = r.stdout + r.stderr
+    assert r.returncode == 0, out[-3000:]
+    assert re.search(r"^errors 0$", out, re.M), out[-3000:]
+    assert int(re.search(r"routed (\d+)", out).group(1)) == routed, out
+    if env.get("XS_FUSE_COMBINE") == "1":
+        assert re.search(r"fused 1", out), out
+    c = {m.group(1): int(m.group(2)) for m in re.finditer(r"^([\w ]+?) mismatches (\d+)", out, re.M)}
+    router = args[8]
+    for n in ("idx", "w", "counts", "offsets", "perm", "inv"):
+        assert c[n] == 0, (n, out)
+    if router in (1, 2):
+        assert c["ref idx"] == 0, out
+    if router == 2:
+        assert c["logit"] == 0, out
+    assert float(re.search(r"max-abs-rel (\S+)", out).group(1)) <= 2e-2, out

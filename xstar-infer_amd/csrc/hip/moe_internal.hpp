@@ -63,7 +63,8 @@ __device__ __forceinline__ void store8(float *p, const float *v)
 // FP8 1x128 activation quant of 8 consecutive values held by one lane; the
 // 16 lanes of an aligned 16-lane group hold one 128-column group.  amax over
 // the group, inv = 448/amax, q = e4m3_rne(v * inv) (amax == 0: q = 0, scale 1),
-// scale = amax/448 written through `s` by the group's first lane (s != null).
+// scale = amax/448 written through `s` by the group's first lane (s != null);
+// q == null: the shuffles run, nothing is stored (lanes past the data).
 __device__ __forceinline__ void quant8_fp8(const float *v, uint8_t *__restrict__ q, float *__restrict__ s)
 {
     float amax = 0.0f;
@@ -80,7 +81,7 @@ __device__ __forceinline__ void quant8_fp8(const float *v, uint8_t *__restrict__
     uint32_t lo = e4m3_pack2_hw(r[0], r[1]) | (e4m3_pack2_hw(r[2], r[3]) << 16);
     uint32_t hi = e4m3_pack2_hw(r[4], r[5]) | (e4m3_pack2_hw(r[6], r[7]) << 16);
     if (amax == 0.0f) lo = hi = 0u;   // an all-zero group is code 0, also where its values are -0
-    *reinterpret_cast<v2i *>(q) = v2i{(int)lo, (int)hi};
+    if (q) *reinterpret_cast<v2i *>(q) = v2i{(int)lo, (int)hi};
     if (s) *s = amax == 0.0f ? 1.0f : __fdiv_rn(amax, 448.0f);
 }
 

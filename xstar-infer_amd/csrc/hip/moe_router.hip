@@ -222,7 +222,7 @@ __device__ __forceinline__ void quant_chunk_fp8(const T *__restrict__ xr, int co
 {
     float v[8];
     load8(xr + c8 * 8, v);
-    quant8_fp8(v, qr + c8 * 8, (c8 & 15) == 0 ? sr + c8 / 16 : nullptr);
+    quant8_fp8(v, qr ? qr + c8 * 8 : nullptr, (qr && (c8 & 15) == 0) ? sr + c8 / 16 : nullptr);
 }
 
 // ------------------------------------------------------------- MFMA logits
@@ -276,10 +276,13 @@ __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t 
         // (klen % 128 == 0, so each aligned 16-lane group is one 128-column group)
         const int per_row = klen / 8, rows = 32 * MT;
         for (int c = threadIdx.x; c < rows * per_row; c += 256) {
+            // every lane takes part in the group's amax shuffles; rows past
+            // the batch read the last row and store nothing
             const int t = blockIdx.y * rows + c / per_row;
-            if (t < Tn)
-                quant_chunk_fp8(x + (size_t)t * H, H, blockIdx.z * per_row + c % per_row, q + (size_t)t * H,
-                                qs + (size_t)t * (H / 128));
+            const bool live = t < Tn;
+            const int tr = live ? t : Tn - 1;
+            quant_chunk_fp8(x + (size_t)tr * H, H, blockIdx.z * per_row + c % per_row,
+                            live ? q + (size_t)t * H : nullptr, live ? qs + (size_t)t * (H / 128) : nullptr);
         }
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
