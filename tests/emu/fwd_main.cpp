@@ -2,7 +2,10 @@
 // xs_moe_forward_noalloc, xs_moe_plan), dispatch and launchers, with every
 // kernel run from its source on the CPU (gen_fwd.py, hip_emu.hpp), against
 // the CPU oracle on the same inputs.
-// usage: fwd_emu T H I E k seed fp4 shared router x_f32 zipf norm residual noalloc
+// usage: fwd_emu T H I E k seed fp4 shared router x_f32 zipf norm residual noalloc [frag]
+// frag: 1 also the weights in fragment order (xs_pack_weight_*_frag, run
+// emulated), 2 only those (packed-only layer); with XS_WEIGHT_DIRECT=1 the
+// forward then takes the weight-direct GEMMs.
 // Prints the plan, then "idx mismatches N" etc. (routing, weights, counts,
 // offsets, permutation and inverse against the oracle's routing of the logits
 // the forward routed on), "ref idx mismatches N" (against the oracle's routing
@@ -23,7 +26,7 @@ int main(int argc, char **argv)
     const int seed = (int)arg(6, 1), fp4 = (int)arg(7, 0), shared = (int)arg(8, 1), router = (int)arg(9, 1);
     const int xf32 = (int)arg(10, 0);
     const double zipf = arg(11, 0);
-    const int norm = (int)arg(12, 0), resid = (int)arg(13, 0), noalloc = (int)arg(14, 0);
+    const int norm = (int)arg(12, 0), resid = (int)arg(13, 0), noalloc = (int)arg(14, 0), frag = (int)arg(15, 0);
     g_math = true;
     std::mt19937 rng(seed);
     std::normal_distribution<float> nd(0.f, 1.f);
@@ -101,6 +104,33 @@ int main(int argc, char **argv)
     t.shared_w13 = sw13; t.shared_w13_scale = ss13; t.shared_w2 = sw2; t.shared_w2_scale = ss2;
     t.norm_weight = nw; t.residual = res; t.out = out;
     t.logits = lg; t.topk_idx = idx; t.topk_w = w; t.counts = counts; t.offsets = offsets; t.perm = perm; t.inv = inv;
+    if (frag) {
+        auto pack8 = [&](const uint8_t *w_, int64_t b, int64_t n, int64_t kk, const char *nm) {
+            uint8_t *o_ = (uint8_t *)emu_alloc((size_t)(b * n * kk), nm);
+            if (xs_pack_weight_fp8_frag(w_, b, n, kk, o_, nullptr)) { printf("pack failed: %s\n", xs_last_error()); exit(1); }
+            return o_;
+        };
+        if (fp4) {
+            uint8_t *p13 = (uint8_t *)emu_alloc((size_t)E * 2 * I * H / 2, "w13 packed");
+            uint8_t *q13 = (uint8_t *)emu_alloc((size_t)E * 2 * I * H / 32, "s13 packed");
+            uint8_t *p2 = (uint8_t *)emu_alloc((size_t)E * H * I / 2, "w2 packed");
+            uint8_t *q2 = (uint8_t *)emu_alloc((size_t)E * H * I / 32, "s2 packed");
+            if (xs_pack_weight_mxfp4_frag(w13, (uint8_t *)s13, E, 2 * I, H, p13, q13, nullptr) ||
+                xs_pack_weight_mxfp4_frag(w2, (uint8_t *)s2, E, H, I, p2, q2, nullptr)) {
+                printf("pack failed: %s\n", xs_last_error());
+                return 1;
+            }
+            t.w13_frag = p13; t.w2_frag = p2; t.w13_scale_frag = q13; t.w2_scale_frag = q2;
+        } else {
+            t.w13_frag = pack8(w13, E, 2 * I, H, "w13 packed");
+            t.w2_frag = pack8(w2, E, H, I, "w2 packed");
+        }
+        if (shared) {
+            t.shared_w13_frag = pack8(sw13, 1, 2 * I, H, "shared w13 packed");
+            t.shared_w2_frag = pack8(sw2, 1, H, I, "shared w2 packed");
+        }
+        if (frag == 2) t.w13 = t.w2 = t.shared_w13 = t.shared_w2 = nullptr;
+    }
     xs_moe_plan_t pl;
     if (xs_moe_plan(&p, &t, &pl)) { printf("plan failed: %s\n", xs_last_error()); return 1; }
     printf("plan tile_rows %d routed %d shared %d fused %d\n", pl.tile_rows, pl.routed_gemm, pl.shared_gemm, pl.fused_combine);

@@ -172,3 +172,28 @@ inline void emu_kl(F fn, dim3 g, dim3 b, size_t smem = 0, hipStream_t = nullptr)
         }
     }
 }
+
+// compiler-visible register loads of the weight-direct kernels: read now (the
+// compiler waits for them before any use), counted in the lane's vmcnt queue
+// as the hardware counts them
+inline v4i wd_gload(const uint8_t *p)
+{
+    if (!emu_check_global(p, 16)) EMU_ERR("register load %p outside every buffer", (const void *)p);
+    v4i v;
+    memcpy(&v, p, 16);
+    push(Op{2, nullptr, 0, 0, nullptr, nullptr});
+    return v;
+}
+inline uint8_t wd_gload1(const uint8_t *p)
+{
+    if (!emu_check_global(p, 1)) EMU_ERR("scale load %p outside every buffer", (const void *)p);
+    push(Op{2, nullptr, 0, 0, nullptr, nullptr});
+    return *p;
+}
+inline v4i wd_gload_now(const uint8_t *p)
+{
+    if (!emu_check_global(p, 16)) EMU_ERR("register load %p outside every buffer", (const void *)p);
+    v4i v;
+    memcpy(&v, p, 16);
+    return v;
+}

@@ -14,7 +14,9 @@ the layer's 2e-2 bound of the oracle's dequantize-then-f32 layer.  The cases
 cover each GEMM family of the default dispatch: one-block-per-tile, the
 persistent stream-K kernels, the tall tiles with the separate and the fused
 combine, MXFP4 routed experts, the pre-norm with a residual, the
-no-allocation entry point, f32 inputs, and E = 1024 with top-16."""
+no-allocation entry point, f32 inputs, E = 1024 with top-16, and the
+weight-direct GEMMs behind XS_WEIGHT_DIRECT=1 (packed by the library's own
+packing kernels; decode always, prefill and MXFP4 with XS_EMU_FULL=1)."""
 import os
 import re
 import shutil
@@ -52,7 +54,7 @@ def fwd_emu(tmp_path_factory):
     shutil.rmtree(d, ignore_errors=True)
 
 
-# name, env, (T H I E k seed fp4 shared router x_f32 zipf norm residual noalloc), expected routed GEMM
+# name, env, (T H I E k seed fp4 shared router x_f32 zipf norm residual noalloc [frag]), expected routed GEMM
 CASES = [
     ("tiled", {"XS_MOE_STREAM": "0"}, (64, 256, 256, 8, 2, 1, 0, 1, 1, 0, 0, 0, 0, 0), 0),
     ("stream", {}, (64, 256, 256, 8, 2, 1, 0, 1, 1, 0, 0, 0, 0, 0), 1),
@@ -67,7 +69,18 @@ CASES = [
     ("mfma_router", {}, (64, 256, 256, 8, 2, 7, 0, 1, 0, 0, 0, 0, 0, 0), 1),
     ("e1024_top16", {}, (48, 256, 128, 1024, 16, 10, 0, 1, 1, 0, 0, 0, 0, 0), 1),
     ("f32_norm_residual", {}, (64, 256, 128, 8, 2, 12, 0, 1, 1, 1, 0, 1, 1, 0), 0),
+    # the weight-direct GEMMs (opt-in), packed by the library's own packing
+    # kernels: decode on a packed-only layer
+    ("wd_decode_packed_only", {"XS_WEIGHT_DIRECT": "1"}, (16, 1024, 512, 16, 4, 24, 0, 1, 1, 0, 0, 0, 0, 0, 2), 4),
 ]
+# one to two minutes of CPU each: with XS_EMU_FULL=1
+FULL_CASES = [
+    ("wd_prefill", {"XS_WEIGHT_DIRECT": "1"}, (300, 1024, 512, 4, 2, 22, 0, 1, 1, 0, 1.1, 0, 0, 0, 1), 3),
+    ("wd_mxfp4", {"XS_WEIGHT_DIRECT": "1"}, (160, 1024, 512, 16, 6, 23, 1, 1, 1, 0, 0, 0, 0, 0, 1), 5),
+    ("wd_mxfp4_packed_only", {"XS_WEIGHT_DIRECT": "1"}, (100, 1024, 512, 16, 6, 25, 1, 1, 1, 0, 0, 0, 0, 0, 2), 5),
+]
+if os.environ.get("XS_EMU_FULL") == "1":
+    CASES += FULL_CASES
 
 
 @pytest.mark.parametrize("name,env,args,routed", CASES, ids=[c[0] for c in CASES])
