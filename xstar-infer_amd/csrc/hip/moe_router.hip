@@ -593,7 +593,9 @@ struct CertArgs {
 //     so sum_k |S_k| <= 32 sum_j |S_j0| + 32 A.  The MFMA's own result is
 //     allowed 66 u (|acc| + a_j) per instruction: 33 additions of at most
 //     one unit in the last place of a magnitude below |acc| + a_j, whatever
-//     the hardware's internal order and rounding (truncation included).
+//     the hardware's internal order and rounding (truncation included); it
+//     must not flush subnormal bf16 operands (products that underflow are
+//     covered by the 2^-100 absolute term).
 //     Slice s starts its accumulator at 0 while L_ref's partial sums carry
 //     P_s (the slices before it), which adds 32 n_s |P_s| for its n_s
 //     blocks; summing the slices rounds by at most u |P_s+1| per add.  Hence
