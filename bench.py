@@ -283,13 +283,9 @@ def prefill(a, X, torch):
                      "mfma_tflops": gu_flops / (gu_ms * 1e-3) / 1e12,
                      "mfma_frac": gu_flops / (gu_ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS},
     }
-    # the bit-exact router (gemm_cpu order, f32, no FMA) on the same workload
-    lx = layer_from(g, router_exact=True)
-    msx, stx = time_forward(lx, g["x"], a.steps, a.warmup, profile=True)
-    res["router_exact"] = {"ms_per_step": msx, "router_logits_ms": stx["router_logits"],
-                           "router_logits_ms_mfma": stages["router_logits"],
-                           "extra_frac_of_layer": (msx - ms) / ms}
-    del lx
+    # the default (certified, bit-exact top-k) router against the approximate
+    # MFMA router and the chain router (every logit in gemm_cpu order)
+    res["router"] = router_report(layer, g["x"], T, ms, stages, a, layer_from, g)
     del layer
     if not a.no_cpu:
         log("cpu baseline ...")
@@ -299,6 +295,24 @@ def prefill(a, X, torch):
     del g
     torch.cuda.empty_cache()
     return res
+
+
+def router_report(layer, x, T, ms, stages, a, layer_from, g):
+    """The default certified router's share of the layer (its logits launch
+    with the bound terms; route, exact pass and second route together make the
+    route stage) and how much the exact pass did on this batch, next to the
+    same layer with the approximate MFMA router and with the chain router."""
+    layer.forward(x)
+    pairs, tokens = layer.router_stats(T)
+    rep = {"kind": "certified", "logits_ms": stages["router_logits"], "route_ms": stages["route"],
+           "exact_pass": {"logits": pairs, "tokens": tokens, "token_frac": tokens / max(T, 1)}}
+    for name, kind in (("mfma", 0), ("chain", 2)):
+        lx = layer_from(g, router=kind)
+        msx, stx = time_forward(lx, x, a.steps, a.warmup, profile=True)
+        rep[name] = {"ms_per_step": msx, "logits_ms": stx["router_logits"], "route_ms": stx["route"],
+                     "layer_ms_vs_certified": msx - ms}
+        del lx
+    return rep
 
 
 def decode(a, X, torch):
@@ -314,13 +328,11 @@ def decode(a, X, torch):
         msd, st = time_forward(L, xd, max(a.steps, 50), a.warmup, profile=True)
         ned = routed_expert_count(L, xd)
         by = (ned + 1) * expert_bytes(H, I, False) + E * H * 2 + Td * H * 4
-        Lx = layer_from(gd, router_exact=True)
-        msx, stx = time_forward(Lx, xd, max(a.steps, 50), a.warmup, profile=True)
+        a_dec = argparse.Namespace(**dict(vars(a), steps=max(a.steps, 50)))
         dec[str(Td)] = {"ms": msd, "experts_touched": ned + 1, "hbm_gbs": by / (msd * 1e-3) / 1e9,
                         "frac_hbm_peak": by / (msd * 1e-3) / 1e9 / PEAK_HBM_GBS,
                         "tokens_per_s": Td / (msd * 1e-3), "stage_ms": st, "plan": safe_plan(L, Td),
-                        "router_exact": {"ms": msx, "router_logits_ms": stx["router_logits"],
-                                         "extra_frac_of_layer": (msx - msd) / msd}}
+                        "router": router_report(L, xd, Td, msd, st, a_dec, layer_from, gd)}
     del gd
     torch.cuda.empty_cache()
     return dec

@@ -310,6 +310,14 @@ typedef struct {
 } xs_moe_plan_t;
 int xs_moe_plan(const xs_moe_params *p, const xs_moe_tensors *t, xs_moe_plan_t *out);
 
+/* Diagnostics of the certified router (no reference counterpart: for
+ * benchmarks and tests).  After a forward with these params on this workspace
+ * (NULL: the no-allocation scratch) has been enqueued on `stream`: out[0] =
+ * the (token, expert) logits its exact pass recomputed in gemm_cpu order,
+ * out[1] = the tokens it routed after that pass.  Waits for the stream.  Other
+ * routers report 0, 0. */
+int xs_moe_router_stats(const xs_moe_params *p, const void *workspace, int64_t out[2], void *stream);
+
 /* [RMSNorm] + activation quant -> router -> top-k -> permute -> grouped gate_up
  * GEMM with SwiGLU and FP8 re-quant -> grouped down GEMM -> weighted combine
  * (+ shared).  With has_norm the layer computes moe(rmsnorm(x, norm_weight,

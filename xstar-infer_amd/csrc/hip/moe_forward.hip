@@ -645,6 +645,28 @@ size_t xs_moe_workspace_size(const xs_moe_params *p)
     return layout(p).total;
 }
 
+int xs_moe_router_stats(const xs_moe_params *p, const void *workspace, int64_t out[2], void *stream)
+{
+    XS_REQUIRE(out != nullptr, "null pointer");
+    int rc = check_params(p);
+    if (rc) return rc;
+    out[0] = out[1] = 0;
+    if (p->T == 0 || router_kind(p->router_exact, p->x_dtype) != XS_ROUTER_CERTIFIED) return XS_OK;
+    const char *base = (const char *)workspace;
+    if (!base) {
+        void *sp = nullptr;
+        if ((rc = scratch_for_current_device(&sp))) return rc;
+        base = (const char *)sp;
+    }
+    int32_t c[2] = {0, 0};
+    hipStream_t st = (hipStream_t)stream;
+    XS_HIP(hipMemcpyAsync(c, base + layout(p).ccert, sizeof(c), hipMemcpyDeviceToHost, st));
+    XS_HIP(hipStreamSynchronize(st));
+    out[0] = c[0];
+    out[1] = c[1];
+    return XS_OK;
+}
+
 int xs_moe_plan(const xs_moe_params *p, const xs_moe_tensors *t, xs_moe_plan_t *out)
 {
     XS_REQUIRE(out != nullptr, "null pointer");

@@ -72,6 +72,7 @@ EXPORTS = {
     "xs_gemm_fp8_blockscale_packed": (C.c_int, [P, P, P, I64, I64, I64, P, P, C.c_size_t, P]),
     "xs_moe_workspace_size": (C.c_size_t, [P]),
     "xs_moe_plan": (C.c_int, [P, P, P]),
+    "xs_moe_router_stats": (C.c_int, [P, P, P, P]),
     "xs_moe_forward": (C.c_int, [P, P, P, C.c_size_t, P]),
     "xs_moe_noalloc_scratch_bytes": (C.c_size_t, []),
     "xs_moe_forward_noalloc": (C.c_int, [P, P, P]),
@@ -393,6 +394,15 @@ class MoeLayer:
                        *[_ptr(f) for f in self.frag])
         check(lib().xs_moe_forward(C.byref(p), C.byref(t), _ptr(ws), ws.numel(), _stream()))
         return out
+
+    def router_stats(self, T, x_dtype=XS_BF16):
+        """After forward() on T tokens: (logits the certified router's exact
+        pass recomputed, tokens routed after it); (0, 0) for other routers.
+        Waits for the stream."""
+        out = (C.c_int64 * 2)()
+        p = self.params(T, x_dtype)
+        check(lib().xs_moe_router_stats(C.byref(p), _ptr(self._ws), out, _stream()))
+        return int(out[0]), int(out[1])
 
     def plan(self, T, x_dtype=XS_BF16):
         """The kernels forward() would launch for T tokens (see plan())."""
