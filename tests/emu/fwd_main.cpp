@@ -135,6 +135,7 @@ int main(int argc, char **argv)
     if (xs_moe_plan(&p, &t, &pl)) { printf("plan failed: %s\n", xs_last_error()); return 1; }
     printf("plan tile_rows %d routed %d shared %d fused %d\n", pl.tile_rows, pl.routed_gemm, pl.shared_gemm, pl.fused_combine);
     int rc;
+    void *last_ws = nullptr;
     if (noalloc) {
         rc = xs_moe_forward_noalloc(&p, &t, nullptr);
     } else {
@@ -142,8 +143,14 @@ int main(int argc, char **argv)
         void *ws = emu_alloc(wsb, "workspace");
         memset(ws, 0xA7, wsb);   // the forward must not rely on a zeroed workspace
         rc = xs_moe_forward(&p, &t, ws, wsb, nullptr);
+        last_ws = ws;
     }
     if (rc) { printf("forward failed: %d %s\n", rc, xs_last_error()); return 1; }
+    {
+        int64_t st[2];
+        if (xs_moe_router_stats(&p, noalloc ? nullptr : last_ws, st, nullptr)) { printf("stats failed\n"); return 1; }
+        printf("exact pass logits %lld tokens %lld\n", (long long)st[0], (long long)st[1]);
+    }
 
     // the oracle on the (normalized) x the router read
     std::vector<uint8_t> xin((size_t)T * H * el);

@@ -69,6 +69,9 @@ CASES = [
     ("mfma_router", {}, (64, 256, 256, 8, 2, 7, 0, 1, 0, 0, 0, 0, 0, 0), 1),
     ("e1024_top16", {}, (48, 256, 128, 1024, 16, 10, 0, 1, 1, 0, 0, 0, 0, 0), 1),
     ("f32_norm_residual", {}, (64, 256, 128, 8, 2, 12, 0, 1, 1, 1, 0, 1, 1, 0), 0),
+    # every token through the certified router's exact pass
+    ("exact_pass_everywhere", {"XS_ROUTER_MARGIN": "1e30"}, (24, 512, 256, 16, 4, 26, 0, 1, 1, 0, 0, 0, 0, 0), 1),
+    ("exact_pass_noalloc", {"XS_ROUTER_MARGIN": "1e30"}, (24, 512, 256, 16, 4, 27, 0, 1, 1, 0, 0, 0, 0, 1), 1),
     # the weight-direct GEMMs (opt-in), packed by the library's own packing
     # kernels: decode on a packed-only layer
     ("wd_decode_packed_only", {"XS_WEIGHT_DIRECT": "1"}, (16, 1024, 512, 16, 4, 24, 0, 1, 1, 0, 0, 0, 0, 0, 2), 4),
@@ -102,3 +105,9 @@ def test_forward_emulated(fwd_emu, name, env, args, routed):
     if router == 2:
         assert c["logit"] == 0, out
     assert float(re.search(r"max-abs-rel (\S+)", out).group(1)) <= 2e-2, out
+    pairs, tokens = map(int, re.search(r"exact pass logits (\d+) tokens (\d+)", out).groups())
+    if env.get("XS_ROUTER_MARGIN"):
+        assert (pairs, tokens) == (args[0] * args[3], args[0]), out
+        assert c["logit"] == 0, out     # every logit routed on is the oracle's gemm_cpu logit
+    elif router != 1:
+        assert (pairs, tokens) == (0, 0), out

@@ -335,6 +335,7 @@ def test_certified_router_exact_pass_everywhere(T, monkeypatch):
     dbg = _debug(T_, E, k)
     out = layer.forward(g["x"], debug=dbg)
     torch.cuda.synchronize()
+    assert layer.router_stats(T_) == (T_ * E, T_)     # every logit recomputed, every token re-routed
     r = oracle_forward(c)
     assert np.array_equal(dbg["logits"].cpu().numpy(), r["logits"])
     assert np.array_equal(dbg["topk_idx"].cpu().numpy(), r["idx"])
