@@ -16,7 +16,7 @@ persistent stream-K kernels, the tall tiles with the separate and the fused
 combine, MXFP4 routed experts, the pre-norm with a residual, the
 no-allocation entry point, f32 inputs, E = 1024 with top-16, and the
 weight-direct GEMMs behind XS_WEIGHT_DIRECT=1 (packed by the library's own
-packing kernels; decode always, prefill and MXFP4 with XS_EMU_FULL=1)."""
+packing kernels, with XS_EMU_FULL=1)."""
 import os
 import re
 import shutil
@@ -72,12 +72,11 @@ CASES = [
     # every token through the certified router's exact pass
     ("exact_pass_everywhere", {"XS_ROUTER_MARGIN": "1e30"}, (24, 512, 256, 16, 4, 26, 0, 1, 1, 0, 0, 0, 0, 0), 1),
     ("exact_pass_noalloc", {"XS_ROUTER_MARGIN": "1e30"}, (24, 512, 256, 16, 4, 27, 0, 1, 1, 0, 0, 0, 0, 1), 1),
-    # the weight-direct GEMMs (opt-in), packed by the library's own packing
-    # kernels: decode on a packed-only layer
-    ("wd_decode_packed_only", {"XS_WEIGHT_DIRECT": "1"}, (16, 1024, 512, 16, 4, 24, 0, 1, 1, 0, 0, 0, 0, 0, 2), 4),
 ]
-# one to two minutes of CPU each: with XS_EMU_FULL=1
+# the weight-direct GEMMs (opt-in), packed by the library's own packing
+# kernels; one to two minutes of CPU each: with XS_EMU_FULL=1
 FULL_CASES = [
+    ("wd_decode_packed_only", {"XS_WEIGHT_DIRECT": "1"}, (16, 1024, 512, 16, 4, 24, 0, 1, 1, 0, 0, 0, 0, 0, 2), 4),
     ("wd_prefill", {"XS_WEIGHT_DIRECT": "1"}, (300, 1024, 512, 4, 2, 22, 0, 1, 1, 0, 1.1, 0, 0, 0, 1), 3),
     ("wd_mxfp4", {"XS_WEIGHT_DIRECT": "1"}, (160, 1024, 512, 16, 6, 23, 1, 1, 1, 0, 0, 0, 0, 0, 1), 5),
     ("wd_mxfp4_packed_only", {"XS_WEIGHT_DIRECT": "1"}, (100, 1024, 512, 16, 6, 25, 1, 1, 1, 0, 0, 0, 0, 0, 2), 5),
