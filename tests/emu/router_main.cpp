@@ -3,7 +3,7 @@
 // error-bound terms, route MODE 1, the chain kernel over the listed pairs,
 // route MODE 2) and the chain router over every logit, against the CPU
 // oracle's gemm_cpu-order logits and routing.
-// usage: router_emu mode T E k H seed [nsplit] [margin] [bias_std] [zipf] [dup] [n_group topk_group]
+// usage: router_emu mode T E k H seed [nsplit] [margin] [bias_std] [zipf] [dup] [n_group topk_group] [path]
 //   mode cert: the certified router; prints "idx mismatches N" (must be 0),
 //     "w mismatches N" (weights against the oracle's routing of the logits
 //     the kernels routed on: 0), "mask mismatches N", and the listed pairs;
@@ -12,6 +12,10 @@
 //   dup > 0: router rows E-dup..E-1 (and their biases) copy rows 0..dup-1
 //     (exact ties, broken by the lower index), every other copy with one
 //     element one bf16 step apart (near ties).
+//   path: how the exact pass runs: 0 as the forward does (one launch with a
+//     block per listed token for T <= 256, else the pair-parallel chain
+//     launch and a second routing launch), 1 always the latter, 2 always the
+//     former.
 //   mode chain_bf16 / chain_f32: every logit in gemm_cpu order; prints
 //     "logit mismatches N".
 #include "router_emu.hpp"
@@ -36,6 +40,7 @@ int main(int argc, char **argv)
     const double zipf = argc > 10 ? atof(argv[10]) : 0.0;
     const int dup = argc > 11 ? atoi(argv[11]) : 0;
     const int n_group = argc > 12 ? atoi(argv[12]) : 1, topk_group = argc > 13 ? atoi(argv[13]) : 1;
+    const int path = argc > 14 ? atoi(argv[14]) : 0;
     if (getenv("EMU_MFMA_MODEL")) g_mfma_model = atoi(getenv("EMU_MFMA_MODEL"));
     if (mode == "sigmoid") {
         // xs_sigmoid (the route kernel's) against the sigmoid in double: every
@@ -109,6 +114,8 @@ int main(int argc, char **argv)
     int32_t *pairs = (int32_t *)emu_alloc(8 * TE, "pairs");
     int32_t *cnt = (int32_t *)emu_alloc(8, "counters");
     int32_t *flagged = (int32_t *)emu_alloc(4 * (size_t)T, "flagged");
+    int32_t *fbase = (int32_t *)emu_alloc(4 * (size_t)T, "flagged pair base");
+    int32_t *fcnt = (int32_t *)emu_alloc(4 * (size_t)T, "flagged pair count");
     int32_t *idx = (int32_t *)emu_alloc(4 * (size_t)T * k, "idx");
     float *w = (float *)emu_alloc(4 * (size_t)T * k, "w");
     const int Wd = (T + 31) / 32;
@@ -116,8 +123,8 @@ int main(int argc, char **argv)
     float *lout = (float *)emu_alloc(4 * TE, "logits_out");
     cnt[0] = cnt[1] = 12345;    // the logits launch zeroes them
     memset(mask, 0xff, 4 * (size_t)Wd * E);
-    CertState cs{dpart, H / nsplit / 32, flog, pairs, cnt, flagged, margin};
-    CertArgs ca{dpart, cs.kblocks, flog, pairs, cnt, flagged, margin};
+    CertState cs{dpart, H / nsplit / 32, flog, pairs, cnt, flagged, fbase, fcnt, margin};
+    CertArgs ca{dpart, cs.kblocks, flog, pairs, cnt, flagged, fbase, fcnt, margin};
     const uint16_t *xb = (const uint16_t *)x, *wb = (const uint16_t *)wr;
     if (T <= 256) {
         emu_launch3([&] { router_logits_mfma_kernel<1, 2, true>(xb, wb, T, E, H, H / nsplit, part, mask,
@@ -146,13 +153,24 @@ int main(int argc, char **argv)
     };
     route(1);
     const int npairs = cnt[0], nflag = cnt[1];
-    {
+    if (path == 2 || (path == 0 && T <= 256)) {
+        // a block per listed token (grid smaller than the count: blocks loop)
+        const unsigned grid = (unsigned)std::min(T, 3);
+        auto body = [&] {
+            switch (nv) {
+            case 1: router_token_exact_kernel<uint16_t, 1>(xb, wb, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, lout, ca); break;
+            case 2: router_token_exact_kernel<uint16_t, 2>(xb, wb, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, lout, ca); break;
+            default: router_token_exact_kernel<uint16_t, 4>(xb, wb, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, lout, ca);
+            }
+        };
+        emu_launch3(body, grid, 1, 1, kChainThreads, sizeof(float) * 2 * 64 * kCR, 3);
+    } else {
         const int64_t groups = (TE + 63) / 64;
         const unsigned grid = (unsigned)std::min<int64_t>(groups, 3);
         emu_launch3([&] { router_chain_kernel<uint16_t>(xb, wb, E, H, pairs, cnt, (int64_t)TE, flog, nullptr, 0); },
                     grid, 1, 1, kChainThreads, sizeof(float) * 2 * 64 * kCR, 3);
+        route(2);
     }
-    route(2);
     // the oracle's routing of the reference logits, and of the logits routed on
     std::vector<int32_t> ridx((size_t)T * k), midx((size_t)T * k);
     std::vector<float> rw((size_t)T * k), mw((size_t)T * k);
@@ -174,7 +192,9 @@ int main(int argc, char **argv)
         bad_pair += memcmp(&flog[(size_t)t * E + e], &ref[(size_t)t * E + e], 4) != 0;
     }
     if (margin > 1e6f)
-        for (size_t i = 0; i < TE; ++i) bad_exact += memcmp(&lout[i], &ref[i], 4) != 0;
+        for (size_t i = 0; i < TE; ++i)
+            if (memcmp(&lout[i], &ref[i], 4) != 0 && bad_exact++ < 5)
+                printf("logit (%zu, %zu): %.9g, flog %.9g, reference %.9g\n", i / E, i % E, lout[i], flog[i], ref[i]);
     double maxerr = 0, maxdelta = 0;
     for (size_t i = 0; i < TE; ++i) {
         float lg = part[i];

@@ -11,7 +11,8 @@ pass) every logit is.  The MFMA is modelled three ways (exact sum rounded
 once, k-order rounded adds, truncated adds); the bound must hold for each.
 Covers decode (split-K MFMA kernel) and prefill (LDS-ring tile kernel) logits,
 exact and near ties (duplicated router rows), group-limited routing, and E
-not a multiple of 64."""
+not a multiple of 64, and both forms of the exact pass (a block per listed
+token; pairs spread over blocks plus a second routing launch)."""
 import os
 import re
 import shutil
@@ -65,7 +66,7 @@ def test_chain_router_matches_gemm_cpu(router_emu, dtype):
     assert _counts(out)["logit"] == 0, out
 
 
-# mode T E k H seed nsplit margin bias_std zipf dup n_group topk_group
+# mode T E k H seed nsplit margin bias_std zipf dup n_group topk_group path
 CERT_CASES = [
     ("decode16", (16, 256, 6, 4096, 1, 16)),
     ("decode_skew", (32, 256, 6, 2048, 2, 8, 1, 0.1, 1.1)),
@@ -75,6 +76,12 @@ CERT_CASES = [
     ("groups", (32, 256, 8, 2048, 9, 8, 1, 0.1, 0, 8, 8, 4)),
     ("all_exact", (16, 256, 6, 2048, 4, 16, 1e30)),
     ("all_exact_groups", (8, 256, 8, 1024, 9, 4, 1e30, 0.1, 0, 0, 8, 4)),
+    # the exact pass the other way than the forward picks for the batch: the
+    # pair-parallel launch plus a routing launch at decode, one block per
+    # listed token at prefill
+    ("decode16_pair_parallel", (16, 256, 6, 4096, 1, 16, 1, 0.1, 0, 0, 1, 1, 1)),
+    ("all_exact_pair_parallel", (16, 256, 6, 2048, 4, 16, 1e30, 0.1, 0, 0, 1, 1, 1)),
+    ("prefill_tile_token_blocks", (300, 256, 6, 2048, 6, 4, 1, 0.1, 0, 0, 1, 1, 2)),
 ]
 
 

@@ -39,7 +39,7 @@ static int prof_mark(int stage, hipStream_t st)
 }
 
 struct WsLayout {
-    size_t logits, dpart, flog, pairs, ccert, flagged, idx, w, mask, wordprefix, counts, offsets, perm, inv, row_token, tiles, tiletab, part, cnt1, cnt2;
+    size_t logits, dpart, flog, pairs, ccert, flagged, fbase, fcnt, idx, w, mask, wordprefix, counts, offsets, perm, inv, row_token, tiles, tiletab, part, cnt1, cnt2;
     size_t xn, xq, xs, xmq, xms, actq, acts, actms, y, ccnt;
     size_t total;
 };
@@ -134,6 +134,8 @@ static WsLayout layout(const xs_moe_params *p)
     take(L.pairs, cert ? 8 * T * E : 0);
     take(L.ccert, cert ? 8 : 0);
     take(L.flagged, cert ? 4 * T : 0);
+    take(L.fbase, cert ? 4 * T : 0);
+    take(L.fcnt, cert ? 4 * T : 0);
     take(L.idx, 4 * S);
     take(L.w, 4 * S);
     take(L.mask, 4 * W * E);
@@ -365,6 +367,8 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         cs.pairs = WS(int32_t, pairs);
         cs.cnt = WS(int32_t, ccert);
         cs.flagged = WS(int32_t, flagged);
+        cs.fbase = WS(int32_t, fbase);
+        cs.fcnt = WS(int32_t, fcnt);
         cs.margin_scale = router_margin_scale();
     }
     rc = launch_router_logits(xin, t->router_w, p->x_dtype, T, E, H, p->router_exact, logits, nsplit, st, mask,
@@ -378,11 +382,20 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     if (rc) return rc;
     if (certified) {
         // the pairs the bound left undecided, in gemm_cpu order, then the
-        // listed tokens' routing on their patched logit rows
-        if ((rc = launch_router_fix(xin, t->router_w, p->x_dtype, T, E, H, cs, st))) return rc;
-        rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
-                          p->routed_scaling, idx, w, mask, Wd, 1, t->logits, st, &cs, 2);
-        if (rc) return rc;
+        // listed tokens' routing on their patched logit rows: decode batches
+        // in one launch (a block per listed token), prefill as a pair-parallel
+        // launch and a routing launch
+        if (T <= 256) {
+            rc = launch_router_token_exact(xin, t->router_w, p->x_dtype, t->router_bias, T, E, H, k, p->n_group,
+                                           p->topk_group, p->renormalize, p->routed_scaling, idx, w, mask, Wd,
+                                           t->logits, cs, st);
+            if (rc) return rc;
+        } else {
+            if ((rc = launch_router_fix(xin, t->router_w, p->x_dtype, T, E, H, cs, st))) return rc;
+            rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
+                              p->routed_scaling, idx, w, mask, Wd, 1, t->logits, st, &cs, 2);
+            if (rc) return rc;
+        }
     }
     // 3. permute: (expert, token)-sorted positions, tile offsets
     if ((rc = prof_mark(3, st))) return rc;

@@ -105,7 +105,7 @@ int launch_router_logits(const void *x, const void *wr, int dtype, int64_t T, in
 // dpart [nsplit][T][E] error-bound terms of the MFMA logit slices, flog [T][E]
 // logit rows of the tokens it could not settle, pairs [T*E][2] the (token,
 // expert) logits to recompute exactly, cnt[2] {pairs, flagged tokens}
-// (zeroed by the logits launch), flagged [T].
+// (zeroed by the logits launch), flagged [T] with each token's pair range.
 struct CertState {
     float *dpart;
     int kblocks;          // 32-wide K blocks per logit slice (H / nsplit / 32)
@@ -113,6 +113,8 @@ struct CertState {
     int32_t *pairs;
     int32_t *cnt;
     int32_t *flagged;
+    int32_t *fbase;       // [T] first pair of flagged token j
+    int32_t *fcnt;        // [T] its number of pairs
     float margin_scale;   // 1 (XS_ROUTER_MARGIN scales it: tests of the exact path)
 };
 // Routes on the sum (in slice order) of nsplit partial logit slices; writes the
@@ -123,6 +125,12 @@ int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, i
                  int64_t n_group, int64_t topk_group, int renorm, float scaling, int32_t *idx,
                  float *w, uint32_t *mask, int mask_words, int nsplit, float *logits_out,
                  hipStream_t st, const CertState *cert = nullptr, int mode = 0);
+// The exact pass and the listed tokens' routing in one launch (decode
+// batches, T <= 256): one block per flagged token.
+int launch_router_token_exact(const void *x, const void *wr, int dtype, const float *bias, int64_t T, int64_t E,
+                              int64_t H, int64_t k, int64_t n_group, int64_t topk_group, int renorm, float scaling,
+                              int32_t *idx, float *w, uint32_t *mask, int mask_words, float *logits_out,
+                              const CertState &cert, hipStream_t st);
 // The exact (gemm_cpu order) logits of the listed pairs into cert->flog.
 int launch_router_fix(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
                       const CertState &cert, hipStream_t st);

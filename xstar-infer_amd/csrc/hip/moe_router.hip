@@ -92,6 +92,83 @@ __device__ __forceinline__ void chain_unit_products(const ChainUnit<T> &u, float
     *reinterpret_cast<v4f *>(dst + 4) = hi;
 }
 
+// One group of up to 64 pairs (pair_of(l) -> {token, expert}, l < cnt) by all
+// kChainThreads threads of the block: wave 0's lane l runs pair l's chain and
+// stores it to out[token * E + expert]; the other waves compute the products.
+template <typename T, typename PairOf>
+__device__ __forceinline__ void chain_group(const T *__restrict__ x, const T *__restrict__ wr, int E, int H,
+                                            int cnt, PairOf pair_of, float *__restrict__ out, float *prod)
+{
+#pragma clang fp contract(off)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nc = H / kCK;
+    if (wave == 0) {
+        float acc = 0.0f;
+        for (int c = 0; c < nc; ++c) {
+            __syncthreads();              // chunk c's products are in buffer c & 1
+            const float *row = prod + (c & 1) * 64 * kCR + lane * kCR;
+#pragma unroll
+            for (int k = 0; k < kCK; k += 4) {
+                const v4f pv = *reinterpret_cast<const v4f *>(row + k);
+                acc = acc + pv[0];
+                acc = acc + pv[1];
+                acc = acc + pv[2];
+                acc = acc + pv[3];
+            }
+        }
+        __syncthreads();                  // the last chunk: the product waves' final barrier
+        if (lane < cnt) {
+            const v2i te = pair_of(lane);
+            out[(size_t)te[0] * E + te[1]] = acc;
+        }
+    } else {
+        // product waves: 256 threads x 4 units = 64 pairs x 16 units of 8 k per
+        // chunk; 16 consecutive threads cover one pair's 128 k (256 contiguous
+        // bytes of bf16)
+        const int htid = tid - 64;
+        const T *xr[4], *wrow[4];
+        int l[4], k8[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int u = i * 256 + htid;
+            l[i] = u >> 4;
+            k8[i] = u & 15;
+            const v2i te = pair_of(l[i] < cnt ? l[i] : 0);
+            xr[i] = x + (size_t)te[0] * H + 8 * k8[i];
+            wrow[i] = wr + (size_t)te[1] * H + 8 * k8[i];
+        }
+        ChainUnit<T> ua[4], ub[4];
+        // chunk 0 into buffer 0 and chunk 1's loads in flight, then per
+        // iteration c: products of chunk c + 1 (loaded one iteration ago)
+        // into buffer (c + 1) & 1 and chunk c + 2's loads issued
+#pragma unroll
+        for (int i = 0; i < 4; ++i) chain_unit_load(ua[i], xr[i], wrow[i]);
+        if (nc > 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) chain_unit_load(ub[i], xr[i] + kCK, wrow[i] + kCK);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) chain_unit_products(ua[i], prod + l[i] * kCR + 8 * k8[i]);
+        for (int c = 0; c < nc; ++c) {
+            __syncthreads();
+            if (c + 1 < nc) {
+                ChainUnit<T> *cur = (c & 1) ? ua : ub;   // chunk c + 1
+                ChainUnit<T> *nxt = (c & 1) ? ub : ua;   // chunk c + 2 goes where chunk c was
+                float *dst = prod + ((c + 1) & 1) * 64 * kCR;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) chain_unit_products(cur[i], dst + l[i] * kCR + 8 * k8[i]);
+                if (c + 2 < nc) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        chain_unit_load(nxt[i], xr[i] + (size_t)(c + 2) * kCK, wrow[i] + (size_t)(c + 2) * kCK);
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kChainThreads) void router_chain_kernel(const T *__restrict__ x,
                                                                      const T *__restrict__ wr, int E, int H,
@@ -100,93 +177,18 @@ __global__ __launch_bounds__(kChainThreads) void router_chain_kernel(const T *__
                                                                      int64_t npairs, float *__restrict__ out,
                                                                      uint32_t *__restrict__ mask, int64_t mask_words)
 {
-#pragma clang fp contract(off)
     clear_mask(mask, mask_words);
     extern __shared__ __attribute__((aligned(16))) float prod[];   // [2][64][kCR]
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t n = pairs ? (int64_t)*npairs_dev : npairs;
-    const int nc = H / kCK;
-    // product waves: 256 threads x 4 units = 64 pairs x 16 units of 8 k per chunk;
-    // 16 consecutive threads cover one pair's 128 k (256 contiguous bytes of bf16)
-    const int htid = tid - 64;
     for (int64_t base = (int64_t)blockIdx.x * 64; base < n; base += (int64_t)gridDim.x * 64) {
         const int cnt = (int)min((int64_t)64, n - base);
-        if (wave == 0) {
-            float acc = 0.0f;
-            for (int c = 0; c < nc; ++c) {
-                __syncthreads();              // chunk c's products are in buffer c & 1
-                const float *row = prod + (c & 1) * 64 * kCR + lane * kCR;
-#pragma unroll
-                for (int k = 0; k < kCK; k += 4) {
-                    const v4f pv = *reinterpret_cast<const v4f *>(row + k);
-                    acc = acc + pv[0];
-                    acc = acc + pv[1];
-                    acc = acc + pv[2];
-                    acc = acc + pv[3];
-                }
-            }
-            __syncthreads();                  // the last chunk: the product waves' final barrier
-            if (lane < cnt) {
-                int t, e;
-                if (pairs) {
-                    t = pairs[2 * (base + lane)];
-                    e = pairs[2 * (base + lane) + 1];
-                } else {
-                    t = (int)((base + lane) / E);
-                    e = (int)((base + lane) % E);
-                }
-                out[(size_t)t * E + e] = acc;
-            }
-        } else {
-            const T *xr[4], *wrow[4];
-            int l[4], k8[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int u = i * 256 + htid;
-                l[i] = u >> 4;
-                k8[i] = u & 15;
-                const int64_t pp = base + (l[i] < cnt ? l[i] : 0);
-                int t, e;
-                if (pairs) {
-                    t = pairs[2 * pp];
-                    e = pairs[2 * pp + 1];
-                } else {
-                    t = (int)(pp / E);
-                    e = (int)(pp % E);
-                }
-                xr[i] = x + (size_t)t * H + 8 * k8[i];
-                wrow[i] = wr + (size_t)e * H + 8 * k8[i];
-            }
-            ChainUnit<T> ua[4], ub[4];
-            // chunk 0 into buffer 0 and chunk 1's loads in flight, then per
-            // iteration c: products of chunk c + 1 (loaded one iteration ago)
-            // into buffer (c + 1) & 1 and chunk c + 2's loads issued
-#pragma unroll
-            for (int i = 0; i < 4; ++i) chain_unit_load(ua[i], xr[i], wrow[i]);
-            if (nc > 1) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) chain_unit_load(ub[i], xr[i] + kCK, wrow[i] + kCK);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) chain_unit_products(ua[i], prod + l[i] * kCR + 8 * k8[i]);
-            for (int c = 0; c < nc; ++c) {
-                __syncthreads();
-                if (c + 1 < nc) {
-                    ChainUnit<T> *cur = (c & 1) ? ua : ub;   // chunk c + 1
-                    ChainUnit<T> *nxt = (c & 1) ? ub : ua;   // chunk c + 2 goes where chunk c was
-                    float *dst = prod + ((c + 1) & 1) * 64 * kCR;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) chain_unit_products(cur[i], dst + l[i] * kCR + 8 * k8[i]);
-                    if (c + 2 < nc) {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            chain_unit_load(nxt[i], xr[i] + (size_t)(c + 2) * kCK, wrow[i] + (size_t)(c + 2) * kCK);
-                    }
-                }
-            }
-            __syncthreads();
-        }
+        chain_group(x, wr, E, H, cnt,
+                    [&](int l) -> v2i {
+                        const int64_t pp = base + l;
+                        if (pairs) return v2i{pairs[2 * pp], pairs[2 * pp + 1]};
+                        return v2i{(int)(pp / E), (int)(pp % E)};
+                    },
+                    out, prod);
     }
 }
 
@@ -580,6 +582,8 @@ struct CertArgs {
     int32_t *pairs;       // [T * E][2]: (token, expert) pairs to recompute in gemm_cpu order
     int32_t *cnt;         // [0] pairs, [1] flagged tokens (zeroed by the logits launch)
     int32_t *flagged;     // [T]: tokens whose routing waits for their exact logits
+    int32_t *fbase;       // [T]: first pair of flagged token j in the pair list
+    int32_t *fcnt;        // [T]: its number of pairs
     float margin_scale;   // 1; larger values widen every interval (tests of the exact path)
 };
 
@@ -814,7 +818,10 @@ __device__ __forceinline__ void route_token(int t, int lane, const float *__rest
             int pbase = 0;
             if (lane == 0) {
                 pbase = atomicAdd(&ca.cnt[0], total);
-                ca.flagged[atomicAdd(&ca.cnt[1], 1)] = t;
+                const int slot = atomicAdd(&ca.cnt[1], 1);
+                ca.flagged[slot] = t;
+                ca.fbase[slot] = pbase;
+                ca.fcnt[slot] = total;
             }
             pbase = __builtin_amdgcn_readlane(pbase, 0);
             int o = pbase + incl - n_amb;
@@ -873,6 +880,79 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ lo
     }
 }
 
+// The exact pass and the second routing in one launch (decode batches): block
+// j takes flagged token j, computes its listed pairs in gemm_cpu order
+// (chain_group, 64 at a time) into its flog row, and wave 0 then routes the
+// token on that row.  The token's exact logits are written and read by wave 0
+// of the same block (ordered by a block barrier), so no other block is waited
+// for.
+template <typename T, int NV>
+__global__ __launch_bounds__(kChainThreads) void router_token_exact_kernel(
+    const T *__restrict__ x, const T *__restrict__ wr, const float *__restrict__ bias, int Tn, int E, int H, int k,
+    int n_group, int topk_group, int renorm, float scaling, int32_t *__restrict__ idx, float *__restrict__ wout,
+    uint32_t *__restrict__ mask, int mask_words, float *__restrict__ logits_out, CertArgs ca)
+{
+    extern __shared__ __attribute__((aligned(16))) float prod[];   // [2][64][kCR]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int n = ca.cnt[1];
+    for (int j = blockIdx.x; j < n; j += gridDim.x) {
+        const int t = ca.flagged[j], base = ca.fbase[j], np = ca.fcnt[j];
+        for (int g = 0; g < np; g += 64)
+            chain_group(x, wr, E, H, min(64, np - g),
+                        [&](int l) -> v2i {
+                            const int pp = base + g + l;
+                            return v2i{ca.pairs[2 * (size_t)pp], ca.pairs[2 * (size_t)pp + 1]};
+                        },
+                        ca.flog, prod);
+        // the chain lanes' stores are read by other lanes of wave 0: the
+        // barrier's workgroup fence orders them
+        __syncthreads();
+        if (wave == 0)
+            route_token<NV, 2>(t, lane, nullptr, bias, Tn, E, k, n_group, topk_group, renorm, scaling, idx, wout, mask,
+                               mask_words, 1, logits_out, ca);
+    }
+}
+
+int launch_router_token_exact(const void *x, const void *wr, int dtype, const float *bias, int64_t T, int64_t E,
+                              int64_t H, int64_t k, int64_t n_group, int64_t topk_group, int renorm, float scaling,
+                              int32_t *idx, float *w, uint32_t *mask, int mask_words, float *logits_out,
+                              const CertState &cert, hipStream_t st)
+{
+    if (T == 0) return XS_OK;
+    CertArgs ca = {cert.dpart, cert.kblocks, cert.flog, cert.pairs, cert.cnt, cert.flagged, cert.fbase, cert.fcnt,
+                   cert.margin_scale};
+    const size_t smem = sizeof(float) * 2 * 64 * kCR;
+    // one block per token at most (T <= 256 here); blocks past the flagged count exit
+    dim3 grid((unsigned)std::min(T, (int64_t)256)), block(kChainThreads);
+    const int nv = (int)((E + 63) / 64);
+#define XS_TOKEN_EXACT(TT, NVV)                                                                              \
+    do {                                                                                                     \
+        static bool attr_set = false;                                                                        \
+        if (!attr_set) {                                                                                     \
+            XS_HIP(hipFuncSetAttribute((const void *)router_token_exact_kernel<TT, NVV>,                      \
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));               \
+            attr_set = true;                                                                                 \
+        }                                                                                                    \
+        router_token_exact_kernel<TT, NVV><<<grid, block, smem, st>>>(                                       \
+            (const TT *)x, (const TT *)wr, bias, (int)T, (int)E, (int)H, (int)k, (int)n_group, (int)topk_group, \
+            renorm, scaling, idx, w, mask, mask_words, logits_out, ca);                                      \
+    } while (0)
+#define XS_TOKEN_EXACT_NV(TT)                   \
+    if (nv <= 1) XS_TOKEN_EXACT(TT, 1);         \
+    else if (nv <= 2) XS_TOKEN_EXACT(TT, 2);    \
+    else if (nv <= 4) XS_TOKEN_EXACT(TT, 4);    \
+    else if (nv <= 8) XS_TOKEN_EXACT(TT, 8);    \
+    else XS_TOKEN_EXACT(TT, 16);
+    // the certified router takes bf16 inputs only (f32 inputs use the chain router)
+    if (dtype != XS_BF16) return set_error(XS_ERR_INVALID, "certified router: bf16 inputs only");
+    XS_TOKEN_EXACT_NV(uint16_t)
+#undef XS_TOKEN_EXACT_NV
+#undef XS_TOKEN_EXACT
+    XS_LAUNCH_CHECK();
+    return XS_OK;
+}
+
 int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, int64_t k,
                  int64_t n_group, int64_t topk_group, int renorm, float scaling, int32_t *idx,
                  float *w, uint32_t *mask, int mask_words, int nsplit, float *logits_out,
@@ -887,6 +967,8 @@ int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, i
         ca.pairs = cert->pairs;
         ca.cnt = cert->cnt;
         ca.flagged = cert->flagged;
+        ca.fbase = cert->fbase;
+        ca.fcnt = cert->fcnt;
         ca.margin_scale = cert->margin_scale;
     }
     // MODE 2 loops over the flagged tokens: a grid for a quarter of them at most
