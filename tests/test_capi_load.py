@@ -253,3 +253,36 @@ def test_packed_gemm_validation_without_gpu(monkeypatch):
     assert rc == 1 and b"null" in L.xs_last_error()
     # M = 0: nothing to do, nothing launched
     assert L.xs_gemm_fp8_blockscale_packed(v, v, v, 0, 4096, 4096, v, v, ws, None) == 0
+
+
+def test_router_stats_without_gpu():
+    """xs_moe_router_stats validates its params and reports 0, 0 for routers
+    other than the certified one without touching a GPU."""
+    import xs_moe_capi as X
+    L = X.lib()
+    out = (ctypes.c_int64 * 2)(7, 7)
+    p = X.MoeParams(16, 4096, 2048, 256, 6, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 1, X.XS_ROUTER_MFMA)
+    assert L.xs_moe_router_stats(ctypes.byref(p), ctypes.c_void_p(4096), out, None) == 0
+    assert list(out) == [0, 0]
+    p.router_exact = X.XS_ROUTER_CHAIN
+    assert L.xs_moe_router_stats(ctypes.byref(p), ctypes.c_void_p(4096), out, None) == 0 and list(out) == [0, 0]
+    p.router_exact = 3
+    assert L.xs_moe_router_stats(ctypes.byref(p), ctypes.c_void_p(4096), out, None) == 1
+    assert b"router_exact must be" in L.xs_last_error()
+    assert L.xs_moe_router_stats(ctypes.byref(p), ctypes.c_void_p(4096), None, None) == 1
+
+
+def test_certified_router_workspace_grows_with_its_lists():
+    """The certified router's workspace regions (bound terms per slice, logit
+    rows and pair list of the listed tokens, the token list with pair ranges)
+    are there only when it is the router."""
+    import xs_moe_capi as X
+    L = X.lib()
+    sizes = {}
+    for r in (X.XS_ROUTER_MFMA, X.XS_ROUTER_CERTIFIED, X.XS_ROUTER_CHAIN):
+        p = X.MoeParams(16, 4096, 2048, 256, 6, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 1, r)
+        sizes[r] = L.xs_moe_workspace_size(ctypes.byref(p))
+    T, E, nsplit = 16, 256, 16
+    extra = 4 * T * E * nsplit + 4 * T * E + 8 * T * E + 3 * 4 * T + 8
+    assert sizes[X.XS_ROUTER_CERTIFIED] - sizes[X.XS_ROUTER_MFMA] >= extra
+    assert sizes[X.XS_ROUTER_CHAIN] < sizes[X.XS_ROUTER_MFMA]       # one logit slice instead of 16
