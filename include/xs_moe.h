@@ -306,7 +306,8 @@ typedef struct {
     int tile_rows;       /* rows per tile of the routed GEMMs */
     int routed_gemm;     /* xs_gemm_kind of the routed experts' gate_up and down */
     int shared_gemm;     /* xs_gemm_kind of the shared expert (FP8 layers: the routed launch); -1: none */
-    int fused_combine;   /* 1: the down GEMM sums each token's rows itself */
+    int fused_combine;   /* 1: the down GEMM sums each token's rows itself; 2: the shared
+                          * expert's down launch sums them (XS_SHARED_COMBINE=1) */
 } xs_moe_plan_t;
 int xs_moe_plan(const xs_moe_params *p, const xs_moe_tensors *t, xs_moe_plan_t *out);
 

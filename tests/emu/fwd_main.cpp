@@ -6,6 +6,8 @@
 // frag: 1 also the weights in fragment order (xs_pack_weight_*_frag, run
 // emulated), 2 only those (packed-only layer); with XS_WEIGHT_DIRECT=1 the
 // forward then takes the weight-direct GEMMs.
+// toggle NAME=VALUE: a second forward with that environment switch set must
+// give the same output bits ("toggle mismatches N", its plan printed too).
 // Prints the plan, then "idx mismatches N" etc. (routing, weights, counts,
 // offsets, permutation and inverse against the oracle's routing of the logits
 // the forward routed on), "ref idx mismatches N" (against the oracle's routing
@@ -27,6 +29,7 @@ int main(int argc, char **argv)
     const int xf32 = (int)arg(10, 0);
     const double zipf = arg(11, 0);
     const int norm = (int)arg(12, 0), resid = (int)arg(13, 0), noalloc = (int)arg(14, 0), frag = (int)arg(15, 0);
+    const char *toggle = argc > 16 ? argv[16] : nullptr;
     g_math = true;
     std::mt19937 rng(seed);
     std::normal_distribution<float> nd(0.f, 1.f);
@@ -152,6 +155,25 @@ int main(int argc, char **argv)
         printf("exact pass logits %lld tokens %lld\n", (long long)st[0], (long long)st[1]);
     }
 
+    if (toggle) {
+        std::string kv(toggle);
+        const size_t eq = kv.find('=');
+        setenv(kv.substr(0, eq).c_str(), kv.substr(eq + 1).c_str(), 1);
+        xs_moe_plan_t pl2;
+        if (xs_moe_plan(&p, &t, &pl2)) { printf("plan failed: %s\n", xs_last_error()); return 1; }
+        printf("toggle plan tile_rows %d routed %d shared %d fused %d\n", pl2.tile_rows, pl2.routed_gemm, pl2.shared_gemm,
+               pl2.fused_combine);
+        std::vector<uint8_t> first((uint8_t *)out, (uint8_t *)out + (size_t)T * H * el);
+        memset(out, 0xEE, (size_t)T * H * el);
+        if (resid && res == out) { printf("toggle with an in-place residual is not supported\n"); return 1; }
+        const size_t wsb = xs_moe_workspace_size(&p);
+        void *ws2 = emu_alloc(wsb, "workspace 2");
+        memset(ws2, 0xA7, wsb);
+        if ((rc = xs_moe_forward(&p, &t, ws2, wsb, nullptr))) { printf("forward failed: %d %s\n", rc, xs_last_error()); return 1; }
+        long bad = 0;
+        for (size_t i = 0; i < first.size(); ++i) bad += first[i] != ((uint8_t *)out)[i];
+        printf("toggle mismatches %ld\n", bad);
+    }
     // the oracle on the (normalized) x the router read
     std::vector<uint8_t> xin((size_t)T * H * el);
     if (norm) xo_rmsnorm(x, nw, xf32 ? 0 : 1, T, H, 1e-6f, xin.data());

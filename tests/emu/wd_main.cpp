@@ -130,6 +130,9 @@ int main(int argc, char **argv)
     g2.Bp = w2p; g2.Bshp = sw2p;
     g2.offsets = offsets; g2.tile_tab = (const int32_t *)tab; g2.E = E; g2.K = I; g2.N = H; g2.bm = BM;
     g2.Cf = y; g2.ldc = H;
+    // every tile of the table: the shared segment (when present) and the routed experts
+    g1.e_lo = g2.e_lo = 0;
+    g1.e_hi = g2.e_hi = E + 1;
 
     for (int pass = 0; pass < 2; ++pass) {
         const GemmArgs &a = pass ? g2 : g1;

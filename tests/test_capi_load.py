@@ -286,3 +286,24 @@ def test_certified_router_workspace_grows_with_its_lists():
     extra = 4 * T * E * nsplit + 4 * T * E + 8 * T * E + 3 * 4 * T + 8
     assert sizes[X.XS_ROUTER_CERTIFIED] - sizes[X.XS_ROUTER_MFMA] >= extra
     assert sizes[X.XS_ROUTER_CHAIN] < sizes[X.XS_ROUTER_MFMA]       # one logit slice instead of 16
+
+
+def test_shared_combine_plan(monkeypatch):
+    """XS_SHARED_COMBINE=1 moves the combine into the shared expert's down
+    launch on the tall tiles only, and never when the y_rows inspection output
+    (which needs the shared rows stored) is asked for."""
+    import xs_moe_capi as X
+    for n in ("XS_MOE_GEMM", "XS_FUSE_COMBINE", "XS_WEIGHT_DIRECT"):
+        monkeypatch.delenv(n, raising=False)
+    p = X.MoeParams(8192, 4096, 2048, 256, 6, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 1, 1)
+    assert not X.plan(p, _stand_in_tensors(X))["shared_combine"]
+    monkeypatch.setenv("XS_SHARED_COMBINE", "1")
+    got = X.plan(p, _stand_in_tensors(X))
+    assert got["shared_combine"] and not got["fused_combine"] and got["routed"] == "tall"
+    t = _stand_in_tensors(X)
+    t.y_rows = ctypes.c_void_p(4096)
+    assert not X.plan(p, t)["shared_combine"]
+    p.T = 16                                   # decode: not the tall tiles
+    assert not X.plan(p, _stand_in_tensors(X))["shared_combine"]
+    p.T, p.has_shared = 8192, 0                # no shared expert
+    assert not X.plan(p, _stand_in_tensors(X, shared=False))["shared_combine"]

@@ -54,12 +54,17 @@ def fwd_emu(tmp_path_factory):
     shutil.rmtree(d, ignore_errors=True)
 
 
-# name, env, (T H I E k seed fp4 shared router x_f32 zipf norm residual noalloc [frag]), expected routed GEMM
+# name, env, (T H I E k seed fp4 shared router x_f32 zipf norm residual noalloc [frag [toggle]]), expected routed GEMM
 CASES = [
     ("tiled", {"XS_MOE_STREAM": "0"}, (64, 256, 256, 8, 2, 1, 0, 1, 1, 0, 0, 0, 0, 0), 0),
     ("stream", {}, (64, 256, 256, 8, 2, 1, 0, 1, 1, 0, 0, 0, 0, 0), 1),
     ("tall", {}, (300, 256, 256, 4, 2, 2, 0, 1, 1, 0, 1.1, 0, 0, 0), 2),
     ("tall_fused_combine", {"XS_FUSE_COMBINE": "1"}, (300, 256, 256, 4, 2, 2, 0, 1, 1, 0, 1.1, 0, 0, 0), 2),
+    # the combine in the shared expert's down epilogue: the same bits as the
+    # separate combine (a second forward with the switch set), with the
+    # pre-norm and a residual, and for f32 layers
+    ("tall_shared_combine", {}, (300, 256, 256, 4, 2, 3, 0, 1, 1, 0, 1.1, 1, 1, 0, 0, "XS_SHARED_COMBINE=1"), 2),
+    ("tall_shared_combine_f32", {}, (300, 256, 256, 4, 2, 4, 0, 1, 2, 1, 1.1, 0, 1, 0, 0, "XS_SHARED_COMBINE=1"), 2),
     ("c1_f32_chain", {}, (64, 256, 128, 8, 2, 11, 0, 1, 2, 1, 0, 0, 0, 0), 0),
     ("mxfp4_stream", {}, (48, 512, 512, 16, 6, 3, 1, 1, 1, 0, 0, 0, 0, 0), 1),
     ("mxfp4_tiled64", {"XS_MOE_STREAM": "0"}, (160, 512, 512, 16, 6, 4, 1, 1, 1, 0, 0, 0, 0, 0), 0),
@@ -99,6 +104,9 @@ def test_forward_emulated(fwd_emu, name, env, args, routed):
     router = args[8]
     for n in ("idx", "w", "counts", "offsets", "perm", "inv"):
         assert c[n] == 0, (n, out)
+    if len(args) > 15:
+        assert re.search(r"toggle plan .* fused 2", out), out
+        assert c["toggle"] == 0, out
     if router in (1, 2):
         assert c["ref idx"] == 0, out
     if router == 2:

@@ -275,6 +275,32 @@ def test_moe_fused_combine_matches_separate(bf16, monkeypatch):
     assert max_abs_rel(outs["1"][0].float().cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("bf16", [True, False])
+def test_moe_shared_combine_matches_separate(bf16, monkeypatch):
+    """The combine in the shared expert's down epilogue (XS_SHARED_COMBINE=1:
+    routed rows first, then the shared segment sums each token's rows in the
+    combine's order) against the separate combine kernel: identical bits, with
+    and without a residual and with the residual aliasing the output."""
+    monkeypatch.setenv("XS_MOE_GEMM", "wide")
+    c = make_case(700, 1024, 1024, 16, 4, seed=22, zipf=1.1, bf16=bf16)
+    g = to_device(c)
+    layer = layer_for(c, g, router_exact=True)
+    res = torch.randn(700, 1024, device="cuda").to(g["x"].dtype)
+    outs = {}
+    for sc in ("1", "0"):
+        monkeypatch.setenv("XS_SHARED_COMBINE", sc)
+        assert layer.plan(700)["shared_combine"] == (sc == "1")
+        a = layer.forward(g["x"])
+        r = layer.forward(g["x"], residual=res)
+        inplace = res.clone()
+        layer.forward(g["x"], out=inplace, residual=inplace)
+        torch.cuda.synchronize()
+        assert torch.equal(r, inplace)
+        outs[sc] = (a, r)
+    assert torch.equal(outs["1"][0], outs["0"][0])
+    assert torch.equal(outs["1"][1], outs["0"][1])
+
+
 def test_moe_group_limited_and_scaling():
     c = make_case(96, 512, 128, 32, 4, seed=3)
     g = to_device(c)

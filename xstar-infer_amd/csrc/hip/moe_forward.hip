@@ -206,6 +206,7 @@ static int check_params(const xs_moe_params *p)
 struct Plan {
     int bm;
     bool wide, fused, direct, ddirect, direct4, sdirect, stream;
+    bool shcomb;   // tall-tile down GEMM: routed launch, then the shared segment with the combine in its epilogue
 };
 
 static int make_plan(const xs_moe_params *p, const xs_moe_tensors *t, Plan &pl)
@@ -267,7 +268,12 @@ static int make_plan(const xs_moe_params *p, const xs_moe_tensors *t, Plan &pl)
     const int stream_tiles = fp4 ? routed_tiles : routed_tiles + shared_tiles;
     const bool stream = !direct && !ddirect && !direct4 && stream_fits(bm, fp4, stream_tiles, rows_all) && (!fp4 || (H % 512 == 0 && I % 512 == 0)) &&
                         (sm == 2 || (sm == 1 && stream_items(true, (int)I, stream_tiles) >= 2 * (int64_t)stream_blocks()));
-    pl = Plan{bm, wide, fused, direct, ddirect, direct4, sdirect, stream};
+    // XS_SHARED_COMBINE=1: the combine in the shared expert's down epilogue
+    // (tall tiles; not with the y_rows inspection output, which needs the
+    // shared rows stored)
+    const bool shcomb = wide && !packed_only && !fused && !direct && shared_rows && !t->y_rows &&
+                        getenv_flag("XS_SHARED_COMBINE", false);
+    pl = Plan{bm, wide, fused, direct, ddirect, direct4, sdirect, stream, shcomb};
     return XS_OK;
 }
 
@@ -503,6 +509,24 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
         g2.As = WS(float, acts);
         g2.e_lo = 0;
         g2.e_hi = g1.e_hi;
+        if (pl.shcomb) {
+            // the routed rows first, then the shared segment, whose epilogue
+            // sums each token's rows in the combine's order and writes out
+            GemmArgs gr = g2;
+            gr.e_hi = (int)E;
+            if ((rc = launch_gemm_wide(gr, false, routed_tiles, st))) return rc;
+            GemmArgs gs = g2;
+            gs.e_lo = (int)E;
+            gs.shared_combine = 1;
+            gs.inv = inv;
+            gs.cw = w;
+            gs.topk = (int)k;
+            gs.shared_base = S;
+            gs.out = t->out;
+            gs.residual = t->residual;
+            gs.out_dtype = p->x_dtype;
+            rc = launch_gemm_wide(gs, false, shared_tiles, st);
+        } else
         rc = stream   ? launch_gemm_stream(g2, false, false, stream_tiles, rows_all, st)
              : direct ? launch_gemm_wd(g2, false, routed_tiles + shared_tiles, st)
              : ddirect ? launch_gemm_wdd(g2, false, routed_tiles + shared_tiles, st)
@@ -560,7 +584,7 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
     }
     // 5. weighted combine (+ shared), one cast to the output dtype
     if ((rc = prof_mark(6, st))) return rc;
-    if (!fused) {
+    if (!fused && !pl.shcomb) {
         rc = launch_combine(WS(float, y), inv, w, T, k, H, S, shared_rows ? 1 : 0, t->out, p->x_dtype, st,
                             t->residual);
         if (rc) return rc;
@@ -698,7 +722,7 @@ int xs_moe_plan(const xs_moe_params *p, const xs_moe_tensors *t, xs_moe_plan_t *
                        : pl.wide    ? XS_GEMM_TALL
                                     : XS_GEMM_TILED;
     out->shared_gemm = !p->has_shared ? -1 : !fp4 ? out->routed_gemm : pl.sdirect ? XS_GEMM_DIRECT_PREFILL : XS_GEMM_TILED;
-    out->fused_combine = pl.fused ? 1 : 0;
+    out->fused_combine = pl.fused ? 1 : pl.shcomb ? 2 : 0;
     return XS_OK;
 }
 

@@ -48,6 +48,12 @@ struct GemmArgs {
     // without a tile table
     int64_t sh_rows;
     int32_t *ccnt;             // [T, H/256] counters, zero on entry
+    // tall-tile down GEMM over the shared segment alone, with the weighted
+    // combine in its epilogue: each shared row's f32 result is summed with
+    // its token's routed rows (Cf, written by the routed launch before) in
+    // the combine's order and written to out; the shared row is not stored.
+    // Uses inv, cw, topk, shared_base, out, residual, out_dtype.
+    int shared_combine;
     void *out;                 // [T, H] of out_dtype
     const void *residual;      // [T, H] of out_dtype or NULL (may alias out)
     int out_dtype;

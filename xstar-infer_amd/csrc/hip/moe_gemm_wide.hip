@@ -146,6 +146,7 @@ __device__ __forceinline__ void store_f32_tile(const GemmArgs &a, const v4f (&ac
     const int r16 = lane & 15, g = lane >> 4;
     const int n0 = slab * 256;
     const bool fuse = a.fuse_combine != 0;
+    const bool shcomb = a.shared_combine != 0;
     float *fs = reinterpret_cast<float *>(smem);
     __syncthreads();   // every wave is past its loop: the ring is free for staging
 #pragma unroll
@@ -158,7 +159,53 @@ __device__ __forceinline__ void store_f32_tile(const GemmArgs &a, const v4f (&ac
             for (int j = 0; j < 4; ++j) *reinterpret_cast<v4f *>(fs + rl * FS + 64 * wn + 16 * j + 4 * g) = acc[i][j];
         }
         __syncthreads();
-        if (fuse) {
+        if (shcomb) {
+            // the combine of the tokens of these shared rows, slab columns
+            // n0 .. n0 + 255: acc = the shared row (f32, as it would be
+            // stored), then acc + w_j * y_j over the routed slots in order,
+            // then the residual, one cast (combine_kernel's arithmetic)
+#pragma unroll 2
+            for (int pass = 0; pass < HR / (NT / 64); ++pass) {
+                const int rl = (NT / 64) * pass + (tid >> 6), c = 4 * (tid & 63), row = h * HR + rl;
+                if (row >= rows) continue;
+                const int t = (int)(pos0 + row - a.shared_base);
+                v4f s = *reinterpret_cast<const v4f *>(fs + rl * FS + c);
+                v4f yv[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    if (j < a.topk)
+                        yv[j] = *reinterpret_cast<const v4f *>(a.Cf + (size_t)a.inv[(size_t)t * a.topk + j] * a.ldc +
+                                                               n0 + c);
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    if (j < a.topk) {
+                        const float wt = a.cw[(size_t)t * a.topk + j];
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) s[v] = s[v] + wt * yv[j][v];   // no contraction (pragma above)
+                    }
+                const size_t o = (size_t)t * a.N + n0 + c;
+                if (a.out_dtype == XS_BF16) {
+                    if (a.residual) {
+                        const v2i r = *reinterpret_cast<const v2i *>(reinterpret_cast<const uint16_t *>(a.residual) + o);
+                        s[0] = __uint_as_float((uint32_t)r[0] << 16) + s[0];
+                        s[1] = __uint_as_float((uint32_t)r[0] & 0xFFFF0000u) + s[1];
+                        s[2] = __uint_as_float((uint32_t)r[1] << 16) + s[2];
+                        s[3] = __uint_as_float((uint32_t)r[1] & 0xFFFF0000u) + s[3];
+                    }
+                    v2i pk;
+                    pk[0] = (int)((uint32_t)bf16_from_f32(s[0]) | ((uint32_t)bf16_from_f32(s[1]) << 16));
+                    pk[1] = (int)((uint32_t)bf16_from_f32(s[2]) | ((uint32_t)bf16_from_f32(s[3]) << 16));
+                    *reinterpret_cast<v2i *>(reinterpret_cast<uint16_t *>(a.out) + o) = pk;
+                } else {
+                    if (a.residual) {
+                        const v4f r = *reinterpret_cast<const v4f *>(reinterpret_cast<const float *>(a.residual) + o);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) s[v] = r[v] + s[v];
+                    }
+                    *reinterpret_cast<v4f *>(reinterpret_cast<float *>(a.out) + o) = s;
+                }
+            }
+        } else if (fuse) {
 #pragma unroll 4
             for (int pass = 0; pass < HR / (NT / 128); ++pass) {
                 const int rl = (NT / 128) * pass + (tid >> 7), c = 2 * (tid & 127), row = h * HR + rl;
@@ -552,7 +599,11 @@ __global__ __launch_bounds__(64 * NW) void moe_gemm_wide_kernel(GemmArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int4 *tab = reinterpret_cast<const int4 *>(a.tile_tab);   // shared + routed tiles
-    const int tiles = tab[0].x;
+    // the launch's range of the table (shared tiles come first): the shared
+    // segment alone, the routed experts alone, or both
+    int lo = 0, tiles = tab[0].x;
+    if (a.e_lo >= a.E) tiles = tab[0].y;
+    else if (a.e_hi <= a.E) lo = tab[0].y;
     int tile, slab;
     if (a.xcd_order) {
         // 1-D grid.  Blocks go round-robin to the 8 XCDs (linear id L to XCD
@@ -566,11 +617,11 @@ __global__ __launch_bounds__(64 * NW) void moe_gemm_wide_kernel(GemmArgs a)
         const int L = (int)blockIdx.x, j = L >> 3;
         const int sg = (L & 7) + 8 * (j >> 5), i = j & 31;
         const int g = sg / nq, q = sg - g * nq;
-        tile = 8 * g + (i >> 2);
+        tile = lo + 8 * g + (i >> 2);
         slab = 4 * q + (i & 3);
         if (tile >= tiles) return;
     } else {
-        tile = (int)blockIdx.y;
+        tile = lo + (int)blockIdx.y;
         slab = (int)blockIdx.x;
         if (tile >= tiles) return;
     }

@@ -295,12 +295,14 @@ def pack_weight_mxfp4_frag(w, s):
 def plan(params, tensors):
     """xs_moe_plan: the kernels xs_moe_forward would launch for these params and
     tensors (nothing runs; no GPU needed) as a dict: tile_rows, routed, shared
-    (names from GEMM_KINDS; shared None without a shared expert), fused_combine."""
+    (names from GEMM_KINDS; shared None without a shared expert), fused_combine
+    (the down GEMM sums each token's rows), shared_combine (the shared expert's
+    down launch does)."""
     out = MoePlan()
     check(lib().xs_moe_plan(C.byref(params), C.byref(tensors), C.byref(out)))
     kind = lambda k: None if k < 0 else GEMM_KINDS[k]  # noqa: E731
     return {"tile_rows": out.tile_rows, "routed": kind(out.routed_gemm), "shared": kind(out.shared_gemm),
-            "fused_combine": bool(out.fused_combine)}
+            "fused_combine": out.fused_combine == 1, "shared_combine": out.fused_combine == 2}
 
 
 class MoeLayer:
