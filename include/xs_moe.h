@@ -77,7 +77,8 @@ int xs_stream_synchronize(void *stream);
  * x [T, H], router_w [E, H], dtype XS_F32 or XS_BF16 (both the same);
  * logits [T, E] f32.  exact != 0: sequential-k f32 accumulation with separately
  * rounded products, bit-identical to gemm_cpu (gemm.h:57-83).  exact = 0 (bf16
- * only): bf16 MFMA with f32 accumulation.  H % 128 == 0. */
+ * only): bf16 MFMA with f32 accumulation.  H % 128 == 0; x and router_w
+ * 16-byte aligned. */
 int xs_moe_router_logits(const void *x, const void *router_w, int dtype, int64_t T, int64_t E,
                          int64_t H, int exact, float *logits, void *stream);
 

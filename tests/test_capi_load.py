@@ -307,3 +307,17 @@ def test_shared_combine_plan(monkeypatch):
     assert not X.plan(p, _stand_in_tensors(X))["shared_combine"]
     p.T, p.has_shared = 8192, 0                # no shared expert
     assert not X.plan(p, _stand_in_tensors(X, shared=False))["shared_combine"]
+
+
+def test_router_logits_validation_without_gpu():
+    """xs_moe_router_logits refuses bad shapes and misaligned operands before
+    any GPU call."""
+    import xs_moe_capi as X
+    L = X.lib()
+    v = ctypes.c_void_p(4096)
+    assert L.xs_moe_router_logits(v, v, X.XS_BF16, 4, 8, 200, 1, v, None) == 1
+    assert b"H % 128" in L.xs_last_error()
+    assert L.xs_moe_router_logits(ctypes.c_void_p(4098), v, X.XS_BF16, 4, 8, 256, 1, v, None) == 1
+    assert b"misaligned" in L.xs_last_error()
+    assert L.xs_moe_router_logits(v, v, 7, 4, 8, 256, 1, v, None) == 1
+    assert b"unsupported dtype" in L.xs_last_error()

@@ -1232,6 +1232,8 @@ int xs_moe_router_logits(const void *x, const void *router_w, int dtype, int64_t
     XS_REQUIRE(x && router_w && logits, "null pointer");
     XS_REQUIRE(dtype == XS_F32 || dtype == XS_BF16, "unsupported dtype");
     XS_REQUIRE(T >= 0 && E >= 1 && H >= 128 && H % 128 == 0, "shape mismatch: H %% 128 != 0");
+    XS_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)router_w & 15) == 0 && ((uintptr_t)logits & 3) == 0,
+               "misaligned operand: x and router_w need 16-byte, logits 4-byte alignment");
     return launch_router_logits(x, router_w, dtype, T, E, H, exact, logits, 1, (hipStream_t)stream);
 }
 
