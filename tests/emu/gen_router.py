@@ -33,7 +33,7 @@ def main(src_path, dev_path, int_path, out_path):
                 "template <int N>\n__device__ __forceinline__ void rt_wait_vm()",
                 "int launch_route(", "int router_kind(", "int router_logits_splits(",
                 "bool router_quantizes(", "int launch_router_logits(", "int launch_router_fix(",
-                "int launch_router_token_exact("]:
+                "int launch_route_block("]:
         body = drop_fn(body, sig)
     body = replace(body, "extern __shared__ __attribute__((aligned(16))) float prod[];",
                    "float *prod = reinterpret_cast<float *>(emu_smem());")

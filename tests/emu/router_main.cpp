@@ -12,8 +12,9 @@
 //   dup > 0: router rows E-dup..E-1 (and their biases) copy rows 0..dup-1
 //     (exact ties, broken by the lower index), every other copy with one
 //     element one bf16 step apart (near ties).
-//   path: how the exact pass runs: 0 as the forward does (one launch with a
-//     block per listed token for T <= 256, else the pair-parallel chain
+//   path: how the certified routing runs: 0 as the forward does (for
+//     T <= 256 one launch with a block per token that routes, runs the exact
+//     pass and routes again; else the routing launch, the pair-parallel chain
 //     launch and a second routing launch), 1 always the latter, 2 always the
 //     former.
 //   mode chain_bf16 / chain_f32: every logit in gemm_cpu order; prints
@@ -151,26 +152,26 @@ int main(int argc, char **argv)
         };
         emu_launch3(body, g, 1, 1, 256, 0, 8);
     };
-    route(1);
-    const int npairs = cnt[0], nflag = cnt[1];
     if (path == 2 || (path == 0 && T <= 256)) {
-        // a block per listed token (grid smaller than the count: blocks loop)
-        const unsigned grid = (unsigned)std::min(T, 3);
+        // one launch: a block per token routes it, runs the exact pass of its
+        // undecided pairs and routes it again
         auto body = [&] {
             switch (nv) {
-            case 1: router_token_exact_kernel<uint16_t, 1>(xb, wb, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, lout, ca); break;
-            case 2: router_token_exact_kernel<uint16_t, 2>(xb, wb, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, lout, ca); break;
-            default: router_token_exact_kernel<uint16_t, 4>(xb, wb, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, lout, ca);
+            case 1: route_block_kernel<uint16_t, 1>(xb, wb, part, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsplit, lout, ca); break;
+            case 2: route_block_kernel<uint16_t, 2>(xb, wb, part, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsplit, lout, ca); break;
+            default: route_block_kernel<uint16_t, 4>(xb, wb, part, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsplit, lout, ca);
             }
         };
-        emu_launch3(body, grid, 1, 1, kChainThreads, sizeof(float) * 2 * 64 * kCR, 3);
+        emu_launch3(body, T, 1, 1, kChainThreads, sizeof(float) * 2 * 64 * kCR, 3);
     } else {
+        route(1);
         const int64_t groups = (TE + 63) / 64;
         const unsigned grid = (unsigned)std::min<int64_t>(groups, 3);
         emu_launch3([&] { router_chain_kernel<uint16_t>(xb, wb, E, H, pairs, cnt, (int64_t)TE, flog, nullptr, 0); },
                     grid, 1, 1, kChainThreads, sizeof(float) * 2 * 64 * kCR, 3);
         route(2);
     }
+    const int npairs = cnt[0], nflag = cnt[1];
     // the oracle's routing of the reference logits, and of the logits routed on
     std::vector<int32_t> ridx((size_t)T * k), midx((size_t)T * k);
     std::vector<float> rw((size_t)T * k), mw((size_t)T * k);

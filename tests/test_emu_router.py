@@ -11,8 +11,9 @@ pass) every logit is.  The MFMA is modelled three ways (exact sum rounded
 once, k-order rounded adds, truncated adds); the bound must hold for each.
 Covers decode (split-K MFMA kernel) and prefill (LDS-ring tile kernel) logits,
 exact and near ties (duplicated router rows), group-limited routing, and E
-not a multiple of 64, and both forms of the exact pass (a block per listed
-token; pairs spread over blocks plus a second routing launch)."""
+not a multiple of 64, and both forms of the certified routing (one launch
+with a block per token that routes, runs the exact pass and routes again;
+routing, pair-parallel exact pass and second routing as three launches)."""
 import os
 import re
 import shutil
@@ -76,12 +77,12 @@ CERT_CASES = [
     ("groups", (32, 256, 8, 2048, 9, 8, 1, 0.1, 0, 8, 8, 4)),
     ("all_exact", (16, 256, 6, 2048, 4, 16, 1e30)),
     ("all_exact_groups", (8, 256, 8, 1024, 9, 4, 1e30, 0.1, 0, 0, 8, 4)),
-    # the exact pass the other way than the forward picks for the batch: the
-    # pair-parallel launch plus a routing launch at decode, one block per
-    # listed token at prefill
+    # the certified routing the other way than the forward picks for the
+    # batch: separate routing, pair-parallel exact pass and second routing
+    # launches at decode; one launch with a block per token at prefill
     ("decode16_pair_parallel", (16, 256, 6, 4096, 1, 16, 1, 0.1, 0, 0, 1, 1, 1)),
     ("all_exact_pair_parallel", (16, 256, 6, 2048, 4, 16, 1e30, 0.1, 0, 0, 1, 1, 1)),
-    ("prefill_tile_token_blocks", (300, 256, 6, 2048, 6, 4, 1, 0.1, 0, 0, 1, 1, 2)),
+    ("prefill_tile_route_blocks", (300, 256, 6, 2048, 6, 4, 1, 0.1, 0, 0, 1, 1, 2)),
 ]
 
 

@@ -382,26 +382,26 @@ int moe_forward(const xs_moe_params *p, const xs_moe_tensors *t, void *ws, size_
                               fold_quant ? WS(float, xs) : nullptr, certified ? &cs : nullptr);
     if (rc) return rc;
     if ((rc = prof_mark(2, st))) return rc;
-    rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
-                      p->routed_scaling, idx, w, mask, Wd, nsplit, t->logits, st, certified ? &cs : nullptr,
-                      certified ? 1 : 0);
-    if (rc) return rc;
-    if (certified) {
-        // the pairs the bound left undecided, in gemm_cpu order, then the
-        // listed tokens' routing on their patched logit rows: decode batches
-        // in one launch (a block per listed token), prefill as a pair-parallel
-        // launch and a routing launch
-        if (T <= 256) {
-            rc = launch_router_token_exact(xin, t->router_w, p->x_dtype, t->router_bias, T, E, H, k, p->n_group,
-                                           p->topk_group, p->renormalize, p->routed_scaling, idx, w, mask, Wd,
-                                           t->logits, cs, st);
-            if (rc) return rc;
-        } else {
-            if ((rc = launch_router_fix(xin, t->router_w, p->x_dtype, T, E, H, cs, st))) return rc;
-            rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
-                              p->routed_scaling, idx, w, mask, Wd, 1, t->logits, st, &cs, 2);
-            if (rc) return rc;
-        }
+    if (certified && T <= 256) {
+        // decode batches: routing, the exact pass of the pairs the bound
+        // leaves undecided and the second routing in the one route launch
+        rc = launch_route_block(xin, t->router_w, p->x_dtype, logits, t->router_bias, T, E, H, k, p->n_group,
+                                p->topk_group, p->renormalize, p->routed_scaling, idx, w, mask, Wd, nsplit, t->logits,
+                                cs, st);
+        if (rc) return rc;
+    } else {
+        rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
+                          p->routed_scaling, idx, w, mask, Wd, nsplit, t->logits, st, certified ? &cs : nullptr,
+                          certified ? 1 : 0);
+        if (rc) return rc;
+    }
+    if (certified && T > 256) {
+        // prefill: the undecided pairs in gemm_cpu order spread over blocks,
+        // then the listed tokens' routing on their patched logit rows
+        if ((rc = launch_router_fix(xin, t->router_w, p->x_dtype, T, E, H, cs, st))) return rc;
+        rc = launch_route(logits, t->router_bias, T, E, k, p->n_group, p->topk_group, p->renormalize,
+                          p->routed_scaling, idx, w, mask, Wd, 1, t->logits, st, &cs, 2);
+        if (rc) return rc;
     }
     // 3. permute: (expert, token)-sorted positions, tile offsets
     if ((rc = prof_mark(3, st))) return rc;

@@ -125,12 +125,13 @@ int launch_route(const float *logits, const float *bias, int64_t T, int64_t E, i
                  int64_t n_group, int64_t topk_group, int renorm, float scaling, int32_t *idx,
                  float *w, uint32_t *mask, int mask_words, int nsplit, float *logits_out,
                  hipStream_t st, const CertState *cert = nullptr, int mode = 0);
-// The exact pass and the listed tokens' routing in one launch (decode
-// batches, T <= 256): one block per flagged token.
-int launch_router_token_exact(const void *x, const void *wr, int dtype, const float *bias, int64_t T, int64_t E,
-                              int64_t H, int64_t k, int64_t n_group, int64_t topk_group, int renorm, float scaling,
-                              int32_t *idx, float *w, uint32_t *mask, int mask_words, float *logits_out,
-                              const CertState &cert, hipStream_t st);
+// Certified routing of decode batches (T <= 256) in one launch, in place of
+// launch_route: a block per token routes it and, when the bound leaves
+// experts undecided, computes their logits in gemm_cpu order and routes again.
+int launch_route_block(const void *x, const void *wr, int dtype, const float *logits, const float *bias, int64_t T,
+                       int64_t E, int64_t H, int64_t k, int64_t n_group, int64_t topk_group, int renorm, float scaling,
+                       int32_t *idx, float *w, uint32_t *mask, int mask_words, int nsplit, float *logits_out,
+                       const CertState &cert, hipStream_t st);
 // The exact (gemm_cpu order) logits of the listed pairs into cert->flog.
 int launch_router_fix(const void *x, const void *wr, int dtype, int64_t T, int64_t E, int64_t H,
                       const CertState &cert, hipStream_t st);

@@ -624,8 +624,9 @@ struct CertArgs {
 //     interval ends); when that step is not settled, or a logit or bound is
 //     not finite, every expert of the token is recomputed.
 //   MODE 2: route on flog (the exact logits of U patched in).
+// Returns (MODE 1) the token's listed pair range {first, count}; count 0: routed here.
 template <int NV, int MODE>
-__device__ __forceinline__ void route_token(int t, int lane, const float *__restrict__ logits,
+__device__ __forceinline__ v2i route_token(int t, int lane, const float *__restrict__ logits,
                                             const float *__restrict__ bias, int Tn, int E, int k, int n_group,
                                             int topk_group, int renorm, float scaling, int32_t *__restrict__ idx,
                                             float *__restrict__ wout, uint32_t *__restrict__ mask, int mask_words,
@@ -839,7 +840,7 @@ __device__ __forceinline__ void route_token(int t, int lane, const float *__rest
 #pragma unroll
             for (int i = 0; i < NV; ++i)
                 if (valid[i]) ca.flog[(size_t)t * E + lane + 64 * i] = lgv[i];
-            return;   // routed by MODE 2 once the pairs are exact
+            return v2i{pbase, total};   // routed by MODE 2 once the pairs are exact
         }
     }
     if (logits_out) {
@@ -853,6 +854,7 @@ __device__ __forceinline__ void route_token(int t, int lane, const float *__rest
         wout[(size_t)t * k + lane] = wv;
         if (mask && my_e >= 0) atomicOr(&mask[(size_t)my_e * mask_words + (t >> 5)], 1u << (t & 31));
     }
+    return v2i{0, 0};
 }
 
 // One wave per token (MODE 0, 1), or per listed token (MODE 2: the flagged
@@ -880,75 +882,82 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ lo
     }
 }
 
-// The exact pass and the second routing in one launch (decode batches): block
-// j takes flagged token j, computes its listed pairs in gemm_cpu order
-// (chain_group, 64 at a time) into its flog row, and wave 0 then routes the
-// token on that row.  The token's exact logits are written and read by wave 0
-// of the same block (ordered by a block barrier), so no other block is waited
-// for.
+// Certified routing of decode batches in one launch: a block of
+// kChainThreads threads per token.  Wave 0 routes the token (MODE 1); when
+// the bound leaves experts undecided, the whole block computes their logits in
+// gemm_cpu order (chain_group over the pairs wave 0 listed) into the token's
+// flog row, and wave 0 routes it again (MODE 2).  Block barriers order wave
+// 0's listing before the other waves read it, and the chain lanes' stores
+// before wave 0's second routing reads them.  No launch is added to the
+// approximate router's.
 template <typename T, int NV>
-__global__ __launch_bounds__(kChainThreads) void router_token_exact_kernel(
-    const T *__restrict__ x, const T *__restrict__ wr, const float *__restrict__ bias, int Tn, int E, int H, int k,
-    int n_group, int topk_group, int renorm, float scaling, int32_t *__restrict__ idx, float *__restrict__ wout,
-    uint32_t *__restrict__ mask, int mask_words, float *__restrict__ logits_out, CertArgs ca)
+__global__ __launch_bounds__(kChainThreads) void route_block_kernel(
+    const T *__restrict__ x, const T *__restrict__ wr, const float *__restrict__ logits,
+    const float *__restrict__ bias, int Tn, int E, int H, int k, int n_group, int topk_group, int renorm,
+    float scaling, int32_t *__restrict__ idx, float *__restrict__ wout, uint32_t *__restrict__ mask, int mask_words,
+    int nsplit, float *__restrict__ logits_out, CertArgs ca)
 {
-    extern __shared__ __attribute__((aligned(16))) float prod[];   // [2][64][kCR]
+    extern __shared__ __attribute__((aligned(16))) float prod[];   // [2][64][kCR]; [0..1] first the pair range
+    int *range = reinterpret_cast<int *>(prod);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    const int n = ca.cnt[1];
-    for (int j = blockIdx.x; j < n; j += gridDim.x) {
-        const int t = ca.flagged[j], base = ca.fbase[j], np = ca.fcnt[j];
-        for (int g = 0; g < np; g += 64)
-            chain_group(x, wr, E, H, min(64, np - g),
-                        [&](int l) -> v2i {
-                            const int pp = base + g + l;
-                            return v2i{ca.pairs[2 * (size_t)pp], ca.pairs[2 * (size_t)pp + 1]};
-                        },
-                        ca.flog, prod);
-        // the chain lanes' stores are read by other lanes of wave 0: the
-        // barrier's workgroup fence orders them
-        __syncthreads();
-        if (wave == 0)
-            route_token<NV, 2>(t, lane, nullptr, bias, Tn, E, k, n_group, topk_group, renorm, scaling, idx, wout, mask,
-                               mask_words, 1, logits_out, ca);
+    const int t = blockIdx.x;
+    if (wave == 0) {
+        const v2i r = route_token<NV, 1>(t, lane, logits, bias, Tn, E, k, n_group, topk_group, renorm, scaling, idx,
+                                         wout, mask, mask_words, nsplit, logits_out, ca);
+        if (lane == 0) {
+            range[0] = r[0];
+            range[1] = r[1];
+        }
     }
+    __syncthreads();
+    const int base = range[0], np = range[1];
+    if (np == 0) return;                  // routed by wave 0 (the whole block leaves together)
+    __syncthreads();                      // every wave has its copy: the chain may reuse the LDS
+    for (int g = 0; g < np; g += 64)
+        chain_group(x, wr, E, H, min(64, np - g),
+                    [&](int l) -> v2i {
+                        const int pp = base + g + l;
+                        return v2i{ca.pairs[2 * (size_t)pp], ca.pairs[2 * (size_t)pp + 1]};
+                    },
+                    ca.flog, prod);
+    __syncthreads();
+    if (wave == 0)
+        route_token<NV, 2>(t, lane, nullptr, bias, Tn, E, k, n_group, topk_group, renorm, scaling, idx, wout, mask,
+                           mask_words, 1, logits_out, ca);
 }
 
-int launch_router_token_exact(const void *x, const void *wr, int dtype, const float *bias, int64_t T, int64_t E,
-                              int64_t H, int64_t k, int64_t n_group, int64_t topk_group, int renorm, float scaling,
-                              int32_t *idx, float *w, uint32_t *mask, int mask_words, float *logits_out,
-                              const CertState &cert, hipStream_t st)
+int launch_route_block(const void *x, const void *wr, int dtype, const float *logits, const float *bias, int64_t T,
+                       int64_t E, int64_t H, int64_t k, int64_t n_group, int64_t topk_group, int renorm, float scaling,
+                       int32_t *idx, float *w, uint32_t *mask, int mask_words, int nsplit, float *logits_out,
+                       const CertState &cert, hipStream_t st)
 {
     if (T == 0) return XS_OK;
+    // the certified router takes bf16 inputs only (f32 inputs use the chain router)
+    if (dtype != XS_BF16) return set_error(XS_ERR_INVALID, "certified router: bf16 inputs only");
     CertArgs ca = {cert.dpart, cert.kblocks, cert.flog, cert.pairs, cert.cnt, cert.flagged, cert.fbase, cert.fcnt,
                    cert.margin_scale};
     const size_t smem = sizeof(float) * 2 * 64 * kCR;
-    // one block per token at most (T <= 256 here); blocks past the flagged count exit
-    dim3 grid((unsigned)std::min(T, (int64_t)256)), block(kChainThreads);
+    dim3 grid((unsigned)T), block(kChainThreads);
     const int nv = (int)((E + 63) / 64);
-#define XS_TOKEN_EXACT(TT, NVV)                                                                              \
-    do {                                                                                                     \
-        static bool attr_set = false;                                                                        \
-        if (!attr_set) {                                                                                     \
-            XS_HIP(hipFuncSetAttribute((const void *)router_token_exact_kernel<TT, NVV>,                      \
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));               \
-            attr_set = true;                                                                                 \
-        }                                                                                                    \
-        router_token_exact_kernel<TT, NVV><<<grid, block, smem, st>>>(                                       \
-            (const TT *)x, (const TT *)wr, bias, (int)T, (int)E, (int)H, (int)k, (int)n_group, (int)topk_group, \
-            renorm, scaling, idx, w, mask, mask_words, logits_out, ca);                                      \
+#define XS_ROUTE_BLOCK(NVV)                                                                                    \
+    do {                                                                                                       \
+        static bool attr_set = false;                                                                          \
+        if (!attr_set) {                                                                                       \
+            XS_HIP(hipFuncSetAttribute((const void *)route_block_kernel<uint16_t, NVV>,                         \
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));                 \
+            attr_set = true;                                                                                   \
+        }                                                                                                      \
+        route_block_kernel<uint16_t, NVV><<<grid, block, smem, st>>>(                                          \
+            (const uint16_t *)x, (const uint16_t *)wr, logits, bias, (int)T, (int)E, (int)H, (int)k, (int)n_group, \
+            (int)topk_group, renorm, scaling, idx, w, mask, mask_words, nsplit, logits_out, ca);               \
     } while (0)
-#define XS_TOKEN_EXACT_NV(TT)                   \
-    if (nv <= 1) XS_TOKEN_EXACT(TT, 1);         \
-    else if (nv <= 2) XS_TOKEN_EXACT(TT, 2);    \
-    else if (nv <= 4) XS_TOKEN_EXACT(TT, 4);    \
-    else if (nv <= 8) XS_TOKEN_EXACT(TT, 8);    \
-    else XS_TOKEN_EXACT(TT, 16);
-    // the certified router takes bf16 inputs only (f32 inputs use the chain router)
-    if (dtype != XS_BF16) return set_error(XS_ERR_INVALID, "certified router: bf16 inputs only");
-    XS_TOKEN_EXACT_NV(uint16_t)
-#undef XS_TOKEN_EXACT_NV
-#undef XS_TOKEN_EXACT
+    if (nv <= 1) XS_ROUTE_BLOCK(1);
+    else if (nv <= 2) XS_ROUTE_BLOCK(2);
+    else if (nv <= 4) XS_ROUTE_BLOCK(4);
+    else if (nv <= 8) XS_ROUTE_BLOCK(8);
+    else XS_ROUTE_BLOCK(16);
+#undef XS_ROUTE_BLOCK
     XS_LAUNCH_CHECK();
     return XS_OK;
 }
