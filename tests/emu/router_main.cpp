@@ -146,8 +146,12 @@ int main(int argc, char **argv)
                            : route_kernel<1, 2>(part, bias, T, E, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsp, lout, ca); break;
             case 2: m == 1 ? route_kernel<2, 1>(part, bias, T, E, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsp, lout, ca)
                            : route_kernel<2, 2>(part, bias, T, E, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsp, lout, ca); break;
-            default: m == 1 ? route_kernel<4, 1>(part, bias, T, E, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsp, lout, ca)
-                            : route_kernel<4, 2>(part, bias, T, E, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsp, lout, ca);
+            case 3: case 4: m == 1 ? route_kernel<4, 1>(part, bias, T, E, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsp, lout, ca)
+                            : route_kernel<4, 2>(part, bias, T, E, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsp, lout, ca); break;
+            case 5: case 6: case 7: case 8: m == 1 ? route_kernel<8, 1>(part, bias, T, E, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsp, lout, ca)
+                            : route_kernel<8, 2>(part, bias, T, E, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsp, lout, ca); break;
+            default: m == 1 ? route_kernel<16, 1>(part, bias, T, E, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsp, lout, ca)
+                            : route_kernel<16, 2>(part, bias, T, E, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsp, lout, ca);
             }
         };
         emu_launch3(body, g, 1, 1, 256, 0, 8);
@@ -159,7 +163,9 @@ int main(int argc, char **argv)
             switch (nv) {
             case 1: route_block_kernel<uint16_t, 1>(xb, wb, part, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsplit, lout, ca); break;
             case 2: route_block_kernel<uint16_t, 2>(xb, wb, part, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsplit, lout, ca); break;
-            default: route_block_kernel<uint16_t, 4>(xb, wb, part, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsplit, lout, ca);
+            case 3: case 4: route_block_kernel<uint16_t, 4>(xb, wb, part, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsplit, lout, ca); break;
+            case 5: case 6: case 7: case 8: route_block_kernel<uint16_t, 8>(xb, wb, part, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsplit, lout, ca); break;
+            default: route_block_kernel<uint16_t, 16>(xb, wb, part, bias, T, E, H, k, n_group, topk_group, 1, 1.f, idx, w, mask, Wd, nsplit, lout, ca);
             }
         };
         emu_launch3(body, T, 1, 1, kChainThreads, sizeof(float) * 2 * 64 * kCR, 3);

@@ -77,6 +77,8 @@ CERT_CASES = [
     ("groups", (32, 256, 8, 2048, 9, 8, 1, 0.1, 0, 8, 8, 4)),
     ("all_exact", (16, 256, 6, 2048, 4, 16, 1e30)),
     ("all_exact_groups", (8, 256, 8, 1024, 9, 4, 1e30, 0.1, 0, 0, 8, 4)),
+    ("e1024_top16", (24, 1024, 16, 512, 31, 4)),
+    ("all_exact_e1024", (4, 1024, 16, 512, 32, 4, 1e30)),
     # the certified routing the other way than the forward picks for the
     # batch: separate routing, pair-parallel exact pass and second routing
     # launches at decode; one launch with a block per token at prefill
