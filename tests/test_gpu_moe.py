@@ -425,12 +425,13 @@ def test_moe_fp4_c5_full_size():
 
 
 def test_moe_prefill_full_size_properties():
-    """C3 at full size (8192 tokens, Zipf(1.1) popularity): routing, counts and
-    permutation bit-exact against the oracle on the GPU logits; outputs of a
-    sample of tokens against the oracle run on those tokens alone."""
+    """C3 at full size (8192 tokens, Zipf(1.1) popularity) on the default
+    (certified) router: routing, counts and permutation bit-exact against the
+    oracle on the logits routed on, and the top-k equal to the oracle's from x;
+    outputs of a sample of tokens against the oracle run on those tokens alone."""
     T, E, k = 8192, 256, 6
     c, g = make_case_gpu(T, 4096, 2048, E, k, seed=8, zipf=1.1)
-    layer = layer_for(c, g)
+    layer = layer_for(c, g, router_exact=None)
     dbg = _debug(T, E, k)
     out = layer.forward(g["x"], debug=dbg)
     torch.cuda.synchronize()
@@ -530,7 +531,7 @@ def test_moe_prefill_32k_tokens_properties():
     rows against the oracle, routed weights summing to 1."""
     T, E, k = 32768, 256, 6
     c, g = make_case_gpu(T, 4096, 2048, E, k, seed=9, zipf=1.1)
-    layer = layer_for(c, g)
+    layer = layer_for(c, g, router_exact=None)    # the default (certified) router
     dbg = _debug(T, E, k)
     out = layer.forward(g["x"], debug=dbg)
     torch.cuda.synchronize()
