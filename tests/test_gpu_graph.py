@@ -2,8 +2,10 @@
 equals the eager output bit for bit, with the program's own eager forwards and
 synchronisations between the replays.  The forward records no memset (its
 persistent-GEMM counters are cleared by the permute kernel), so a captured
-graph replays the same work each time.  Also: the activation quant folded
-into the decode router launch equals the separate quant pass."""
+graph replays the same work each time; the certified router's list
+counters are cleared by its logits launch the same way.  Also: the
+activation quant folded into the decode router launch equals the separate
+quant pass."""
 import numpy as np
 import pytest
 
@@ -19,20 +21,30 @@ def _gpu():
     import xs_moe_capi  # noqa: F401  (fails loudly when the library is missing)
 
 
-@pytest.mark.parametrize("T,stream,norm", [(16, "1", False), (16, "0", True), (200, "1", True), (64, "0", False)])
-def test_graph_replays_equal_eager(monkeypatch, T, stream, norm):
+@pytest.mark.parametrize("T,stream,norm,router,margin", [
+    (16, "1", False, "mfma", None), (16, "0", True, "mfma", None), (200, "1", True, "mfma", None),
+    (64, "0", False, "mfma", None),
+    # the default certified router: the one route launch at decode, the three
+    # launches at prefill, and with every token through the exact pass
+    (16, "1", False, "certified", None), (300, "0", False, "certified", None),
+    (16, "1", False, "certified", "1e30"), (300, "0", True, "certified", "1e30")])
+def test_graph_replays_equal_eager(monkeypatch, T, stream, norm, router, margin):
     from moe_cases import make_case, to_device, layer_for
     monkeypatch.setenv("XS_MOE_STREAM", stream)
+    if margin:
+        monkeypatch.setenv("XS_ROUTER_MARGIN", margin)
     H, I, E, k = 512, 256, 16, 4
     c = make_case(max(T, 40), H, I, E, k, seed=T)
     g = to_device(c)
     kw = {}
     if norm:
         kw = dict(norm_weight=torch.ones(H, dtype=torch.bfloat16, device="cuda"), norm_eps=1e-6)
+    if router == "certified":
+        kw["router_exact"] = None
     L = layer_for(c, g, **kw)
     x = g["x"][:T].contiguous()
     other = g["x"][T // 2:T // 2 + 7].contiguous()
-    print(f"graph T={T} XS_MOE_STREAM={stream} norm={norm}", flush=True)
+    print(f"graph T={T} XS_MOE_STREAM={stream} norm={norm} router={router} margin={margin}", flush=True)
     eager = L.forward(x).clone()
     out = torch.empty_like(eager)
     res = x.clone()
