@@ -102,7 +102,7 @@ def test_cpp_moe_matches_capi_and_oracle():
     from moe_cases import make_case, to_device, layer_for, oracle_forward, max_abs_rel
     c = make_case(40, 512, 256, 16, 4, seed=77)
     g = to_device(c)
-    ref_gpu = layer_for(c, g).forward(g["x"])
+    ref_gpu = layer_for(c, g, router_exact=None).forward(g["x"])   # both on the default (certified) router
     torch.cuda.synchronize()
     cu = lambda a, d=None: xstar_cpp.to_cuda(torch_to_cpp(torch.from_numpy(np.ascontiguousarray(a)), d))  # noqa: E731
     xt = xstar_cpp.to_cuda(torch_to_cpp(g["x"]))

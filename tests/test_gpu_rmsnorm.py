@@ -258,8 +258,9 @@ def test_moe_block_ffn_from_a_checkpoint(tmp_path):
     got = cpp_to_torch(xstar_cpp.to_cpu(out), (T, H))
     g = to_device(c)
     lnd = _dev(ln)
-    fused = layer_for(c, g, norm_weight=lnd, norm_eps=1e-6).forward(g["x"], residual=g["x"])
-    moe_out = layer_for(c, g).forward(X.rmsnorm(g["x"], lnd, 1e-6))
+    # the C ABI layers on the C++ op's default (certified) router
+    fused = layer_for(c, g, router_exact=None, norm_weight=lnd, norm_eps=1e-6).forward(g["x"], residual=g["x"])
+    moe_out = layer_for(c, g, router_exact=None).forward(X.rmsnorm(g["x"], lnd, 1e-6))
     unfused = g["x"].float() + moe_out.float()
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), fused.cpu().view(torch.int16))
