@@ -195,14 +195,25 @@ def main():
     res = {}
     if "prefill" in sections:
         res = prefill(a, X, torch)
+    # the other configurations: a failure in one is recorded in its place and
+    # does not take the headline line with it
+    def leg(name, fn):
+        try:
+            res[name] = fn()
+        except Exception as e:  # noqa: BLE001
+            log(f"{name} failed: {e!r}")
+            res[name] = {"error": repr(e)}
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+
     if "decode" in sections:
-        res["decode"] = decode(a, X, torch)
+        leg("decode", lambda: decode(a, X, torch))
     if "gemm" in sections:
-        res["gemm_fp8_512x4096x4096"] = single_gemm(a, X, torch)
+        leg("gemm_fp8_512x4096x4096", lambda: single_gemm(a, X, torch))
     if "fp4" in sections:
-        res["fp4_2048"] = fp4_layer(a, X, torch)
+        leg("fp4_2048", lambda: fp4_layer(a, X, torch))
     if "norm" in sections or "block" in sections:
-        res["rmsnorm_8192x4096"] = norm_legs(a, X, torch, kernels="norm" in sections, block="block" in sections)
+        leg("rmsnorm_8192x4096", lambda: norm_legs(a, X, torch, kernels="norm" in sections, block="block" in sections))
     print(json.dumps(res))
     return 0
 
@@ -285,7 +296,11 @@ def prefill(a, X, torch):
     }
     # the default (certified, bit-exact top-k) router against the approximate
     # MFMA router and the chain router (every logit in gemm_cpu order)
-    res["router"] = router_report(layer, g["x"], T, ms, stages, a, layer_from, g)
+    try:
+        res["router"] = router_report(layer, g["x"], T, ms, stages, a, layer_from, g)
+    except Exception as e:  # noqa: BLE001
+        log(f"router report failed: {e!r}")
+        res["router"] = {"error": repr(e)}
     del layer
     if not a.no_cpu:
         log("cpu baseline ...")
