@@ -1,7 +1,9 @@
-// CPU emulation shim for the DMA-ring GEMM kernels: one host thread per GPU
-// lane, block barriers, wave exchanges for readfirstlane / shuffles / MFMA,
-// DMA ops queued per lane and landed at s_waitcnt (LATE mode) or at issue
-// (EARLY mode), bounds-checked against registered buffers and the LDS size.
+// CPU emulation shim for the DMA-ring GEMM kernels: one cooperative fiber per
+// GPU lane (a block's lanes share one host thread and switch only at block
+// barriers and wave exchanges; blocks run on a pool of host threads), wave
+// exchanges for readfirstlane / shuffles / MFMA, DMA ops queued per lane and
+// landed at s_waitcnt (LATE mode) or at issue (EARLY mode), bounds-checked
+// against registered buffers and the LDS size.
 #pragma once
 #include <atomic>
 #include <barrier>
@@ -11,6 +13,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <deque>
+#include <functional>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -19,6 +22,7 @@
 #include <algorithm>
 #include <sys/mman.h>
 #include <unistd.h>
+#include <ucontext.h>
 
 #define __global__
 #define __device__
@@ -78,10 +82,34 @@ enum { MODE_LATE = 0, MODE_EARLY = 1 };
 inline int g_mode = MODE_LATE;
 
 struct Op { int kind; const uint8_t *src; uint32_t dst; int n; int32_t *atom; int32_t *result; };
+
+// A barrier among the fibers of one block (the interface of std::barrier):
+// a fiber that arrives before the others yields until the phase completes.
+inline void emu_progress();
+inline void emu_yield();
+struct EmuBarrier {
+    ptrdiff_t expected, arrived = 0, drops = 0;
+    uint64_t phase = 0;
+    explicit EmuBarrier(ptrdiff_t n) : expected(n) {}
+    void complete() { arrived = 0; expected -= drops; drops = 0; ++phase; }
+    void arrive_and_wait()
+    {
+        const uint64_t ph = phase;
+        emu_progress();
+        if (++arrived == expected) { complete(); return; }
+        while (phase == ph) emu_yield();
+    }
+    void arrive_and_drop()
+    {
+        emu_progress();
+        ++drops;
+        if (++arrived == expected) complete();
+    }
+};
 struct Blk {
     uint8_t *smem; size_t smem_size;
-    std::barrier<> *bar;
-    std::barrier<> *wbar[16];
+    EmuBarrier *bar;
+    EmuBarrier *wbar[16];
     uint64_t xch[16][64];
     uint8_t wx[16][64][64];
     uint64_t xseq[16][64];   // per lane: how many wave exchanges it has entered
@@ -402,49 +430,150 @@ inline v4f emu_mfma(v8i a, v8i b, v4f c, int cbsz, int blgp, int opa, int sa, in
 #define __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4 emu_mfma
 
 // ------------------------------------------------------------ launch
-template <typename F>
-inline void emu_launch(F fn, unsigned gx, unsigned gy, unsigned nt, size_t smem, unsigned conc)
+// Lanes run as fibers: a host thread takes one block at a time and resumes
+// its lanes in turn; a lane runs until it waits at a barrier (block barrier or
+// wave exchange) or returns.  The per-lane state above (thread_local, shared
+// by the fibers of one host thread) is saved and restored around each resume.
+// The card runs a block's waves in no fixed order either, and no kernel here
+// spins on a flag written by another lane of its block, so cooperative
+// scheduling changes no result; blocks never wait for one another.
+struct EmuLane {
+    ucontext_t ctx;
+    bool done = false;
+    EmuDim tid, bid;
+    Blk *b = nullptr;
+    std::deque<Op> q;
+    int32_t claims[64];
+    int nclaim = 0;
+    uint64_t xseq = 0, ndma = 0;
+    size_t shoff = 0;
+    uint32_t m0 = 0;
+    const uint8_t *sbase = nullptr;
+};
+struct EmuSched {
+    ucontext_t main;
+    std::vector<EmuLane> lanes;
+    std::vector<uint8_t *> stacks;
+    size_t cur = 0;
+    long idle = 0;               // resumes since the last barrier arrival or lane exit
+    const std::function<void()> *body = nullptr;
+};
+inline thread_local EmuSched *t_sched = nullptr;
+static constexpr size_t kEmuStack = 1u << 20;
+inline void emu_progress() { if (t_sched) t_sched->idle = 0; }
+inline void emu_yield()
 {
-    gridDim = {gx, gy, 1};
+    EmuSched *s = t_sched;
+    swapcontext(&s->lanes[s->cur].ctx, &s->main);
+}
+inline void emu_lane_load(EmuLane &c)
+{
+    threadIdx = c.tid; blockIdx = c.bid; tb = c.b;
+    std::swap(tq, c.q);
+    memcpy(t_claims, c.claims, sizeof c.claims);
+    t_nclaim = c.nclaim; t_xseq = c.xseq; t_ndma = c.ndma; t_shoff = c.shoff; t_m0 = c.m0; t_sbase = c.sbase;
+}
+inline void emu_lane_save(EmuLane &c)
+{
+    std::swap(tq, c.q);
+    memcpy(c.claims, t_claims, sizeof c.claims);
+    c.nclaim = t_nclaim; c.xseq = t_xseq; c.ndma = t_ndma; c.shoff = t_shoff; c.m0 = t_m0; c.sbase = t_sbase;
+}
+inline void emu_lane_entry()
+{
+    EmuSched *s = t_sched;
+    (*s->body)();
+    const unsigned t = threadIdx.x;
+    if (!tq.empty()) EMU_ERR("lane exits with %zu DMA ops outstanding", tq.size());
+    emu_wait(0);
+    tb->gone[t / 64][t % 64] = true;
+    tb->wbar[t / 64]->arrive_and_drop();
+    tb->bar->arrive_and_drop();
+    s->lanes[s->cur].done = true;   // returning resumes the scheduler (uc_link)
+}
+// Runs every block of the grid: lanes as fibers of one host thread per block,
+// blocks spread over a pool of host threads.  smem: the block's LDS bytes;
+// shoff: where static __shared__ arrays start within it.
+inline void emu_run_grid(std::function<void()> fn, EmuDim g, unsigned nt, size_t smem, size_t shoff)
+{
+    gridDim = g;
     blockDim = {nt, 1, 1};
-    std::vector<std::pair<unsigned, unsigned>> blocks;
-    for (unsigned y = 0; y < gy; ++y)
-        for (unsigned x = 0; x < gx; ++x) blocks.push_back({x, y});
-    for (size_t b0 = 0; b0 < blocks.size(); b0 += conc) {
-        const size_t nb = std::min<size_t>(conc, blocks.size() - b0);
-        std::vector<Blk *> bk(nb);
-        std::vector<std::thread> th;
-        for (size_t i = 0; i < nb; ++i) {
+    std::vector<EmuDim> blocks;
+    for (unsigned z = 0; z < g.z; ++z)
+        for (unsigned y = 0; y < g.y; ++y)
+            for (unsigned x = 0; x < g.x; ++x) blocks.push_back({x, y, z});
+    std::atomic<size_t> next{0};
+    auto worker = [&] {
+        EmuSched S;
+        S.body = &fn;
+        S.lanes.resize(nt);
+        for (unsigned t = 0; t < nt; ++t) {
+            uint8_t *st = (uint8_t *)mmap(nullptr, kEmuStack, PROT_READ | PROT_WRITE,
+                                          MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE, -1, 0);
+            mprotect(st, 4096, PROT_NONE);   // guard page below the stack
+            S.stacks.push_back(st);
+        }
+        t_sched = &S;
+        for (size_t bi; (bi = next.fetch_add(1)) < blocks.size();) {
             Blk *B = new Blk();
             B->smem_size = smem;
             B->smem = (uint8_t *)aligned_alloc(256, (smem + 255) / 256 * 256 + 256);
             memset(B->smem, 0x5A, smem);
-            B->bar = new std::barrier<>(nt);
-            for (unsigned w = 0; w < nt / 64; ++w) B->wbar[w] = new std::barrier<>(64);
-            bk[i] = B;
-            for (unsigned t = 0; t < nt; ++t)
-                th.emplace_back([=] {
-                    threadIdx = {t, 0, 0};
-                    blockIdx = {blocks[b0 + i].first, blocks[b0 + i].second, 0};
-                    tb = B;
-                    tq.clear();
-                    t_m0 = 0; t_sbase = nullptr; t_ndma = 0; t_shoff = 0; t_xseq = 0;
-                    fn();
-                    if (!tq.empty()) EMU_ERR("lane exits with %zu DMA ops outstanding", tq.size());
-                    emu_wait(0);
-                    B->gone[t / 64][t % 64] = true;
-                    B->wbar[t / 64]->arrive_and_drop();
-                    B->bar->arrive_and_drop();
-                });
-        }
-        for (auto &t : th) t.join();
-        for (auto *B : bk) {
+            B->bar = new EmuBarrier(nt);
+            for (unsigned w = 0; w < nt / 64; ++w) B->wbar[w] = new EmuBarrier(64);
+            for (unsigned t = 0; t < nt; ++t) {
+                EmuLane &c = S.lanes[t];
+                c.done = false;
+                c.tid = {t, 0, 0};
+                c.bid = blocks[bi];
+                c.b = B;
+                c.q.clear();
+                c.nclaim = 0; c.xseq = 0; c.ndma = 0; c.shoff = shoff; c.m0 = 0; c.sbase = nullptr;
+                getcontext(&c.ctx);
+                c.ctx.uc_stack.ss_sp = S.stacks[t];
+                c.ctx.uc_stack.ss_size = kEmuStack;
+                c.ctx.uc_link = &S.main;
+                makecontext(&c.ctx, emu_lane_entry, 0);
+            }
+            S.idle = 0;
+            for (size_t live = nt; live > 0;) {
+                live = 0;
+                for (unsigned t = 0; t < nt; ++t) {
+                    EmuLane &c = S.lanes[t];
+                    if (c.done) continue;
+                    S.cur = t;
+                    emu_lane_load(c);
+                    swapcontext(&S.main, &c.ctx);
+                    emu_lane_save(c);
+                    if (!c.done) ++live;
+                    else S.idle = 0;
+                    if (++S.idle > 4l * nt + 8) {
+                        threadIdx = c.tid; blockIdx = c.bid;
+                        EMU_ERR("every live lane waits at a barrier the others never reach (divergent barrier)");
+                        fflush(stderr);
+                        abort();
+                    }
+                }
+            }
             free(B->smem);
             delete B->bar;
             for (unsigned w = 0; w < nt / 64; ++w) delete B->wbar[w];
             delete B;
         }
-    }
+        t_sched = nullptr;
+        for (auto *st : S.stacks) munmap(st, kEmuStack);
+    };
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const size_t nw = std::min<size_t>({blocks.size(), (size_t)std::min(hw, 8u), 8});
+    std::vector<std::thread> th;
+    for (size_t i = 1; i < nw; ++i) th.emplace_back(worker);
+    worker();
+    for (auto &t : th) t.join();
+}
+template <typename F>
+inline void emu_launch(F fn, unsigned gx, unsigned gy, unsigned nt, size_t smem, unsigned /*conc*/)
+{
+    emu_run_grid(fn, {gx, gy, 1}, nt, smem, 0);
 }
 inline uint32_t emu_first_lane(uint32_t v)
 {

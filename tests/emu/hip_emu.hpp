@@ -1,7 +1,7 @@
 // Host stand-in of the HIP runtime and of the gfx950 builtins the library's
 // sources use, for the whole-forward emulation (fwd_main.cpp): the product's
 // own C ABI entry points, dispatch and launchers run on the CPU, and every
-// kernel launch runs the kernel's source through emu.hpp (one thread per
+// kernel launch runs the kernel's source through emu.hpp (one fiber per
 // lane).  Launches are synchronous; streams and events are no-ops.
 #pragma once
 #include "router_emu.hpp"
@@ -116,61 +116,15 @@ inline auto min(A a, B b) { using C = std::common_type_t<A, B>; return (C)a < (C
 template <typename A, typename B, typename = std::enable_if_t<!std::is_same_v<A, B>>>
 inline auto max(A a, B b) { using C = std::common_type_t<A, B>; return (C)a > (C)b ? (C)a : (C)b; }
 
-// static __shared__ arrays are carved after the launch's dynamic LDS
-inline thread_local size_t t_dyn_lds = 0;
-
-// a kernel launch: every block's lanes as threads, blocks in groups that fit
-// about 1024 threads, synchronous
+// a kernel launch: every block's lanes as fibers (emu_run_grid), synchronous;
+// static __shared__ arrays follow the dynamic LDS
 template <typename F>
 inline void emu_kl(F fn, dim3 g, dim3 b, size_t smem = 0, hipStream_t = nullptr)
 {
     const unsigned nt = b.x * b.y * b.z;
     if (nt % 64 || nt > 1024) { fprintf(stderr, "[emu] block of %u threads\n", nt); g_errors++; return; }
     const size_t dyn = (smem + 15) / 16 * 16;
-    gridDim = {g.x, g.y, g.z};
-    blockDim = {nt, 1, 1};
-    std::vector<EmuDim> blocks;
-    for (unsigned z = 0; z < g.z; ++z)
-        for (unsigned y = 0; y < g.y; ++y)
-            for (unsigned x = 0; x < g.x; ++x) blocks.push_back({x, y, z});
-    const size_t conc = std::max<size_t>(1, 1024 / nt);
-    for (size_t b0 = 0; b0 < blocks.size(); b0 += conc) {
-        const size_t nb = std::min<size_t>(conc, blocks.size() - b0);
-        std::vector<Blk *> bk(nb);
-        std::vector<std::thread> th;
-        for (size_t i = 0; i < nb; ++i) {
-            Blk *B = new Blk();
-            B->smem_size = dyn + 65536;
-            B->smem = (uint8_t *)aligned_alloc(256, (B->smem_size + 255) / 256 * 256 + 256);
-            memset(B->smem, 0x5A, B->smem_size);
-            B->bar = new std::barrier<>(nt);
-            for (unsigned w = 0; w < nt / 64; ++w) B->wbar[w] = new std::barrier<>(64);
-            bk[i] = B;
-            const EmuDim bid = blocks[b0 + i];
-            for (unsigned t = 0; t < nt; ++t)
-                th.emplace_back([=] {
-                    threadIdx = {t, 0, 0};
-                    blockIdx = bid;
-                    tb = B;
-                    tq.clear();
-                    t_m0 = 0; t_sbase = nullptr; t_ndma = 0; t_xseq = 0;
-                    t_shoff = dyn;
-                    fn();
-                    if (!tq.empty()) EMU_ERR("lane exits with %zu DMA ops outstanding", tq.size());
-                    emu_wait(0);
-                    B->gone[t / 64][t % 64] = true;
-                    B->wbar[t / 64]->arrive_and_drop();
-                    B->bar->arrive_and_drop();
-                });
-        }
-        for (auto &t : th) t.join();
-        for (auto *B : bk) {
-            free(B->smem);
-            delete B->bar;
-            for (unsigned w = 0; w < nt / 64; ++w) delete B->wbar[w];
-            delete B;
-        }
-    }
+    emu_run_grid(fn, {g.x, g.y, g.z}, nt, dyn + 65536, dyn);
 }
 
 // compiler-visible register loads of the weight-direct kernels: read now (the

@@ -117,48 +117,7 @@ inline void dma16x(const void *g, uint32_t lds)
 }
 
 template <typename F>
-inline void emu_launch3(F fn, unsigned gx, unsigned gy, unsigned gz, unsigned nt, size_t smem, unsigned conc)
+inline void emu_launch3(F fn, unsigned gx, unsigned gy, unsigned gz, unsigned nt, size_t smem, unsigned /*conc*/)
 {
-    gridDim = {gx, gy, gz};
-    blockDim = {nt, 1, 1};
-    std::vector<EmuDim> blocks;
-    for (unsigned z = 0; z < gz; ++z)
-        for (unsigned y = 0; y < gy; ++y)
-            for (unsigned x = 0; x < gx; ++x) blocks.push_back({x, y, z});
-    for (size_t b0 = 0; b0 < blocks.size(); b0 += conc) {
-        const size_t nb = std::min<size_t>(conc, blocks.size() - b0);
-        std::vector<Blk *> bk(nb);
-        std::vector<std::thread> th;
-        for (size_t i = 0; i < nb; ++i) {
-            Blk *B = new Blk();
-            B->smem_size = smem ? smem : 16;
-            B->smem = (uint8_t *)aligned_alloc(256, (B->smem_size + 255) / 256 * 256 + 256);
-            memset(B->smem, 0x5A, B->smem_size);
-            B->bar = new std::barrier<>(nt);
-            for (unsigned w = 0; w < nt / 64; ++w) B->wbar[w] = new std::barrier<>(64);
-            bk[i] = B;
-            const EmuDim bid = blocks[b0 + i];
-            for (unsigned t = 0; t < nt; ++t)
-                th.emplace_back([=] {
-                    threadIdx = {t, 0, 0};
-                    blockIdx = bid;
-                    tb = B;
-                    tq.clear();
-                    t_m0 = 0; t_sbase = nullptr; t_ndma = 0; t_shoff = 0; t_xseq = 0;
-                    fn();
-                    if (!tq.empty()) EMU_ERR("lane exits with %zu DMA ops outstanding", tq.size());
-                    emu_wait(0);
-                    B->gone[t / 64][t % 64] = true;
-                    B->wbar[t / 64]->arrive_and_drop();
-                    B->bar->arrive_and_drop();
-                });
-        }
-        for (auto &t : th) t.join();
-        for (auto *B : bk) {
-            free(B->smem);
-            delete B->bar;
-            for (unsigned w = 0; w < nt / 64; ++w) delete B->wbar[w];
-            delete B;
-        }
-    }
+    emu_run_grid(fn, {gx, gy, gz}, nt, smem ? smem : 16, 0);
 }

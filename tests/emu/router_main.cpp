@@ -1,5 +1,5 @@
 // Host emulation of the router kernels of moe_router.hip (the kernels' own
-// source, one thread per lane): the certified router (MFMA logits with their
+// source, one fiber per lane): the certified router (MFMA logits with their
 // error-bound terms, route MODE 1, the chain kernel over the listed pairs,
 // route MODE 2) and the chain router over every logit, against the CPU
 // oracle's gemm_cpu-order logits and routing.

@@ -1,7 +1,7 @@
 """Host emulation of the whole default forward: the library's own C ABI
 (xs_moe_forward, xs_moe_forward_noalloc, xs_moe_plan), dispatch, workspace
 layout and launchers compiled for the host, with every kernel launch running
-the kernel's source on the CPU (tests/emu/gen_fwd.py, hip_emu.hpp; one thread
+the kernel's source on the CPU (tests/emu/gen_fwd.py, hip_emu.hpp; one fiber
 per lane, DMAs landing at their waits, addresses checked against their
 buffers, every wave exchange checked to be reached by all live lanes).
 

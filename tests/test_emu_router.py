@@ -1,6 +1,6 @@
 """Host emulation of the router kernels (moe_router.hip): the certified
 router and the chain router run from the kernels' own source on the CPU (one
-thread per lane, tests/emu/router_emu.hpp) and are checked against the CPU
+fiber per lane, tests/emu/router_emu.hpp) and are checked against the CPU
 oracle (gemm_cpu-order logits, its routing).
 
 Certified router: top-k indices equal the oracle's on its gemm_cpu logits,
