@@ -403,25 +403,33 @@ inline v4f emu_mfma(v8i a, v8i b, v4f c, int cbsz, int blgp, int opa, int sa, in
     emu_xcheck(w, l);
     const int r = l & 15, g = l >> 4;
     v4f out = c;
+    // element decodes and scales from tables; each lane decodes its own A
+    // rows and B row once.  The products keep the order ((a * sa) * b) * sb.
+    static const std::vector<float> e4m3 = [] { std::vector<float> t(256); for (int i = 0; i < 256; ++i) t[i] = e4m3_dec((uint8_t)i); return t; }();
+    static const std::vector<float> pow2 = [] { std::vector<float> t(256); for (int i = 0; i < 256; ++i) t[i] = std::ldexp(1.f, i - 127); return t; }();
     auto elem = [&](int lane_row, int k, int off, bool fp4) -> float {   // element k of row lane_row
         if (fp4) {
             const uint8_t by = tb->wx[w][16 * (k / 32) + lane_row][off + (k % 32) / 2];
             return e2m1_dec((k & 1) ? by >> 4 : by & 15);
         }
         const int chunk = k / 16, gg = chunk & 3, hi = chunk >> 2;
-        return e4m3_dec(tb->wx[w][16 * gg + lane_row][off + 16 * hi + (k & 15)]);
+        return e4m3[tb->wx[w][16 * gg + lane_row][off + 16 * hi + (k & 15)]];
     };
     const bool scaled = cbsz == 4 || blgp == 4;
     auto scl = [&](int lane_row, int blk, bool isa) -> float {
         if (!scaled) return 1.f;
         const uint64_t x = tb->xch[w][16 * blk + lane_row];
-        return std::ldexp(1.f, (int)(isa ? (x >> 8) & 0xff : x & 0xff) - 127);
+        return pow2[isa ? (x >> 8) & 0xff : x & 0xff];
     };
+    float bv[128], bscl[4];
+    for (int k = 0; k < 128; ++k) bv[k] = elem(r, k, 32, blgp == 4);
+    for (int q = 0; q < 4; ++q) bscl[q] = scl(r, q, false);
     for (int v = 0; v < 4; ++v) {
+        float ascl[4], av[128];
+        for (int q = 0; q < 4; ++q) ascl[q] = scl(4 * g + v, q, true);
+        for (int k = 0; k < 128; ++k) av[k] = elem(4 * g + v, k, 0, cbsz == 4) * ascl[k / 32];
         float s = 0;
-        for (int k = 0; k < 128; ++k)
-            s += elem(4 * g + v, k, 0, cbsz == 4) * scl(4 * g + v, k / 32, true) * elem(r, k, 32, blgp == 4) *
-                 scl(r, k / 32, false);
+        for (int k = 0; k < 128; ++k) s += av[k] * bv[k] * bscl[k / 32];
         out[v] += s;
     }
     tb->wbar[w]->arrive_and_wait();

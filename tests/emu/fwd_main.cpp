@@ -88,9 +88,13 @@ int main(int argc, char **argv)
         xo_quant_weight_fp8_block(w2f.data(), H, I, sw2, ss2);
     }
 
+    // EMU_ROUTE="n_group,topk_group,renormalize,routed_scaling" (default 1,1,1,1)
+    int ng = 1, tg = 1, renorm = 1;
+    float scaling = 1.0f;
+    if (const char *r = getenv("EMU_ROUTE")) sscanf(r, "%d,%d,%d,%f", &ng, &tg, &renorm, &scaling);
     xs_moe_params p = {};
-    p.T = T; p.H = H; p.I = I; p.E = E; p.top_k = k; p.n_group = 1; p.topk_group = 1;
-    p.renormalize = 1; p.routed_scaling = 1.0f; p.x_dtype = xf32 ? XS_F32 : XS_BF16;
+    p.T = T; p.H = H; p.I = I; p.E = E; p.top_k = k; p.n_group = ng; p.topk_group = tg;
+    p.renormalize = renorm; p.routed_scaling = scaling; p.x_dtype = xf32 ? XS_F32 : XS_BF16;
     p.routed_format = fp4 ? XS_FP4_E2M1X2 : XS_FP8_E4M3; p.has_shared = shared; p.router_exact = router;
     p.has_norm = norm; p.norm_eps = 1e-6f;
     void *out = emu_alloc((size_t)T * H * el, "out");
@@ -178,7 +182,7 @@ int main(int argc, char **argv)
     std::vector<uint8_t> xin((size_t)T * H * el);
     if (norm) xo_rmsnorm(x, nw, xf32 ? 0 : 1, T, H, 1e-6f, xin.data());
     else memcpy(xin.data(), x, xin.size());
-    xo_moe_cfg cfg = {T, H, I, E, k, 1, 1, 1, 1.0f, xf32 ? 0 : 1, fp4, shared, 1};
+    xo_moe_cfg cfg = {T, H, I, E, k, ng, tg, renorm, scaling, xf32 ? 0 : 1, fp4, shared, 1};
     xo_moe_inputs in = {xin.data(), wr, bias, lg, w13, s13, w2, s2, sw13, ss13, sw2, ss2};
     std::vector<int32_t> ridx((size_t)T * k), rc_((size_t)E), ro((size_t)E + 1), rp((size_t)T * k), ri((size_t)T * k);
     std::vector<float> rw((size_t)T * k), rout((size_t)T * H);
@@ -199,7 +203,7 @@ int main(int argc, char **argv)
     xo_router_logits(xin.data(), wr, xf32 ? 0 : 1, T, E, H, xl.data());
     std::vector<int32_t> xidx((size_t)T * k);
     std::vector<float> xw((size_t)T * k);
-    xo_route(xl.data(), bias, T, E, k, 1, 1, 1, 1.0f, xidx.data(), xw.data());
+    xo_route(xl.data(), bias, T, E, k, ng, tg, renorm, scaling, xidx.data(), xw.data());
     long b_xidx = 0, b_lg = 0;
     for (size_t i = 0; i < (size_t)T * k; ++i) b_xidx += idx[i] != xidx[i];
     for (size_t i = 0; i < (size_t)T * E; ++i) b_lg += memcmp(&lg[i], &xl[i], 4) != 0;
@@ -214,6 +218,9 @@ int main(int argc, char **argv)
     printf("idx mismatches %ld\nw mismatches %ld\ncounts mismatches %ld\noffsets mismatches %ld\n"
            "perm mismatches %ld\ninv mismatches %ld\nref idx mismatches %ld\nlogit mismatches %ld\n",
            b_idx, b_w, b_c, b_o, b_p, b_i, b_xidx, b_lg);
+    uint64_t hsh = 1469598103934665603ull;   // FNV-1a of the output bytes
+    for (size_t i = 0; i < (size_t)T * H * el; ++i) hsh = (hsh ^ ((const uint8_t *)out)[i]) * 1099511628211ull;
+    printf("out hash %016llx\n", (unsigned long long)hsh);
     printf("max-abs-rel %.4g\nerrors %ld\n", dmax / (amax > 0 ? amax : 1), (long)g_errors);
     return 0;
 }

@@ -14,7 +14,8 @@ the layer's 2e-2 bound of the oracle's dequantize-then-f32 layer.  The cases
 cover each GEMM family of the default dispatch: one-block-per-tile, the
 persistent stream-K kernels, the tall tiles with the separate and the fused
 combine, MXFP4 routed experts, the pre-norm with a residual, the
-no-allocation entry point, f32 inputs, E = 1024 with top-16, and the
+no-allocation entry point, f32 inputs, E = 1024 with top-16, group-limited
+routing with scaling and no renormalisation, and the
 weight-direct GEMMs behind XS_WEIGHT_DIRECT=1 (packed by the library's own
 packing kernels, with XS_EMU_FULL=1)."""
 import os
@@ -74,6 +75,9 @@ CASES = [
     ("mfma_router", {}, (64, 256, 256, 8, 2, 7, 0, 1, 0, 0, 0, 0, 0, 0), 1),
     ("e1024_top16", {}, (48, 256, 128, 1024, 16, 10, 0, 1, 1, 0, 0, 0, 0, 0), 1),
     ("f32_norm_residual", {}, (64, 256, 128, 8, 2, 12, 0, 1, 1, 1, 0, 1, 1, 0), 0),
+    # group-limited routing (8 groups, keep 3), no renormalisation, scaling 2.5
+    ("groups_scaling", {"EMU_ROUTE": "8,3,0,2.5"}, (64, 256, 256, 64, 6, 13, 0, 1, 1, 0, 0, 0, 0, 0), 1),
+    ("groups_mfma_router", {"EMU_ROUTE": "8,3,1,2.5"}, (40, 512, 256, 32, 4, 14, 0, 1, 0, 0, 0, 0, 0, 0), 1),
     # every token through the certified router's exact pass
     ("exact_pass_everywhere", {"XS_ROUTER_MARGIN": "1e30"}, (24, 512, 256, 16, 4, 26, 0, 1, 1, 0, 0, 0, 0, 0), 1),
     ("exact_pass_noalloc", {"XS_ROUTER_MARGIN": "1e30"}, (24, 512, 256, 16, 4, 27, 0, 1, 1, 0, 0, 0, 0, 1), 1),
