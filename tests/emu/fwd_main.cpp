@@ -178,10 +178,32 @@ int main(int argc, char **argv)
         for (size_t i = 0; i < first.size(); ++i) bad += first[i] != ((uint8_t *)out)[i];
         printf("toggle mismatches %ld\n", bad);
     }
-    // the oracle on the (normalized) x the router read
+    // the oracle on the (normalized) x the router read.  With the pre-norm
+    // that is xs_rmsnorm's output (the forward runs the same kernel): its sum
+    // order differs from the oracle's sequential one, so a row can differ by
+    // an ulp of inv, which can move an FP8 group scale; the row is checked
+    // against the oracle's norm separately ("norm max code diff N": bf16 codes
+    // or f32 bit patterns)
     std::vector<uint8_t> xin((size_t)T * H * el);
-    if (norm) xo_rmsnorm(x, nw, xf32 ? 0 : 1, T, H, 1e-6f, xin.data());
-    else memcpy(xin.data(), x, xin.size());
+    if (norm) {
+        void *xn = emu_alloc((size_t)T * H * el, "x normalized");
+        if (xs_rmsnorm(x, nw, xf32 ? XS_F32 : XS_BF16, T, H, 1e-6f, xn, nullptr, nullptr, nullptr)) {
+            printf("xs_rmsnorm failed: %s\n", xs_last_error());
+            return 1;
+        }
+        memcpy(xin.data(), xn, xin.size());
+        std::vector<uint8_t> rn(xin.size());
+        xo_rmsnorm(x, nw, xf32 ? 0 : 1, T, H, 1e-6f, rn.data());
+        long dmax_code = 0;
+        for (size_t i = 0; i < (size_t)T * H; ++i) {
+            const long a = xf32 ? (long)((const int32_t *)xn)[i] : (long)((const int16_t *)xn)[i];
+            const long b = xf32 ? (long)((const int32_t *)rn.data())[i] : (long)((const int16_t *)rn.data())[i];
+            dmax_code = std::max(dmax_code, std::labs(a - b));
+        }
+        printf("norm max code diff %ld\n", dmax_code);
+    } else {
+        memcpy(xin.data(), x, xin.size());
+    }
     xo_moe_cfg cfg = {T, H, I, E, k, ng, tg, renorm, scaling, xf32 ? 0 : 1, fp4, shared, 1};
     xo_moe_inputs in = {xin.data(), wr, bias, lg, w13, s13, w2, s2, sw13, ss13, sw2, ss2};
     std::vector<int32_t> ridx((size_t)T * k), rc_((size_t)E), ro((size_t)E + 1), rp((size_t)T * k), ri((size_t)T * k);
