@@ -42,7 +42,6 @@ constexpr int kNSA = 5;                      // activation ring stages (>= kPD +
 constexpr int kAB = kBM * 128;               // activation rows of one step
 constexpr int kSB = kBM * 4;                 // their row scales
 constexpr int kStage = kAB + kSB;
-constexpr int kNA = kBM / 8 / kNW;           // 1 KB activation DMAs per wave and step
 constexpr int kNSW = kSB / 256;              // waves that load the row scales
 static_assert(kNSA >= kPD + 1 && kNSA * kStage + 8 * 1024 <= 160 * 1024 && kNSW <= kNW && kWT == 2 && kMI % 2 == 0,
               "ring");

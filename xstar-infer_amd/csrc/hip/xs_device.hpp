@@ -54,15 +54,6 @@ __device__ __forceinline__ uint16_t bf16_from_f32(float f)
 __device__ __forceinline__ float f32_from_bf16(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
 // ---------------------------------------------------------------- e4m3 codec
-// OCP E4M3FN decode.
-__device__ __forceinline__ float e4m3_decode(uint32_t b)
-{
-    uint32_t e = (b >> 3) & 15u, m = b & 7u;
-    float v = e == 0 ? __builtin_ldexpf((float)m, -9) : __builtin_ldexpf((float)(8u + m), (int)e - 10);
-    if (e == 15 && m == 7) v = __builtin_nanf("");
-    return (b & 0x80u) ? -v : v;
-}
-
 // f32 -> E4M3FN, round to nearest even, saturating to +-448 (integer
 // arithmetic on the f32 bit pattern; the same steps as the CPU restatement).
 __device__ __forceinline__ uint32_t e4m3_encode_sw(float f)
@@ -158,12 +149,6 @@ __device__ __forceinline__ float wave_max(float v)
 {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v)
-{
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
     return v;
 }
 
