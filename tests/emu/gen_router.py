@@ -8,7 +8,6 @@ kernel's asm DMA and wait helpers give way to emu.hpp's stand-ins, the dynamic
 LDS arrays become the block's emulated LDS, and the device helpers the kernels
 call (the reproducible exp and sigmoid, the wave max, load8 and the FP8 1x128
 quantizer) are taken from their headers.  Every replacement is asserted."""
-import re
 import sys
 
 from gen_wd import drop_fn, replace

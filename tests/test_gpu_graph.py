@@ -6,7 +6,6 @@ graph replays the same work each time; the certified router's list
 counters are cleared by its logits launch the same way.  Also: the
 activation quant folded into the decode router launch equals the separate
 quant pass."""
-import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu

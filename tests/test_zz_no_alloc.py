@@ -3,7 +3,6 @@ for callers that cannot allocate) against xs_moe_forward with a workspace:
 identical outputs bit for bit, on two calls in a row with the second call on a
 smaller input (the scratch keeps the first call's contents), for FP8 decode,
 FP8 prefill-shaped tiles and MXFP4; oversized params are rejected."""
-import numpy as np
 import pytest
 
 from moe_cases import make_case, make_case_gpu, to_device, layer_for
