@@ -44,6 +44,17 @@ int main(int argc, char **argv)
     void *wr = emu_alloc((size_t)E * H * el, "router_w");
     float *bias = (float *)emu_alloc(4 * (size_t)E, "bias");
     fill_act(x, (size_t)T * H, 1.0f);
+    // EMU_POISON=nan|inf: rows 0, T/2 and T-1 of x get that value (row 0 in
+    // every element, the others every 97th); only those tokens' outputs may
+    // be non-finite, and the routing must stay in range and the oracle's
+    if (const char *pz = getenv("EMU_POISON")) {
+        const float bad = !strcmp(pz, "nan") ? NAN : INFINITY;
+        for (int t2 : {0, T / 2, T - 1})
+            for (int c = 0; c < H; c += (t2 == 0 ? 1 : 97)) {
+                if (xf32) ((float *)x)[(size_t)t2 * H + c] = bad;
+                else ((uint16_t *)x)[(size_t)t2 * H + c] = xo_bf16_from_f32(bad);
+            }
+    }
     fill_act(wr, (size_t)E * H, 0.02f);
     for (int e = 0; e < E; ++e) bias[e] = 0.1f * nd(rng) + (zipf > 0 ? (float)(-zipf * std::log(1.0 + (e * 7919) % E)) : 0.f);
     void *nw = nullptr, *res = nullptr;
@@ -229,13 +240,45 @@ int main(int argc, char **argv)
     long b_xidx = 0, b_lg = 0;
     for (size_t i = 0; i < (size_t)T * k; ++i) b_xidx += idx[i] != xidx[i];
     for (size_t i = 0; i < (size_t)T * E; ++i) b_lg += memcmp(&lg[i], &xl[i], 4) != 0;
+    // output rows whose reference is non-finite (poisoned tokens) are left
+    // out of the error and counted: the forward's must be non-finite there
+    // and finite everywhere else
     double amax = 0, dmax = 0;
-    for (size_t i = 0; i < (size_t)T * H; ++i) {
-        double r = rout[i], g;
-        if (resid) r += xf32 ? ((float *)res)[i] : xo_f32_from_bf16(((uint16_t *)res)[i]);
-        g = xf32 ? ((float *)out)[i] : xo_f32_from_bf16(((uint16_t *)out)[i]);
-        amax = std::max(amax, std::fabs(r));
-        dmax = std::max(dmax, std::fabs(g - r));
+    long nf_ref = 0, nf_diff = 0;
+    for (int t2 = 0; t2 < T; ++t2) {
+        bool rf = true, gf = true;
+        for (int c = 0; c < H; ++c) {
+            const size_t i = (size_t)t2 * H + c;
+            rf &= std::isfinite(rout[i]);
+            gf &= std::isfinite(xf32 ? ((float *)out)[i] : xo_f32_from_bf16(((uint16_t *)out)[i]));
+        }
+        nf_ref += !rf;
+        nf_diff += rf != gf;
+        if (!rf) continue;
+        for (int c = 0; c < H; ++c) {
+            const size_t i = (size_t)t2 * H + c;
+            double r = rout[i], g;
+            if (resid) r += xf32 ? ((float *)res)[i] : xo_f32_from_bf16(((uint16_t *)res)[i]);
+            g = xf32 ? ((float *)out)[i] : xo_f32_from_bf16(((uint16_t *)out)[i]);
+            amax = std::max(amax, std::fabs(r));
+            dmax = std::max(dmax, std::fabs(g - r));
+        }
+    }
+    long bad_idx = 0;
+    for (size_t i = 0; i < (size_t)T * k; ++i) {
+        bad_idx += idx[i] < 0 || idx[i] >= E;
+        for (size_t j = i - i % k; j < i; ++j) bad_idx += idx[j] == idx[i];
+    }
+    printf("non-finite rows %ld (finiteness mismatches %ld)\nidx out of range or repeated %ld\n", nf_ref, nf_diff,
+           bad_idx);
+    if (!bad_idx) {   // the permutation of the forward's own top-k
+        std::vector<int32_t> oc((size_t)E), oo((size_t)E + 1), op((size_t)T * k), oi((size_t)T * k);
+        xo_permute(idx, T, E, k, oc.data(), oo.data(), op.data(), oi.data());
+        long b = 0;
+        for (int e = 0; e < E; ++e) b += oc[e] != counts[e];
+        for (int e = 0; e <= E; ++e) b += oo[e] != offsets[e];
+        for (size_t i = 0; i < (size_t)T * k; ++i) b += (op[i] != perm[i]) + (oi[i] != inv[i]);
+        printf("own permutation mismatches %ld\n", b);
     }
     printf("idx mismatches %ld\nw mismatches %ld\ncounts mismatches %ld\noffsets mismatches %ld\n"
            "perm mismatches %ld\ninv mismatches %ld\nref idx mismatches %ld\nlogit mismatches %ld\n",

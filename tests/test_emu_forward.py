@@ -19,7 +19,7 @@ cover each GEMM family of the default dispatch: one-block-per-tile, the
 persistent stream-K kernels, the tall tiles with the separate and the fused
 combine, MXFP4 routed experts, the pre-norm with a residual, the
 no-allocation entry point, f32 inputs, E = 1024 with top-16, group-limited
-routing with scaling and no renormalisation, and the
+routing with scaling and no renormalisation, NaN / Inf tokens, and the
 weight-direct GEMMs behind XS_WEIGHT_DIRECT=1 (packed by the library's own
 packing kernels, with XS_EMU_FULL=1)."""
 import os
@@ -82,6 +82,12 @@ CASES = [
     # group-limited routing (8 groups, keep 3), no renormalisation, scaling 2.5
     ("groups_scaling", {"EMU_ROUTE": "8,3,0,2.5"}, (64, 256, 256, 64, 6, 13, 0, 1, 1, 0, 0, 0, 0, 0), 1),
     ("groups_mfma_router", {"EMU_ROUTE": "8,3,1,2.5"}, (40, 512, 256, 32, 4, 14, 0, 1, 0, 0, 0, 0, 0, 0), 1),
+    # NaN / Inf in three tokens' rows of x: routing in range and the oracle's,
+    # only those tokens' outputs non-finite (no spread through shared tiles,
+    # split-K or stream-K partials)
+    ("poison_nan_tall", {"EMU_POISON": "nan"}, (300, 512, 256, 16, 4, 15, 0, 1, 1, 0, 0, 0, 0, 0), 2),
+    ("poison_inf_decode_chain", {"EMU_POISON": "inf"}, (16, 512, 256, 16, 4, 16, 0, 1, 2, 0, 0, 0, 0, 0), 1),
+    ("poison_nan_mxfp4", {"EMU_POISON": "nan"}, (48, 512, 512, 16, 6, 17, 1, 1, 1, 0, 0, 0, 0, 0), 1),
     # every token through the certified router's exact pass
     ("exact_pass_everywhere", {"XS_ROUTER_MARGIN": "1e30"}, (24, 512, 256, 16, 4, 26, 0, 1, 1, 0, 0, 0, 0, 0), 1),
     ("exact_pass_noalloc", {"XS_ROUTER_MARGIN": "1e30"}, (24, 512, 256, 16, 4, 27, 0, 1, 1, 0, 0, 0, 0, 1), 1),
@@ -110,16 +116,24 @@ def test_forward_emulated(fwd_emu, name, env, args, routed):
         assert re.search(r"fused 1", out), out
     c = {m.group(1): int(m.group(2)) for m in re.finditer(r"^([\w ]+?) mismatches (\d+)", out, re.M)}
     router = args[8]
-    for n in ("idx", "w", "counts", "offsets", "perm", "inv"):
+    poison = "EMU_POISON" in env
+    assert c["own permutation"] == 0, out
+    # a NaN key has no rank the reference defines (it has no MoE router, and the
+    # oracle's scan keeps a NaN it starts from): poisoned tokens must only
+    # route in range, to distinct experts, with a consistent permutation
+    for n in () if poison else ("idx", "w", "counts", "offsets", "perm", "inv"):
         assert c[n] == 0, (n, out)
     if len(args) > 15:
         assert re.search(r"toggle plan .* fused 2", out), out
         assert c["toggle"] == 0, out
-    if router in (1, 2):
+    if router in (1, 2) and not poison:
         assert c["ref idx"] == 0, out
     if router == 2:
-        assert c["logit"] == 0, out
+        assert c["logit"] == 0, out     # NaN logits compare by their bits
     assert float(re.search(r"max-abs-rel (\S+)", out).group(1)) <= 2e-2, out
+    assert int(re.search(r"idx out of range or repeated (\d+)", out).group(1)) == 0, out
+    nf, nfd = map(int, re.search(r"non-finite rows (\d+) \(finiteness mismatches (\d+)\)", out).groups())
+    assert nfd == 0 and nf == (3 if "EMU_POISON" in env else 0), out
     if args[11]:    # the pre-norm's row against the oracle's sequential-sum norm
         # bf16: 2 codes.  f32: two orders of a sum of H positive squares
         # differ by at most about 2H ulps of the sum, and inv and y add a few

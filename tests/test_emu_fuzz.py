@@ -1,8 +1,9 @@
 """Randomised host emulation (opt-in: XS_EMU_FUZZ=N runs N cases of each
 kind, XS_EMU_FUZZ_SEED picks the campaign).  Each case draws a shape, router,
 routing options (group-limited, scaling, renormalisation), dtype, expert
-format, pre-norm, residual, entry point, dispatch switches and (a quarter of
-the cases) fragment-packed weights on the weight-direct GEMMs, runs the whole
+format, pre-norm, residual, entry point, dispatch switches, NaN / Inf tokens
+and (a quarter of the cases) fragment-packed weights on the weight-direct
+GEMMs, runs the whole
 forward through the library's C ABI on the emulator (tests/emu/fwd_main.cpp)
 or the certified router alone (tests/emu/router_main.cpp, with one of the
 three MFMA rounding models), and applies the same checks as the fixed cases:
@@ -57,6 +58,9 @@ def _forward_case(exe, i):
     if r.random() < 0.3:
         ng, tg = _groups(r, E, k)
         env["EMU_ROUTE"] = f"{ng},{tg},{r.choice([0, 1])},{r.choice([1.0, 2.5])}"
+    poison = r.random() < 0.1
+    if poison:
+        env["EMU_POISON"] = r.choice(["nan", "inf"])
     frag = 0
     if r.random() < 0.25:     # the weight-direct GEMMs on fragment-packed weights
         frag, H, I, E = r.choice([1, 2]), 1024, r.choice([512, 1024]), r.choice([4, 8, 16])
@@ -76,8 +80,15 @@ def _forward_case(exe, i):
     bad = []
     if p.returncode != 0 or not re.search(r"^errors 0$", out, re.M):
         bad.append("run")
-    bad += [n for n in ("idx", "w", "counts", "offsets", "perm", "inv", "toggle") if c.get(n, 0)]
-    if router in (1, 2) and c.get("ref idx", 0):
+    bad += [n for n in ("own permutation", "toggle") if c.get(n, 1 if n == "own permutation" else 0)]
+    bad += [] if poison else [n for n in ("idx", "w", "counts", "offsets", "perm", "inv") if c.get(n, 0)]
+    m = re.search(r"idx out of range or repeated (\d+)", out)
+    if not m or int(m.group(1)):
+        bad.append("idx range")
+    m = re.search(r"non-finite rows (\d+) \(finiteness mismatches (\d+)\)", out)
+    if not m or int(m.group(2)) or int(m.group(1)) != (3 if poison else 0):
+        bad.append("finiteness")
+    if router in (1, 2) and not poison and c.get("ref idx", 0):
         bad.append("ref idx")
     if router == 2 and c.get("logit", 0):
         bad.append("logit")
