@@ -24,39 +24,18 @@ weight-direct GEMMs behind XS_WEIGHT_DIRECT=1 (packed by the library's own
 packing kernels, with XS_EMU_FULL=1)."""
 import os
 import re
-import shutil
 import subprocess
-import sys
 
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 EMU = os.path.join(ROOT, "tests", "emu")
-HIP = os.path.join(ROOT, "xstar-infer_amd", "csrc", "hip")
-CLANG = "/opt/rocm/llvm/bin/clang++"
-FLAGS = ["-O1", "-std=c++20", "-pthread", "-Wno-psabi", "-ffp-contract=off"]
 
 
 @pytest.fixture(scope="module")
-def fwd_emu(tmp_path_factory):
-    if not os.path.exists(CLANG):
-        pytest.skip("clang++ not found")
-    import oracle
-    oracle.lib()
-    d = tmp_path_factory.mktemp("fwd_emu")
-    subprocess.run([sys.executable, os.path.join(EMU, "gen_fwd.py"), HIP, str(d)], check=True, cwd=EMU)
-    inc = ["-I", str(d), "-I", EMU, "-I", os.path.join(ROOT, "include")]
-    srcs = sorted(f for f in os.listdir(d) if f.endswith(".cpp"))
-    procs = [subprocess.Popen([CLANG, *FLAGS, *inc, "-c", str(d / f), "-o", str(d / (f[:-4] + ".o"))])
-             for f in srcs]
-    assert all(p.wait() == 0 for p in procs)
-    build = os.path.join(ROOT, "oracle", "_build")
-    exe = d / "fwd_emu"
-    subprocess.run([CLANG, *FLAGS, *inc, "-I", os.path.join(ROOT, "oracle"), os.path.join(EMU, "fwd_main.cpp"),
-                    *[str(d / (f[:-4] + ".o")) for f in srcs], "-o", str(exe), "-L", build, "-loracle",
-                    f"-Wl,-rpath,{build}"], check=True)
-    yield str(exe)
-    shutil.rmtree(d, ignore_errors=True)
+def fwd_emu(emu_fwd_lib, tmp_path_factory):
+    from conftest import emu_link
+    return emu_link(emu_fwd_lib, os.path.join(EMU, "fwd_main.cpp"), tmp_path_factory.mktemp("fwd_emu") / "fwd_emu")
 
 
 # name, env, (T H I E k seed fp4 shared router x_f32 zipf norm residual noalloc [frag [toggle]]), expected routed GEMM

@@ -1,0 +1,43 @@
+"""Host emulation of the stage entry points of the C ABI, the CPU
+counterpart of tests/test_gpu_stages.py: each call runs the library's own
+launcher and kernel source on the CPU (tests/emu/stages_main.cpp over the
+objects of tests/emu/gen_fwd.py) and is compared with the CPU oracle.
+
+- activation quant, FP8 1x128 and MXFP8, bf16 and f32 input: bit for bit;
+- weight quant, FP8 128x128 blocks and MXFP4, batched: bit for bit;
+- the codec inputs cover many binades, zero values and zero groups, values
+  at e4m3 / e2m1 rounding ties after scaling, and near-overflow values;
+- RMSNorm: within 2 bf16 codes of the oracle's sequential sum (f32: the
+  summation-order bound), and its fused FP8 quant equal, bit for bit, to the
+  quantization of its own output;
+- route: plain, exact ties, group-limited, E not a multiple of 64, E = 1024
+  with top-16, E = 1, scaling, with and without renormalisation and bias:
+  indices and weights bit for bit;
+- permute: counts, offsets, permutation and inverse bit for bit from 1 to
+  2000 tokens, and the two rejections (an expert named twice in a row, an
+  index out of range) with their messages;
+- router logits with the chain router, bf16 and f32: gemm_cpu's bits."""
+import os
+import re
+import subprocess
+
+import pytest
+
+EMU = os.path.join(os.path.dirname(os.path.abspath(__file__)), "emu")
+
+
+@pytest.fixture(scope="module")
+def stages_emu(emu_fwd_lib, tmp_path_factory):
+    from conftest import emu_link
+    return emu_link(emu_fwd_lib, os.path.join(EMU, "stages_main.cpp"), tmp_path_factory.mktemp("stages") / "stages")
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_stages_emulated(stages_emu, seed):
+    r = subprocess.run([stages_emu, str(seed)], capture_output=True, text=True, timeout=600)
+    out = r.stdout + r.stderr
+    assert r.returncode == 0, out[-3000:]
+    assert re.search(r"^errors 0$", out, re.M), out[-3000:]
+    c = {m.group(1): int(m.group(2)) for m in re.finditer(r"^(.+?) mismatches (\d+)$", out, re.M)}
+    assert len(c) == 13 and all(v == 0 for v in c.values()), out
+    assert "permute errors ok" in out, out
