@@ -111,8 +111,10 @@ def test_forward_emulated(fwd_emu, name, env, args, routed):
         assert c["logit"] == 0, out     # NaN logits compare by their bits
     assert float(re.search(r"max-abs-rel (\S+)", out).group(1)) <= 2e-2, out
     assert int(re.search(r"idx out of range or repeated (\d+)", out).group(1)) == 0, out
-    nf, nfd = map(int, re.search(r"non-finite rows (\d+) \(finiteness mismatches (\d+)\)", out).groups())
-    assert nfd == 0 and nf == (3 if "EMU_POISON" in env else 0), out
+    npz, pzf, cnf = map(int, re.search(r"poisoned rows (\d+): with a finite output element (\d+); "
+                                       r"clean rows with a non-finite one (\d+)", out).groups())
+    assert npz == (len({0, args[0] // 2, args[0] - 1}) if "EMU_POISON" in env else 0), out
+    assert pzf == 0 and cnf == 0, out
     if args[11]:    # the pre-norm's row against the oracle's sequential-sum norm
         # bf16: 2 codes.  f32: two orders of a sum of H positive squares
         # differ by at most about 2H ulps of the sum, and inv and y add a few

@@ -85,8 +85,9 @@ def _forward_case(exe, i):
     m = re.search(r"idx out of range or repeated (\d+)", out)
     if not m or int(m.group(1)):
         bad.append("idx range")
-    m = re.search(r"non-finite rows (\d+) \(finiteness mismatches (\d+)\)", out)
-    if not m or int(m.group(2)) or int(m.group(1)) != (3 if poison else 0):
+    m = re.search(r"poisoned rows (\d+): with a finite output element (\d+); clean rows with a non-finite one (\d+)",
+                  out)
+    if not m or int(m.group(2)) or int(m.group(3)) or int(m.group(1)) != (len({0, T // 2, T - 1}) if poison else 0):
         bad.append("finiteness")
     if router in (1, 2) and not poison and c.get("ref idx", 0):
         bad.append("ref idx")
