@@ -65,14 +65,20 @@ inline int emu_dpp(int old, int src, int ctrl, int, int, bool)
 // selectable (EMU_MFMA_MODEL): 0 the exact products summed in double and
 // rounded once with C; 1 C plus the products in k order, each add rounded to
 // f32; 2 the same with every add truncated toward zero (the coarsest
-// behaviour the certified router's bound allows for).
+// behaviour the certified router's bound allows for); 3 and 4 C and the 32
+// products added in a random order (a fresh one per output), rounded (3) or
+// truncated (4); 5 a pairwise tree over the products, rounded, then C.
+// Every bf16 x bf16 product is exact in f32.
 inline int g_mfma_model = 0;
+// a + b truncated toward zero, exactly: s = RNE(a + b) and its error e
+// (Knuth's two-sum, exact in f32); the truncated sum is s unless e points
+// toward zero from s, then the next float toward zero
 inline float emu_add_rz(float a, float b)
 {
-    const double s = (double)a + (double)b;   // exact: both are floats of close exponent or one dominates
-    float r = (float)s;
-    if ((double)r != s && std::fabs((double)r) > std::fabs(s)) r = std::nextafter(r, 0.0f);
-    return r;
+    const float s = a + b;
+    const float bb = s - a, e = (a - (s - bb)) + (b - bb);
+    if (e == 0.0f || !std::isfinite(s)) return s;
+    return (e > 0.0f) == (s > 0.0f) ? s : std::nextafter(s, 0.0f);
 }
 inline float bf16v(__bf16 b) { uint16_t u; memcpy(&u, &b, 2); return __uint_as_float((uint32_t)u << 16); }
 inline v4f emu_mfma_bf16(v8bf a, v8bf b, v4f c, int, int, int)
@@ -91,17 +97,33 @@ inline v4f emu_mfma_bf16(v8bf a, v8bf b, v4f c, int, int, int)
         return (double)bf16v(v);
     };
     for (int v = 0; v < 4; ++v) {
+        float p[33];
+        for (int k = 0; k < 32; ++k) p[k] = (float)(el(4 * g + v, k, 0) * el(r, k, 16));
         if (g_mfma_model == 0) {
             double s = c[v];
-            for (int k = 0; k < 32; ++k) s += el(4 * g + v, k, 0) * el(r, k, 16);
+            for (int k = 0; k < 32; ++k) s += p[k];
             out[v] = (float)s;
-        } else {
+        } else if (g_mfma_model <= 2) {
             float s = c[v];
-            for (int k = 0; k < 32; ++k) {
-                const float p = (float)(el(4 * g + v, k, 0) * el(r, k, 16));   // exact: bf16 x bf16
-                s = g_mfma_model == 1 ? s + p : emu_add_rz(s, p);
-            }
+            for (int k = 0; k < 32; ++k) s = g_mfma_model == 1 ? s + p[k] : emu_add_rz(s, p[k]);
             out[v] = s;
+        } else if (g_mfma_model <= 4) {
+            p[32] = c[v];
+            uint64_t z = ((uint64_t)blockIdx.x << 40) ^ ((uint64_t)blockIdx.y << 20) ^ ((uint64_t)threadIdx.x << 8) ^
+                         (t_xseq << 2) ^ (uint64_t)v;   // t_xseq: this lane's exchange count
+            for (int i = 32; i > 0; --i) {   // Fisher-Yates with splitmix64
+                z += 0x9e3779b97f4a7c15ull;
+                uint64_t y = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+                y = (y ^ (y >> 27)) * 0x94d049bb133111ebull;
+                std::swap(p[i], p[(y ^ (y >> 31)) % (uint64_t)(i + 1)]);
+            }
+            float s = p[0];
+            for (int i = 1; i < 33; ++i) s = g_mfma_model == 3 ? s + p[i] : emu_add_rz(s, p[i]);
+            out[v] = s;
+        } else {
+            for (int n = 32; n > 1; n /= 2)
+                for (int i = 0; i < n / 2; ++i) p[i] = p[2 * i] + p[2 * i + 1];
+            out[v] = c[v] + p[0];
         }
     }
     tb->wbar[w]->arrive_and_wait();

@@ -17,6 +17,9 @@
 //     pass and routes again; else the routing launch, the pair-parallel chain
 //     launch and a second routing launch), 1 always the latter, 2 always the
 //     former.
+//   EMU_CANCEL=C: a quarter of K holds pairs x = C, C / w = a, -a whose
+//     products cancel at magnitude 1000 (the bound then carries real weight).
+//   EMU_MFMA_MODEL=0..5: the MFMA summation model (router_emu.hpp).
 //   mode chain_bf16 / chain_f32: every logit in gemm_cpu order; prints
 //     "logit mismatches N".
 #include "router_emu.hpp"
@@ -85,6 +88,25 @@ int main(int argc, char **argv)
         memcpy(dst, src, 2 * (size_t)H);
         if (d & 1) dst[d % H] ^= 1;   // one step of the last mantissa bit
         bias[E - dup + d] = bias[d];
+    }
+    // EMU_CANCEL=C: a quarter of the K columns hold pairs with x = C, C and
+    // w = a, -a (|C a| about 1000): they cancel in exact arithmetic, but every
+    // sum of them rounds at that magnitude, so the MFMA logits and the
+    // gemm_cpu logits differ by far more than the margins' fixed terms cover
+    // and only the proven bound keeps the routing exact
+    if (const char *cz = getenv("EMU_CANCEL"); cz && !f32) {
+        const float C = (float)atof(cz);
+        for (int t = 0; t < T; ++t)
+            for (int i = 0; i < H / 4; i += 2) {
+                ((uint16_t *)x)[(size_t)t * H + i] = bf(C);
+                ((uint16_t *)x)[(size_t)t * H + i + 1] = bf(C);
+            }
+        for (int e = 0; e < E; ++e)
+            for (int i = 0; i < H / 4; i += 2) {
+                const uint16_t a = bf(1000.0f / C * nd(rng));
+                ((uint16_t *)wr)[(size_t)e * H + i] = a;
+                ((uint16_t *)wr)[(size_t)e * H + i + 1] = a ^ 0x8000;
+            }
     }
     std::vector<float> ref((size_t)T * E);
     xo_router_logits(x, wr, f32 ? 0 : 1, T, E, H, ref.data());

@@ -6,7 +6,7 @@ and (a quarter of the cases) fragment-packed weights on the weight-direct
 GEMMs, runs the whole
 forward through the library's C ABI on the emulator (tests/emu/fwd_main.cpp)
 or the certified router alone (tests/emu/router_main.cpp, with one of the
-three MFMA rounding models), and applies the same checks as the fixed cases:
+six MFMA summation models), and applies the same checks as the fixed cases:
 routing, counts and permutation bit for bit, top-k from x for the certified
 and chain routers, the chain router's logits bit for bit, the output within
 2e-2 of the oracle's layer, the pre-norm's row within its bound."""
@@ -116,7 +116,7 @@ def _router_case(exe, i):
     ng, tg = _groups(r, E, k) if r.random() < 0.35 else (1, 1)
     args = ["cert", T, E, k, H, r.randint(1, 10**6), ns, r.choice([1, 1, 1, 1, 2, 1e30]),
             r.choice([0, 0.001, 0.1, 1.0, 5.0]), r.choice([0, 0, 1.1]), dup, ng, tg, r.choice([0, 1, 2])]
-    model = r.choice([0, 1, 2])
+    model = r.choice([0, 1, 2, 3, 4, 5])
     p = subprocess.run([exe, *map(str, args)], capture_output=True, text=True, timeout=900,
                        env=dict(os.environ, EMU_MFMA_MODEL=str(model)))
     out = p.stdout + p.stderr

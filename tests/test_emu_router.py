@@ -7,8 +7,9 @@ Certified router: top-k indices equal the oracle's on its gemm_cpu logits,
 weights equal the oracle's routing of the logits the kernels routed on, the
 per-expert token masks match, every recomputed pair's logit is the oracle's
 bit for bit, and with the margins widened (every token through the exact
-pass) every logit is.  The MFMA is modelled three ways (exact sum rounded
-once, k-order rounded adds, truncated adds); the bound must hold for each.
+pass) every logit is.  The MFMA is modelled six ways (exact sum rounded
+once; k-order adds rounded or truncated; random-order adds rounded or
+truncated; a pairwise tree); the bound must hold for each.
 Covers decode (split-K MFMA kernel) and prefill (LDS-ring tile kernel) logits,
 exact and near ties (duplicated router rows), group-limited routing, and E
 not a multiple of 64, and both forms of the certified routing (one launch
@@ -101,6 +102,43 @@ def test_certified_router_matches_reference_routing(router_emu, name, args, mode
         assert flagged == args[0] and pairs == args[0] * args[1]
     elif name == "ties":
         assert flagged > 0            # exact duplicates always need the exact pass
+
+
+ADVERSARIAL = ["decode16", "prefill_tile", "groups", "ties", "e1024_top16", "decode16_pair_parallel"]
+
+
+@pytest.mark.parametrize("name,args", [c for c in CERT_CASES if c[0] in ADVERSARIAL], ids=ADVERSARIAL)
+@pytest.mark.parametrize("model", [3, 4, 5])
+def test_certified_router_any_mfma_summation_order(router_emu, name, args, model):
+    """The bound assumes nothing about the order in which the MFMA adds its 32
+    products and C: random orders with each add rounded (3) or truncated (4),
+    and a pairwise tree (5), must route exactly like the reference too."""
+    out = _run(router_emu, "cert", *args, model=model)
+    assert _counts(out) == {"idx": 0, "w": 0, "mask": 0, "pair": 0, "exact": 0}, out
+
+
+def test_certified_bound_is_what_keeps_the_routing_exact(router_emu):
+    """Sensitivity of the checks above.  Inputs whose products cancel at
+    magnitude 1000 (EMU_CANCEL) make the MFMA logits differ from gemm_cpu's by
+    far more than the margins' fixed terms (2^-20 and the bias term), and near
+    ties (dup) put experts within that error.  With the proven term removed
+    (margin scale 0), a truncating random-order MFMA routes tokens wrongly;
+    with it, every token is routed exactly.  So a bound missing its
+    error terms fails these tests."""
+    args = ("cert", 64, 256, 6, 2048, 8, 4)
+    env = dict(os.environ, EMU_CANCEL="256", EMU_MFMA_MODEL="4")
+
+    def run(margin):
+        r = subprocess.run([router_emu, *map(str, args), str(margin), "0.1", "0", "32"], capture_output=True,
+                           text=True, timeout=600, env=env)
+        out = r.stdout + r.stderr
+        assert r.returncode == 0 and re.search(r"^errors 0$", out, re.M), out[-3000:]
+        return _counts(out), out
+
+    c0, out0 = run(0)
+    assert c0["idx"] > 0, out0
+    c1, out1 = run(1)
+    assert c1 == {"idx": 0, "w": 0, "mask": 0, "pair": 0, "exact": 0}, out1
 
 
 def test_route_sigmoid_error_bound(router_emu):
