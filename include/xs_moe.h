@@ -210,7 +210,7 @@ enum { XS_ROUTER_MFMA = 0, XS_ROUTER_CERTIFIED = 1, XS_ROUTER_CHAIN = 2 };
  * (xstar_cpp/src/ops/transformer_block.cpp:75,142,204,353).
  * ------------------------------------------------------------------------- */
 typedef struct {
-    int64_t T;            /* tokens */
+    int64_t T;            /* tokens (T x E < 2^31; T x H and T x (top_k + 1) x I < 2^32) */
     int64_t H;            /* hidden (multiple of 256) */
     int64_t I;            /* expert intermediate (multiple of 128) */
     int64_t E;            /* routed experts (<= 1024) */

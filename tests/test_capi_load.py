@@ -47,6 +47,20 @@ def test_argument_validation_without_gpu():
     assert L.xs_moe_workspace_size(ctypes.byref(big)) > 0
     big.T = 300000
     assert L.xs_moe_workspace_size(ctypes.byref(big)) == 0
+    # the router's (token, expert) pair counters are 32-bit: T x E below 2^31
+    wide = X.MoeParams(1 << 23, 256, 128, 256, 1, 1, 1, 1, 1.0, X.XS_BF16, X.XS_FP8_E4M3, 0, 0)
+    assert L.xs_moe_workspace_size(ctypes.byref(wide)) == 0
+    wide.T = (1 << 23) - 1
+    assert L.xs_moe_workspace_size(ctypes.byref(wide)) > 0
+    rc = L.xs_moe_route(ctypes.c_void_p(16), None, 1 << 23, 256, 6, 1, 1, 1, 1.0, ctypes.c_void_p(16),
+                        ctypes.c_void_p(16), None)
+    assert rc == 1 and b"T x E" in L.xs_last_error()
+    rc = L.xs_moe_route(ctypes.c_void_p(16), None, -1, 8, 2, 1, 1, 1, 1.0, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                        None)
+    assert rc == 1
+    rc = L.xs_moe_router_logits(ctypes.c_void_p(16), ctypes.c_void_p(16), X.XS_BF16, 1 << 22, 512, 128, 1,
+                                ctypes.c_void_p(16), None)
+    assert rc == 1 and b"T x E" in L.xs_last_error()
     rc = L.xs_moe_route(None, None, 4, 8, 2, 1, 1, 1, 1.0, None, None, None)
     assert rc == 1 and b"null" in L.xs_last_error()
     rc = L.xs_quant_act_fp8(ctypes.c_void_p(16), X.XS_BF16, 4, 100, ctypes.c_void_p(16), ctypes.c_void_p(16), None)

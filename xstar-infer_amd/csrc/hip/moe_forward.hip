@@ -183,6 +183,8 @@ static int check_params(const xs_moe_params *p)
     XS_REQUIRE(p->routed_format == XS_FP8_E4M3 || p->routed_format == XS_FP4_E2M1X2,
                "unsupported routed expert format");
     XS_REQUIRE(p->T * p->top_k + p->T < ((int64_t)1 << 31), "too many rows");
+    // the certified router lists (token, expert) pairs with 32-bit counters
+    XS_REQUIRE(p->T * p->E < ((int64_t)1 << 31), "too many logits: T x E must stay below 2^31 (split the batch)");
     // the GEMMs address gathered activation rows with 32-bit lane offsets:
     // token x H bytes (gate_up) and position x I bytes (down) stay below 4 GiB
     XS_REQUIRE(p->T * p->H < ((int64_t)1 << 32) && (p->T * p->top_k + p->T) * p->I < ((int64_t)1 << 32),

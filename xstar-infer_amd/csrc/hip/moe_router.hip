@@ -1241,6 +1241,7 @@ int xs_moe_router_logits(const void *x, const void *router_w, int dtype, int64_t
     XS_REQUIRE(x && router_w && logits, "null pointer");
     XS_REQUIRE(dtype == XS_F32 || dtype == XS_BF16, "unsupported dtype");
     XS_REQUIRE(T >= 0 && E >= 1 && H >= 128 && H % 128 == 0, "shape mismatch: H %% 128 != 0");
+    XS_REQUIRE(T * E < ((int64_t)1 << 31), "too many logits: T x E must stay below 2^31 (split the batch)");
     XS_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)router_w & 15) == 0 && ((uintptr_t)logits & 3) == 0,
                "misaligned operand: x and router_w need 16-byte, logits 4-byte alignment");
     return launch_router_logits(x, router_w, dtype, T, E, H, exact, logits, 1, (hipStream_t)stream);
@@ -1252,6 +1253,7 @@ int xs_moe_route(const float *logits, const float *bias, int64_t T, int64_t E, i
 {
     XS_REQUIRE(logits && idx && w, "null pointer");
     XS_REQUIRE(E >= 1 && E <= 1024, "E must be in [1, 1024]");
+    XS_REQUIRE(T >= 0 && T * E < ((int64_t)1 << 31), "too many logits: T x E must stay below 2^31 (split the batch)");
     XS_REQUIRE(k >= 1 && k <= 16 && k <= E, "top_k must be in [1, min(16, E)]");
     if (n_group > 1) {
         XS_REQUIRE(n_group <= 64 && E % n_group == 0 && E / n_group >= 2,
