@@ -597,9 +597,8 @@ struct CertArgs {
 //     so sum_k |S_k| <= 32 sum_j |S_j0| + 32 A.  The MFMA's own result is
 //     allowed 66 u (|acc| + a_j) per instruction: 33 additions of at most
 //     one unit in the last place of a magnitude below |acc| + a_j, whatever
-//     the hardware's internal order and rounding (truncation included); it
-//     must not flush subnormal bf16 operands (products that underflow are
-//     covered by the 2^-100 absolute term).
+//     the hardware's internal order and rounding (truncation included).
+//     Products that underflow are covered by the 2^-100 absolute term.
 //     Slice s starts its accumulator at 0 while L_ref's partial sums carry
 //     P_s (the slices before it), which adds 32 n_s |P_s| for its n_s
 //     blocks; summing the slices rounds by at most u |P_s+1| per add.  Hence
@@ -611,6 +610,13 @@ struct CertArgs {
 //     the bias add rounds by at most 2^-24 (|key| + 1), so the reference's
 //     key lies in [key - m, key + m] with
 //       m = (delta / 4)(1 + 2^-8) + 2^-20 + 2^-22 |bias|.
+//     (The two keys' sigmoid and rounding errors take at most
+//     2^-21 + 2^-23 (1 + |bias|) of the fixed part, leaving 3 2^-23.  An MFMA
+//     that flushed subnormal bf16 operands would lose products totalling less
+//     than H M 2^-126, M the largest operand magnitude, which moves a key by a
+//     quarter of that: within the leftover whenever H M <= 2^106, e.g. any
+//     H <= 65536 with operands below 10^27.  So the bound does not depend on
+//     how the MFMA treats subnormal operands.)
 //     Let T be the top-k on these keys and U the experts whose interval
 //     meets the interval of another expert where either is in T.  Every
 //     expert outside T and U lies below all of T under the reference's keys
