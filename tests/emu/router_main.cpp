@@ -25,6 +25,7 @@
 #include "router_emu.hpp"
 #include <cmath>
 #include <random>
+#include <thread>
 
 #include "router_emu.inc"
 #include "moe_oracle.h"
@@ -47,22 +48,42 @@ int main(int argc, char **argv)
     const int path = argc > 14 ? atoi(argv[14]) : 0;
     if (getenv("EMU_MFMA_MODEL")) g_mfma_model = atoi(getenv("EMU_MFMA_MODEL"));
     if (mode == "sigmoid") {
-        // xs_sigmoid (the route kernel's) against the sigmoid in double: every
-        // 13th float bit pattern (both signs) up to |x| = 2^7, then every
-        // 4099th to infinity; prints the largest absolute error in units of 2^-22
-        double worst = 0;
-        float at = 0;
-        auto check = [&](uint32_t u) {
-            float x;
-            memcpy(&x, &u, 4);
-            const double r = 1.0 / (1.0 + std::exp(-(double)x));
-            const double err = std::fabs((double)xs_sigmoid(x) - r);
-            if (err > worst) { worst = err; at = x; }
-        };
-        for (uint32_t u = 0; u < 0x43000000u; u += 13) { check(u); check(u | 0x80000000u); }
-        for (uint32_t u = 0x43000000u; u < 0x7f800000u; u += 4099) { check(u); check(u | 0x80000000u); }
-        check(0x7f800000u); check(0xff800000u);
-        printf("sigmoid max error %.4f x 2^-22 at %.9g\nerrors %ld\n", worst * 4194304.0, at, (long)g_errors);
+        // xs_sigmoid (the route kernel's) against the sigmoid in double and
+        // against the oracle's xo_sigmoid (bit for bit; on every ostride-th
+        // pattern, argument 2, default 1) on every float but NaN
+        // (2^32 - 2^24 bit patterns, both signs, infinities), over 8 host
+        // threads; prints the largest absolute error in units of 2^-22, where
+        // it occurs, and the number of floats where the two differ
+        const int nth = 8;
+        const uint64_t ostride = argc > 2 ? (uint64_t)std::max(1, atoi(argv[2])) : 1;   // oracle comparison stride
+        std::vector<double> worst(nth, 0.0);
+        std::vector<float> at(nth, 0.0f);
+        std::vector<long> differ(nth, 0);
+        std::vector<std::thread> th;
+        for (int q = 0; q < nth; ++q)
+            th.emplace_back([&, q] {
+                const uint64_t lo = ((uint64_t)1 << 32) * q / nth, hi = ((uint64_t)1 << 32) * (q + 1) / nth;
+                for (uint64_t v = lo; v < hi; ++v) {
+                    const uint32_t u = (uint32_t)v;
+                    if ((u & 0x7fffffffu) > 0x7f800000u) continue;   // NaN
+                    float x;
+                    memcpy(&x, &u, 4);
+                    const double r = 1.0 / (1.0 + std::exp(-(double)x));
+                    const float g = xs_sigmoid(x);
+                    const double err = std::fabs((double)g - r);
+                    if (err > worst[q]) { worst[q] = err; at[q] = x; }
+                    if (v % ostride == 0) {
+                        const float o = xo_sigmoid(x);
+                        differ[q] += memcmp(&g, &o, 4) != 0;
+                    }
+                }
+            });
+        for (auto &t : th) t.join();
+        const int b = (int)(std::max_element(worst.begin(), worst.end()) - worst.begin());
+        long nd = 0;
+        for (long d : differ) nd += d;
+        printf("sigmoid max error %.4f x 2^-22 at %.9g\nsigmoid oracle mismatches %ld\nerrors %ld\n",
+               worst[b] * 4194304.0, at[b], nd, (long)g_errors);
         return 0;
     }
     std::mt19937 rng(seed);
