@@ -20,12 +20,16 @@
 //   EMU_CANCEL=C: a quarter of K holds pairs x = C, C / w = a, -a whose
 //     products cancel at magnitude 1000 (the bound then carries real weight).
 //   EMU_MFMA_MODEL=0..5: the MFMA summation model (router_emu.hpp).
+//   mode bf16 [libxsref.so]: the bf16 rounding on every float (device,
+//     oracle and, given its path, the reference's own); mode sigmoid
+//     [stride]: xs_sigmoid's error on every float, and against the oracle.
 //   mode chain_bf16 / chain_f32: every logit in gemm_cpu order; prints
 //     "logit mismatches N".
 #include "router_emu.hpp"
 #include <cmath>
 #include <random>
 #include <thread>
+#include <dlfcn.h>
 
 #include "router_emu.inc"
 #include "moe_oracle.h"
@@ -84,6 +88,52 @@ int main(int argc, char **argv)
         for (long d : differ) nd += d;
         printf("sigmoid max error %.4f x 2^-22 at %.9g\nsigmoid oracle mismatches %ld\nerrors %ld\n",
                worst[b] * 4194304.0, at[b], nd, (long)g_errors);
+        return 0;
+    }
+    if (mode == "bf16") {
+        // xs::bf16_from_f32 (every kernel's bf16 rounding) against the
+        // oracle's xo_bf16_from_f32, and the oracle against the reference's
+        // own bfloat16(float) (xstar_cpp/src/bfloat16.cpp, compiled into
+        // oracle/_ref, argument 2: its path, when built; argument 3: compare
+        // with it on every n-th chunk of 65536 floats), on every float
+        // including NaN and infinities, over 8 host threads
+        typedef void (*RefFn)(const float *, uint16_t *, int64_t);
+        RefFn ref = nullptr;
+        if (argc > 2) {
+            if (void *h = dlopen(argv[2], RTLD_NOW)) ref = (RefFn)dlsym(h, "xsref_bf16_from_f32");
+            if (!ref) { printf("cannot load the reference conversion from %s\n", argv[2]); return 1; }
+        }
+        const int nth = 8;
+        const uint64_t rstride = argc > 3 ? (uint64_t)std::max(1, atoi(argv[3])) : 1;   // reference: every rstride-th chunk
+        std::vector<long> dev(nth, 0), rdiff(nth, 0);
+        std::vector<std::thread> th;
+        for (int q = 0; q < nth; ++q)
+            th.emplace_back([&, q] {
+                const uint64_t lo = ((uint64_t)1 << 32) * q / nth, hi = ((uint64_t)1 << 32) * (q + 1) / nth;
+                const size_t chunk = 1 << 16;
+                std::vector<float> xs(chunk);
+                std::vector<uint16_t> rs(chunk);
+                for (uint64_t c0 = lo; c0 < hi; c0 += chunk) {
+                    const size_t n = (size_t)std::min<uint64_t>(chunk, hi - c0);
+                    for (size_t i = 0; i < n; ++i) {
+                        const uint32_t u = (uint32_t)(c0 + i);
+                        memcpy(&xs[i], &u, 4);
+                    }
+                    const bool withref = ref && (c0 / chunk) % rstride == 0;
+                    if (withref) ref(xs.data(), rs.data(), (int64_t)n);
+                    for (size_t i = 0; i < n; ++i) {
+                        const uint16_t o = xo_bf16_from_f32(xs[i]);
+                        dev[q] += bf16_from_f32(xs[i]) != o;
+                        if (withref) rdiff[q] += rs[i] != o;
+                    }
+                }
+            });
+        for (auto &t : th) t.join();
+        long nd_ = 0, nr = 0;
+        for (int q = 0; q < nth; ++q) { nd_ += dev[q]; nr += rdiff[q]; }
+        printf("bf16 device mismatches %ld\n", nd_);
+        if (ref) printf("bf16 reference mismatches %ld\n", nr);
+        printf("errors %ld\n", (long)g_errors);
         return 0;
     }
     std::mt19937 rng(seed);

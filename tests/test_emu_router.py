@@ -43,7 +43,7 @@ def router_emu(tmp_path_factory):
     exe = d / "router_emu"
     subprocess.run([CLANG, "-O2", "-std=c++20", "-pthread", "-Wno-psabi", "-ffp-contract=off", "-I", EMU,
                     "-I", str(d), "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROOT, "oracle"),
-                    os.path.join(EMU, "router_main.cpp"), "-o", str(exe), "-L", build, "-loracle",
+                    os.path.join(EMU, "router_main.cpp"), "-o", str(exe), "-L", build, "-loracle", "-ldl",
                     f"-Wl,-rpath,{build}"], check=True)
     yield str(exe)
     shutil.rmtree(d, ignore_errors=True)
@@ -139,6 +139,22 @@ def test_certified_bound_is_what_keeps_the_routing_exact(router_emu):
     assert c0["idx"] > 0, out0
     c1, out1 = run(1)
     assert c1 == {"idx": 0, "w": 0, "mask": 0, "pair": 0, "exact": 0}, out1
+
+
+def test_bf16_rounding_on_every_float(router_emu):
+    """Row a9 by exhaustion: the kernels' bf16 rounding (xs_device.hpp), the
+    oracle's and the reference's own bfloat16(float) (bfloat16.cpp:5-25,
+    compiled into oracle/_ref when the reference tree is present) agree on all
+    2^32 floats, NaN and infinities included (against the reference: every
+    16th chunk of 65536 floats here, every float with XS_EMU_FULL=1, which
+    takes about 4 minutes)."""
+    ref = os.path.join(ROOT, "oracle", "_ref", "libxsref.so")
+    full = os.environ.get("XS_EMU_FULL") == "1"
+    args = ["bf16"] + ([ref, "1" if full else "16"] if os.path.exists(ref) else [])
+    out = _run(router_emu, *args)
+    assert int(re.search(r"bf16 device mismatches (\d+)", out).group(1)) == 0, out
+    if os.path.exists(ref):
+        assert int(re.search(r"bf16 reference mismatches (\d+)", out).group(1)) == 0, out
 
 
 def test_route_sigmoid_error_bound(router_emu):
