@@ -7,7 +7,8 @@ The kernels are used as written.  Host launchers are dropped, the tile
 kernel's asm DMA and wait helpers give way to emu.hpp's stand-ins, the dynamic
 LDS arrays become the block's emulated LDS, and the device helpers the kernels
 call (the reproducible exp and sigmoid, the wave max, load8 and the FP8 1x128
-quantizer) are taken from their headers.  Every replacement is asserted."""
+quantizer) and the device codecs (bf16, software e4m3 and e2m1 encoders) are
+taken from their headers.  Every replacement is asserted."""
 import sys
 
 from gen_wd import drop_fn, replace
@@ -45,7 +46,11 @@ def main(src_path, dev_path, int_path, out_path):
     assert "asm volatile" not in body, "an asm statement the emulator has no stand-in for"
     helpers = "".join(take_fn(dev, s) for s in [
         "__device__ __forceinline__ float xs_expf(", "__device__ __forceinline__ float xs_sigmoid(",
-        "__device__ __forceinline__ float wave_max("])
+        "__device__ __forceinline__ float wave_max(",
+        # the device codecs as written (xs::; the emulator's own same-named
+        # stand-ins live outside the namespace), for the every-float checks
+        "__device__ __forceinline__ uint16_t bf16_from_f32(", "__device__ __forceinline__ uint32_t e4m3_encode_sw(",
+        "__device__ __forceinline__ uint32_t e2m1_encode_sw("])
     helpers += "".join(take_fn(inter, s) for s in [
         "__device__ __forceinline__ void load8(const uint16_t *p, float *v)",
         "__device__ __forceinline__ void load4(const uint16_t *p, float *v)",

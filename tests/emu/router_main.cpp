@@ -22,7 +22,8 @@
 //   EMU_MFMA_MODEL=0..5: the MFMA summation model (router_emu.hpp).
 //   mode bf16 [libxsref.so]: the bf16 rounding on every float (device,
 //     oracle and, given its path, the reference's own); mode sigmoid
-//     [stride]: xs_sigmoid's error on every float, and against the oracle.
+//     [stride]: xs_sigmoid's error on every float, and against the oracle;
+//     mode codecs: the software e4m3 / e2m1 encoders on every float.
 //   mode chain_bf16 / chain_f32: every logit in gemm_cpu order; prints
 //     "logit mismatches N".
 #include "router_emu.hpp"
@@ -91,7 +92,8 @@ int main(int argc, char **argv)
         return 0;
     }
     if (mode == "bf16") {
-        // xs::bf16_from_f32 (every kernel's bf16 rounding) against the
+        // xs::bf16_from_f32 (every kernel's bf16 rounding, from xs_device.hpp
+        // as written; not the emulator's stand-in of the same name) against the
         // oracle's xo_bf16_from_f32, and the oracle against the reference's
         // own bfloat16(float) (xstar_cpp/src/bfloat16.cpp, compiled into
         // oracle/_ref, argument 2: its path, when built; argument 3: compare
@@ -123,7 +125,7 @@ int main(int argc, char **argv)
                     if (withref) ref(xs.data(), rs.data(), (int64_t)n);
                     for (size_t i = 0; i < n; ++i) {
                         const uint16_t o = xo_bf16_from_f32(xs[i]);
-                        dev[q] += bf16_from_f32(xs[i]) != o;
+                        dev[q] += xs::bf16_from_f32(xs[i]) != o;
                         if (withref) rdiff[q] += rs[i] != o;
                     }
                 }
@@ -134,6 +136,33 @@ int main(int argc, char **argv)
         printf("bf16 device mismatches %ld\n", nd_);
         if (ref) printf("bf16 reference mismatches %ld\n", nr);
         printf("errors %ld\n", (long)g_errors);
+        return 0;
+    }
+    if (mode == "codecs") {
+        // the kernels' software encoders (xs_device.hpp: e4m3_encode_sw for
+        // MXFP8 activations and FP8 weights, e2m1_encode_sw for MXFP4
+        // weights) against the oracle's on every float (every stride-th bit
+        // pattern, argument 2, default 1), NaN and infinities included, over 8
+        // host threads
+        const int nth = 8;
+        const uint64_t stride = argc > 2 ? (uint64_t)std::max(1, atoi(argv[2])) : 1;   // every stride-th pattern
+        std::vector<long> d8(nth, 0), d4(nth, 0);
+        std::vector<std::thread> th;
+        for (int q = 0; q < nth; ++q)
+            th.emplace_back([&, q] {
+                const uint64_t lo = ((uint64_t)1 << 32) * q / nth, hi = ((uint64_t)1 << 32) * (q + 1) / nth;
+                for (uint64_t v = lo + (stride - lo % stride) % stride; v < hi; v += stride) {
+                    const uint32_t u = (uint32_t)v;
+                    float x;
+                    memcpy(&x, &u, 4);
+                    d8[q] += xs::e4m3_encode_sw(x) != (uint32_t)xo_e4m3_encode(x);
+                    d4[q] += xs::e2m1_encode_sw(x) != (uint32_t)xo_e2m1_encode(x);
+                }
+            });
+        for (auto &t : th) t.join();
+        long a = 0, b = 0;
+        for (int q = 0; q < nth; ++q) { a += d8[q]; b += d4[q]; }
+        printf("e4m3 encode mismatches %ld\ne2m1 encode mismatches %ld\nerrors %ld\n", a, b, (long)g_errors);
         return 0;
     }
     std::mt19937 rng(seed);

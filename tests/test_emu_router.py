@@ -157,6 +157,16 @@ def test_bf16_rounding_on_every_float(router_emu):
         assert int(re.search(r"bf16 reference mismatches (\d+)", out).group(1)) == 0, out
 
 
+def test_software_encoders_on_every_float(router_emu):
+    """The kernels' software e4m3 encoder (MXFP8 activations, FP8 weight
+    quantization) and e2m1 encoder (MXFP4 weights) equal the oracle's: on
+    every 61st bit pattern here, on all 2^32 floats with XS_EMU_FULL=1 (about
+    3.5 minutes, clean): RNE, saturation, subnormals, NaN and infinities."""
+    out = _run(router_emu, "codecs", 1 if os.environ.get("XS_EMU_FULL") == "1" else 61)
+    assert int(re.search(r"e4m3 encode mismatches (\d+)", out).group(1)) == 0, out
+    assert int(re.search(r"e2m1 encode mismatches (\d+)", out).group(1)) == 0, out
+
+
 def test_route_sigmoid_error_bound(router_emu):
     """The certified router's margin assumes xs_sigmoid is within 2^-22 of the
     true sigmoid for every float: checked on every float but NaN (both signs,
