@@ -8,8 +8,8 @@ Per source file the hardware helpers (asm DMAs, vmcnt waits, LDS address
 casts) give way to emu.hpp's stand-ins, LDS arrays come from the block's
 emulated LDS, and `k<<<grid, block, smem, st>>>(args)` becomes a synchronous
 emu_kl launch.  The weight-direct GEMMs' register loads count in
-the lane's vmcnt queue (emu.hpp); the single dense GEMM is not part of the
-forward, and its launcher is replaced by a stub that refuses.  Every replacement is asserted."""
+the lane's vmcnt queue (emu.hpp); the single dense GEMM's sc1 partial-tile
+accesses become plain bounds-checked ones.  Every replacement is asserted."""
 import os
 import re
 import sys
@@ -65,6 +65,24 @@ WD_COMMON = [
     ("__device__ __forceinline__ void barrier_lds()", "inline void barrier_lds() { __syncthreads(); }\n"),
 ]
 HELPERS["moe_gemm_wd.hip"] = WD_COMMON
+# the single dense GEMM: its sc1 partial-tile store and load are plain
+# bounds-checked 16-byte accesses here (x86 orders them before the counter's
+# locked atomic, as the sc1 policy and the agent-scope atomic do on the card)
+HELPERS["gemm_dense.hip"] = [
+    ("__device__ __forceinline__ uint32_t lds_addr(", ""),
+    ("__device__ __forceinline__ void dma16(", ""),
+    ("__device__ __forceinline__ void dma4(", ""),
+    ("template <int N>\n__device__ __forceinline__ void wait_vm()", ""),
+    ("__device__ __forceinline__ void store16_coh(",
+     "inline void store16_coh(float *p, v4f v)\n{\n"
+     "    if (!emu_check_global(p, 16)) { EMU_ERR(\"store16_coh outside every buffer\"); return; }\n"
+     "    memcpy(p, &v, 16);\n}\n"),
+    ("__device__ __forceinline__ v4f load16_coh(",
+     "inline v4f load16_coh(const float *base, uint32_t byte_off)\n{\n"
+     "    const uint8_t *p = (const uint8_t *)base + byte_off;\n    v4f v = {0.f, 0.f, 0.f, 0.f};\n"
+     "    if (!emu_check_global(p, 16)) { EMU_ERR(\"load16_coh outside every buffer\"); return v; }\n"
+     "    memcpy(&v, p, 16);\n    return v;\n}\n"),
+]
 HELPERS["moe_gemm_wd4.hip"] = WD_COMMON
 # compiler-visible register loads of the weight-direct kernels, and the empty
 # asm statements that pin their folds in place (compiler constraints only)
@@ -91,17 +109,10 @@ TEXT = {
     ],
 }
 
-FILES = ["moe_gemm_wd.hip", "moe_gemm_wdd.hip", "moe_gemm_wd4.hip", "moe_forward.hip", "moe_router.hip", "moe_permute.hip", "moe_gemm.hip", "moe_gemm_stream.hip",
+FILES = ["gemm_dense.hip", "moe_gemm_wd.hip", "moe_gemm_wdd.hip", "moe_gemm_wd4.hip", "moe_forward.hip", "moe_router.hip", "moe_permute.hip", "moe_gemm.hip", "moe_gemm_stream.hip",
          "moe_gemm_wide.hip", "rmsnorm.hip", "xs_runtime.hip"]
 
-STUBS = r"""// generated by gen_fwd.py: the single dense GEMM is not part of the forward
-#include "moe_gemm.hpp"
-namespace xs {
-size_t dense_part_bytes(int64_t) { return 0; }
-int dense_counters(int64_t, int64_t) { return 0; }
-int launch_gemm_dense(const uint8_t *, const float *, const uint8_t *, const float *, uint16_t *, int64_t, int64_t,
-                      int64_t, float *, int32_t *, hipStream_t) { return set_error(XS_ERR_UNSUPPORTED, "emulated: no dense GEMM"); }
-}  // namespace xs
+STUBS = r"""// generated by gen_fwd.py: nothing to stub (every source is emulated)
 """
 
 

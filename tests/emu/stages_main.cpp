@@ -1,7 +1,7 @@
 // Host emulation of the stage entry points of the C ABI (xs_quant_act_fp8,
 // xs_quant_act_mxfp8, xs_quant_weight_fp8_block, xs_quant_weight_mxfp4,
 // xs_rmsnorm with its fused quant, xs_moe_route, xs_moe_permute and
-// xs_moe_router_logits with the chain router), every kernel run from its
+// xs_moe_router_logits with the chain router, xs_gemm_fp8_blockscale), every kernel run from its
 // source on the CPU (gen_fwd.py, hip_emu.hpp), against the CPU oracle.
 // usage: stages_emu seed
 // Prints "<stage> mismatches N" (each must be 0), "permute errors ok|BAD"
@@ -51,6 +51,7 @@ int main(int argc, char **argv)
     const int seed = argc > 1 ? atoi(argv[1]) : 1;
     rng.seed(seed);
     g_math = true;
+    if (getenv("EMU_EARLY")) g_mode = MODE_EARLY;   // DMAs land at issue instead of at their wait
     long bad;
 
     // ---- activation quant, both dtypes
@@ -227,6 +228,59 @@ int main(int argc, char **argv)
             bl += diff(lg, rl.data(), rl.size());
         }
         printf("logits mismatches %ld\n", bl);
+    }
+    // ---- the single FP8 GEMM (gemm_dense.hip): split-K with the sc1 partial
+    // exchange, and whole-K; against float64 on the dequantized operands
+    // (the activation quantizer is bit-exact), and the same bits again
+    {
+        struct G { int64_t M, N, K; };
+        // local K steps per block: 3, 1, 4 (split 4 ways), 4 (2 ways), 1 (whole-K,
+        // 256 tiles), 7 and 5 (more steps than the 4 ring stages: the ring's
+        // refills, row scales included); XS_EMU_FULL adds the bench's
+        // 512 x 4096 x 4096 (2 ways, 16 steps)
+        std::vector<G> gs = {{40, 256, 384}, {1, 128, 128}, {130, 384, 2048}, {300, 512, 1024},
+                             {2048, 2048, 128}, {256, 512, 896}, {100, 384, 1152}};
+        if (getenv("XS_EMU_FULL") && !strcmp(getenv("XS_EMU_FULL"), "1")) gs.push_back({512, 4096, 4096});
+        long bg = 0;
+        double worst = 0;
+        std::normal_distribution<float> nd(0.f, 1.f);
+        for (const G &c : gs) {
+            uint16_t *A = (uint16_t *)emu_alloc(2 * c.M * c.K, "gA");
+            std::vector<float> af(c.M * c.K), wf(c.N * c.K);
+            for (int64_t i = 0; i < c.M * c.K; ++i) { A[i] = xo_bf16_from_f32(nd(rng)); af[i] = xo_f32_from_bf16(A[i]); }
+            for (auto &v : wf) v = 0.02f * nd(rng);
+            uint8_t *B = (uint8_t *)emu_alloc(c.N * c.K, "gB");
+            float *Bs = (float *)emu_alloc(4 * (c.N / 128) * (c.K / 128), "gBs");
+            xo_quant_weight_fp8_block(wf.data(), c.N, c.K, B, Bs);
+            uint16_t *C = (uint16_t *)emu_alloc(2 * c.M * c.N, "gC");
+            const size_t wsb = xs_gemm_fp8_blockscale_workspace_size(c.M, c.K);
+            void *ws = emu_alloc(wsb, "gws");
+            bg += xs_gemm_fp8_blockscale(A, B, Bs, c.M, c.N, c.K, C, ws, wsb, nullptr) != 0;
+            std::vector<uint16_t> first(C, C + c.M * c.N);
+            bg += xs_gemm_fp8_blockscale(A, B, Bs, c.M, c.N, c.K, C, ws, wsb, nullptr) != 0;
+            bg += diff(C, first.data(), first.size());
+            std::vector<uint8_t> aq(c.M * c.K);
+            std::vector<float> as(c.M * c.K / 128);
+            xo_quant_act_fp8(af.data(), c.M, c.K, aq.data(), as.data());
+            std::vector<double> ad(c.M * c.K), bd(c.N * c.K);
+            for (int64_t i = 0; i < c.M * c.K; ++i) ad[i] = (double)xo_e4m3_decode(aq[i]) * as[i / 128];
+            for (int64_t n = 0; n < c.N; ++n)
+                for (int64_t kk = 0; kk < c.K; ++kk)
+                    bd[n * c.K + kk] = (double)xo_e4m3_decode(B[n * c.K + kk]) * Bs[(n / 128) * (c.K / 128) + kk / 128];
+            double rmax = 0, dmax = 0;
+            for (int64_t m = 0; m < c.M; ++m)
+                for (int64_t n = 0; n < c.N; ++n) {
+                    double r = 0;
+                    for (int64_t kk = 0; kk < c.K; ++kk) r += ad[m * c.K + kk] * bd[n * c.K + kk];
+                    rmax = std::max(rmax, std::fabs(r));
+                    dmax = std::max(dmax, std::fabs((double)xo_f32_from_bf16(C[m * c.N + n]) - r));
+                }
+            const double err = dmax / (rmax > 0 ? rmax : 1);
+            if (getenv("EMU_VERBOSE")) printf("dense %lld x %lld x %lld: max-abs-rel %.3g\n", (long long)c.M, (long long)c.N, (long long)c.K, err);
+            worst = std::max(worst, err);
+            bg += !(err < 4e-3);
+        }
+        printf("dense gemm mismatches %ld\ndense gemm max-abs-rel %.3g\n", bg, worst);
     }
     printf("errors %ld\n", (long)g_errors);
     return 0;

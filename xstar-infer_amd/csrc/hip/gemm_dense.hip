@@ -233,15 +233,17 @@ __global__ __launch_bounds__(64 * NW) void gemm_dense_fp8_kernel(DenseArgs a)
         // Each MFMA slot m of the step, in this order (a scheduling barrier
         // closes each): the MFMA, a quarter of the fold of the previous
         // subtile, and from the second subtile on, which follows the wait and
-        // the block barrier, one DMA of step k+kNS every DG slots and the
-        // fragments (and fold factors) of step k+1.  Subtile 0 needs only
+        // the block barrier, the fragments (and fold factors) of step k+1 and
+        // a share of the P + 1 loads of step k+kNS: slot s after the barrier
+        // issues loads [ceil(s (P+1) / NS_), ceil((s+1) (P+1) / NS_)), so
+        // every load of the step goes out (the row-scale load, the last, on
+        // the scale waves), as the waits count them.  Subtile 0 needs only
         // registers, so the matrix core has work queued across the barrier; a
         // DMA instruction holds its wave until the CU's ~64 B/clk memory path
-        // takes it, so the DMAs go out one at a time between MFMAs.
+        // takes it, so the DMAs go out a few at a time between MFMAs.
         constexpr int M0 = 4;                         // slots before the barrier
         constexpr int NR = 4 + 2 * MI;                // fragment and factor reads
         constexpr int NS_ = 4 * MI - M0;              // slots after the barrier
-        constexpr int DG = NS_ / (P + 1) > 0 ? NS_ / (P + 1) : 1;
         constexpr int RG = (NR + NS_ - 1) / NS_;      // reads per slot
         const uint8_t *nA = smem + ((k + 1) % kNS) * kStage;
         const float *nS = reinterpret_cast<const float *>(nA + kA);
@@ -274,7 +276,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_dense_fp8_kernel(DenseArgs a)
                     else wait_vm<(kNS - 2) * P>();
                     __syncthreads();   // step k+1 landed everywhere; slot k % kNS is free
                 }
-                if (m >= M0 && (m - M0) % DG == 0 && (m - M0) / DG <= P) issue_one(k + kNS, (m - M0) / DG);
+                if (m >= M0) {
+                    const int d0 = ((m - M0) * (P + 1) + NS_ - 1) / NS_, d1 = ((m - M0 + 1) * (P + 1) + NS_ - 1) / NS_;
+#pragma unroll
+                    for (int d = d0; d < d1; ++d) issue_one(k + kNS, d);
+                }
                 q[i & 1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fc.wf[j], fc.bx[i], v4f{0.f, 0.f, 0.f, 0.f},
                                                                                0, 0, 0, 0, 0, 0);
                 if (m >= M0)
