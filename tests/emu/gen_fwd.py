@@ -135,7 +135,7 @@ def matching(s, i, open_ch, close_ch):
     raise ValueError("unbalanced")
 
 
-def rewrite_launches(s):
+def rewrite_launches(s, src="?"):
     out, pos, n = [], 0, 0
     while True:
         i = s.find("<<<", pos)
@@ -166,7 +166,8 @@ def rewrite_launches(s):
         q = matching(s, p, "(", ")")
         args = s[p + 1:q - 1]
         out.append(s[pos:k])
-        out.append(f"emu_kl([&] {{ {name}({args}); }}, {cfg})")
+        site = f"{src}:{name.split('<')[0]}#{n}"   # launch site, for EMU_KERNEL_LOG
+        out.append(f"(emu_note_kernel(\"{site}\"), emu_kl([&] {{ {name}({args}); }}, {cfg}))")
         pos, n = q, n + 1
     out.append(s[pos:])
     return "".join(out), n
@@ -182,7 +183,19 @@ def transform(name, s):
     s = re.sub(r"__shared__ (\w+) (\w+)\[([^\]]+)\];", r"\1 *\2 = emu_shared<\1>(\3);", s)
     s = re.sub(r"__shared__ (\w+) (\w+);", r"\1 &\2 = *emu_shared<\1>(1);", s)
     assert "__shared__" not in s, name
-    s, n = rewrite_launches(s)
+    s, n = rewrite_launches(s, name)
+    # each kernel notes its own instantiation once per launch (EMU_KERNEL_LOG),
+    # after a leading #pragma of its body
+    out, pos = [], 0
+    for m in re.finditer(r"__global__[^;{]*?\)\s*\{", s):
+        e = m.end()
+        rest = s[e:]
+        lead = len(rest) - len(rest.lstrip())
+        if rest.lstrip().startswith("#pragma"):
+            e += lead + rest.lstrip().index("\n") + 1
+        out.append(s[pos:e] + " EMU_NOTE_KERNEL();")
+        pos = e
+    s = "".join(out) + s[pos:]
     assert "<<<" not in s
     assert "asm volatile" not in s, f"{name}: an asm statement the emulator has no stand-in for"
     return s

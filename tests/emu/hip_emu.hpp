@@ -116,6 +116,21 @@ inline auto min(A a, B b) { using C = std::common_type_t<A, B>; return (C)a < (C
 template <typename A, typename B, typename = std::enable_if_t<!std::is_same_v<A, B>>>
 inline auto max(A a, B b) { using C = std::common_type_t<A, B>; return (C)a > (C)b ? (C)a : (C)b; }
 
+// EMU_KERNEL_LOG=<file>: every launched kernel's name is appended to the file
+// (coverage of the emulated suites)
+inline void emu_note_kernel(const char *name)
+{
+    static std::mutex m;
+    if (const char *f = getenv("EMU_KERNEL_LOG")) {
+        std::lock_guard<std::mutex> l(m);
+        if (FILE *fp = fopen(f, "a")) { fprintf(fp, "%s\n", name); fclose(fp); }
+    }
+}
+#define EMU_NOTE_KERNEL()                                                                              \
+    do {                                                                                               \
+        if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && getenv("EMU_KERNEL_LOG")) \
+            emu_note_kernel(__PRETTY_FUNCTION__);                                                      \
+    } while (0)
 // a kernel launch: every block's lanes as fibers (emu_run_grid), synchronous;
 // static __shared__ arrays follow the dynamic LDS
 template <typename F>

@@ -143,6 +143,48 @@ int main(int argc, char **argv)
             xo_quant_act_fp8(yf.data(), rows, hidden, rq.data(), rs.data());
             bq += diff(q, rq.data(), x.size()) + diff(s, rs.data(), rs.size());
         }
+        // every chunk count of the wave kernel (hidden = 512 NC, NC = 1..16,
+        // with the fused quant), and the block kernel: hidden above 8192 (with
+        // the quant), hidden not a multiple of 8, rows misaligned by one element
+        struct N { int64_t rows, hidden; bool quant; int mis; };
+        std::vector<N> ns;
+        for (int nc = 1; nc <= 16; ++nc) ns.push_back({3, 512 * nc, true, 0});
+        ns.push_back({3, 8320, true, 0});
+        ns.push_back({4, 1001, false, 0});
+        ns.push_back({3, 1024, false, 1});
+        for (const N &c : ns)
+            for (int bf = 0; bf < 2; ++bf) {
+                const size_t el = bf ? 2 : 4, n = (size_t)c.rows * c.hidden;
+                uint8_t *xb = (uint8_t *)emu_alloc((n + 8) * el, "sx"), *wb = (uint8_t *)emu_alloc(c.hidden * el, "sw");
+                uint8_t *yb = (uint8_t *)emu_alloc((n + 8) * el, "sy");
+                void *xd = xb + c.mis * el, *y = yb + c.mis * el;
+                for (size_t i = 0; i < n; ++i) {
+                    const float v = 2.f * nd(rng);
+                    if (bf) ((uint16_t *)xd)[i] = xo_bf16_from_f32(v); else ((float *)xd)[i] = v;
+                }
+                for (int64_t i = 0; i < c.hidden; ++i) {
+                    const float v = 1.f + 0.1f * nd(rng);
+                    if (bf) ((uint16_t *)wb)[i] = xo_bf16_from_f32(v); else ((float *)wb)[i] = v;
+                }
+                uint8_t *q = c.quant ? (uint8_t *)emu_alloc(n, "sq") : nullptr;
+                float *sc = c.quant ? (float *)emu_alloc(4 * n / 128, "ss") : nullptr;
+                bq += xs_rmsnorm(xd, wb, bf ? XS_BF16 : XS_F32, c.rows, c.hidden, 1e-6f, y, q, sc, nullptr) != 0;
+                std::vector<uint8_t> ry(n * el);
+                xo_rmsnorm(xd, wb, bf, c.rows, c.hidden, 1e-6f, ry.data());
+                std::vector<float> yf(n);
+                for (size_t i = 0; i < n; ++i) {
+                    const long a = bf ? ((int16_t *)y)[i] : ((int32_t *)y)[i];
+                    const long b = bf ? ((int16_t *)ry.data())[i] : ((int32_t *)ry.data())[i];
+                    over += std::labs(a - b) > (bf ? 2 : 2 * c.hidden + 8);
+                    yf[i] = bf ? xo_f32_from_bf16(((uint16_t *)y)[i]) : ((float *)y)[i];
+                }
+                if (c.quant) {
+                    std::vector<uint8_t> rq(n);
+                    std::vector<float> rs(n / 128);
+                    xo_quant_act_fp8(yf.data(), c.rows, c.hidden, rq.data(), rs.data());
+                    bq += diff(q, rq.data(), n) + diff(sc, rs.data(), rs.size());
+                }
+            }
         printf("norm quant mismatches %ld\nnorm beyond bound mismatches %ld\n", bq, over);
     }
 

@@ -83,14 +83,21 @@ if os.environ.get("XS_EMU_FULL") == "1":
     CASES += FULL_CASES
 
 
-@pytest.mark.parametrize("name,env,args,routed", CASES, ids=[c[0] for c in CASES])
-def test_forward_emulated(fwd_emu, name, env, args, routed):
-    r = subprocess.run([fwd_emu, *map(str, args)], capture_output=True, text=True, timeout=900,
+def run_forward(exe, env, args):
+    r = subprocess.run([exe, *map(str, args)], capture_output=True, text=True, timeout=900,
                        env=dict(os.environ, **env))
-    out = r.stdout + r.stderr
-    assert r.returncode == 0, out[-3000:]
+    return r.returncode, r.stdout + r.stderr
+
+
+def check_forward(rc, out, env, args, routed=None, tile_rows=None):
+    """The checks of one emulated forward (fwd_main.cpp's output), shared with
+    the sweep of tests/test_emu_sweep.py."""
+    assert rc == 0, out[-3000:]
     assert re.search(r"^errors 0$", out, re.M), out[-3000:]
-    assert int(re.search(r"routed (\d+)", out).group(1)) == routed, out
+    if routed is not None:
+        assert int(re.search(r"routed (\d+)", out).group(1)) == routed, out
+    if tile_rows is not None:
+        assert int(re.search(r"plan tile_rows (\d+)", out).group(1)) == tile_rows, out
     if env.get("XS_FUSE_COMBINE") == "1":
         assert re.search(r"fused 1", out), out
     c = {m.group(1): int(m.group(2)) for m in re.finditer(r"^([\w ]+?) mismatches (\d+)", out, re.M)}
@@ -125,3 +132,9 @@ def test_forward_emulated(fwd_emu, name, env, args, routed):
         assert c["logit"] == 0, out     # every logit routed on is the oracle's gemm_cpu logit
     elif router != 1:
         assert (pairs, tokens) == (0, 0), out
+
+
+@pytest.mark.parametrize("name,env,args,routed", CASES, ids=[c[0] for c in CASES])
+def test_forward_emulated(fwd_emu, name, env, args, routed):
+    rc, out = run_forward(fwd_emu, env, args)
+    check_forward(rc, out, env, args, routed)

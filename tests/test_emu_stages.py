@@ -9,7 +9,9 @@ objects of tests/emu/gen_fwd.py) and is compared with the CPU oracle.
   at e4m3 / e2m1 rounding ties after scaling, and near-overflow values;
 - RMSNorm: within 2 bf16 codes of the oracle's sequential sum (f32: the
   summation-order bound), and its fused FP8 quant equal, bit for bit, to the
-  quantization of its own output;
+  quantization of its own output, for every chunk count of the one-wave-per-row
+  kernel (hidden 512..8192) and for the block kernel (hidden above 8192, not a
+  multiple of 8, misaligned rows);
 - route: plain, exact ties, group-limited, E not a multiple of 64, E = 1024
   with top-16, E = 1, scaling, with and without renormalisation and bias:
   indices and weights bit for bit;
