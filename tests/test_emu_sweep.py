@@ -8,6 +8,7 @@ kernel symbols of the built library):
   MXFP4 at 16-row tiles;
 - the persistent stream-K MXFP4 GEMMs at 32- and 64-row tiles;
 - the approximate MFMA router's prefill (tile) kernel;
+- K longer than every LDS ring, so each GEMM family's in-loop refills run;
 - the routing kernels at each width (128, 256, 512 and 1024 experts), the
   one-launch decode routing and the prefill routing with its exact pass.
 
@@ -32,6 +33,15 @@ CASES = [
     ("mxfp4_stream_bm32", {"XS_MOE_STREAM": "1"}, (64, 512, 512, 8, 4, 206, 1, 1, 1, 0, 0, 0, 0, 0), 1, 32),
     ("mxfp4_stream_bm64", {"XS_MOE_STREAM": "1"}, (128, 512, 512, 8, 4, 207, 1, 1, 1, 0, 0, 0, 0, 0), 1, 64),
     ("mfma_router_prefill", {}, (300, 256, 256, 8, 2, 208, 0, 1, 0, 0, 0, 0, 0, 0), None, None),
+    # K longer than every LDS ring (8 K steps and more), so each kernel's
+    # in-loop refills run: tall tiles, stream-K, tiled at 32 and 128 rows,
+    # MXFP4 stream-K (256-wide steps), the approximate router's tile kernel
+    ("tall_deep_k", {}, (300, 1024, 1024, 4, 2, 220, 0, 1, 1, 0, 1.1, 0, 0, 0), 2, 192),
+    ("stream_deep_k", {"XS_MOE_STREAM": "1"}, (64, 1024, 1024, 16, 4, 221, 0, 1, 1, 0, 0, 0, 0, 0), 1, 16),
+    ("tiled_deep_k_bm32", TILED, (64, 1024, 1024, 8, 4, 222, 0, 1, 1, 0, 0, 0, 0, 0), 0, 32),
+    ("tiled_deep_k_bm128", TILED, (256, 1024, 512, 8, 4, 223, 0, 0, 1, 0, 0, 0, 0, 0), 0, 128),
+    ("mxfp4_stream_deep_k", {"XS_MOE_STREAM": "1"}, (64, 2048, 1024, 8, 4, 224, 1, 1, 1, 0, 0, 0, 0, 0), 1, 32),
+    ("mfma_router_prefill_deep_k", {}, (300, 1024, 128, 8, 2, 225, 0, 0, 0, 0, 0, 0, 0, 0), None, None),
     # routing widths (64 experts per lane group): the one-launch decode routing
     # at 128, 256 and 512 experts; the prefill routing launches, with every
     # token through the exact pass (margin) so the second routing runs too
