@@ -134,7 +134,21 @@ def check_forward(rc, out, env, args, routed=None, tile_rows=None):
         assert (pairs, tokens) == (0, 0), out
 
 
+def run_all(exe, cases, workers=4):
+    """Every case's run, several at a time (most cases occupy a few host
+    threads only); {name: (rc, out)}."""
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(workers) as ex:
+        futs = {c[0]: ex.submit(run_forward, exe, c[1], c[2]) for c in cases}
+        return {n: f.result() for n, f in futs.items()}
+
+
+@pytest.fixture(scope="module")
+def forward_runs(fwd_emu):
+    return run_all(fwd_emu, CASES)
+
+
 @pytest.mark.parametrize("name,env,args,routed", CASES, ids=[c[0] for c in CASES])
-def test_forward_emulated(fwd_emu, name, env, args, routed):
-    rc, out = run_forward(fwd_emu, env, args)
+def test_forward_emulated(forward_runs, name, env, args, routed):
+    rc, out = forward_runs[name]
     check_forward(rc, out, env, args, routed)

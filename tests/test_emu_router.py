@@ -89,12 +89,34 @@ CERT_CASES = [
 ]
 
 
+ADVERSARIAL = ["decode16", "prefill_tile", "groups", "ties", "e1024_top16", "decode16_pair_parallel"]
+
+
+@pytest.fixture(scope="module")
+def cert_runs(router_emu):
+    """Every (case, MFMA model) run of the two tests below, four at a time;
+    {(name, model): output} (an AssertionError's message for a failed run)."""
+    from concurrent.futures import ThreadPoolExecutor
+    jobs = [(n, a, m) for n, a in CERT_CASES for m in (0, 1, 2) if not (m and n.startswith("all_exact"))]
+    jobs += [(n, a, m) for n, a in CERT_CASES if n in ADVERSARIAL for m in (3, 4, 5)]
+
+    def one(j):
+        try:
+            return _run(router_emu, "cert", *j[1], model=j[2])
+        except AssertionError as e:
+            return "RUN FAILED " + str(e)
+
+    with ThreadPoolExecutor(4) as ex:
+        return dict(zip([(n, m) for n, _, m in jobs], ex.map(one, jobs)))
+
+
 @pytest.mark.parametrize("name,args", CERT_CASES, ids=[c[0] for c in CERT_CASES])
 @pytest.mark.parametrize("model", [0, 1, 2])
-def test_certified_router_matches_reference_routing(router_emu, name, args, model):
+def test_certified_router_matches_reference_routing(cert_runs, name, args, model):
     if model and name.startswith("all_exact"):
         pytest.skip("the exact pass does not read the MFMA results")
-    out = _run(router_emu, "cert", *args, model=model)
+    out = cert_runs[(name, model)]
+    assert not out.startswith("RUN FAILED"), out
     c = _counts(out)
     assert c == {"idx": 0, "w": 0, "mask": 0, "pair": 0, "exact": 0}, out
     pairs, flagged = map(int, re.search(r"pairs (\d+) flagged (\d+)", out).groups())
@@ -104,16 +126,14 @@ def test_certified_router_matches_reference_routing(router_emu, name, args, mode
         assert flagged > 0            # exact duplicates always need the exact pass
 
 
-ADVERSARIAL = ["decode16", "prefill_tile", "groups", "ties", "e1024_top16", "decode16_pair_parallel"]
-
-
 @pytest.mark.parametrize("name,args", [c for c in CERT_CASES if c[0] in ADVERSARIAL], ids=ADVERSARIAL)
 @pytest.mark.parametrize("model", [3, 4, 5])
-def test_certified_router_any_mfma_summation_order(router_emu, name, args, model):
+def test_certified_router_any_mfma_summation_order(cert_runs, name, args, model):
     """The bound assumes nothing about the order in which the MFMA adds its 32
     products and C: random orders with each add rounded (3) or truncated (4),
     and a pairwise tree (5), must route exactly like the reference too."""
-    out = _run(router_emu, "cert", *args, model=model)
+    out = cert_runs[(name, model)]
+    assert not out.startswith("RUN FAILED"), out
     assert _counts(out) == {"idx": 0, "w": 0, "mask": 0, "pair": 0, "exact": 0}, out
 
 

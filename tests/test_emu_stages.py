@@ -37,11 +37,26 @@ def stages_emu(emu_fwd_lib, tmp_path_factory):
     return emu_link(emu_fwd_lib, os.path.join(EMU, "stages_main.cpp"), tmp_path_factory.mktemp("stages") / "stages")
 
 
-@pytest.mark.parametrize("seed", [1, 2, 3])
-def test_stages_emulated(stages_emu, seed):
-    r = subprocess.run([stages_emu, str(seed)], capture_output=True, text=True, timeout=600)
-    out = r.stdout + r.stderr
-    assert r.returncode == 0, out[-3000:]
+SEEDS = [1, 2, 3]
+
+
+@pytest.fixture(scope="module")
+def stage_runs(stages_emu):
+    """The three seeds' runs at once: {seed: (returncode, output)}."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    def one(seed):
+        r = subprocess.run([stages_emu, str(seed)], capture_output=True, text=True, timeout=600)
+        return r.returncode, r.stdout + r.stderr
+
+    with ThreadPoolExecutor(len(SEEDS)) as ex:
+        return dict(zip(SEEDS, ex.map(one, SEEDS)))
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_stages_emulated(stage_runs, seed):
+    rc, out = stage_runs[seed]
+    assert rc == 0, out[-3000:]
     assert re.search(r"^errors 0$", out, re.M), out[-3000:]
     c = {m.group(1): int(m.group(2)) for m in re.finditer(r"^(.+?) mismatches (\d+)$", out, re.M)}
     assert len(c) == 14 and all(v == 0 for v in c.values()), out

@@ -18,7 +18,7 @@ from concurrent.futures import ThreadPoolExecutor
 
 import pytest
 
-from test_emu_forward import check_forward, fwd_emu, run_forward  # noqa: F401  (fwd_emu: fixture)
+from test_emu_forward import check_forward, fwd_emu, run_all, run_forward  # noqa: F401  (fwd_emu: fixture)
 
 # args: T H I E k seed fp4 shared router x_f32 zipf norm residual noalloc
 TILED = {"XS_MOE_STREAM": "0", "XS_MOE_GEMM": "tiled"}
@@ -60,9 +60,14 @@ CASES = [
 ]
 
 
+@pytest.fixture(scope="module")
+def sweep_runs(fwd_emu):  # noqa: F811
+    return run_all(fwd_emu, CASES)
+
+
 @pytest.mark.parametrize("name,env,args,routed,rows", CASES, ids=[c[0] for c in CASES])
-def test_forward_instantiation(fwd_emu, name, env, args, routed, rows):  # noqa: F811
-    rc, out = run_forward(fwd_emu, env, args)
+def test_forward_instantiation(sweep_runs, name, env, args, routed, rows):
+    rc, out = sweep_runs[name]
     check_forward(rc, out, env, args, routed, rows)
 
 
