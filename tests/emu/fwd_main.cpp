@@ -290,6 +290,37 @@ int main(int argc, char **argv)
     uint64_t hsh = 1469598103934665603ull;   // FNV-1a of the output bytes
     for (size_t i = 0; i < (size_t)T * H * el; ++i) hsh = (hsh ^ ((const uint8_t *)out)[i]) * 1099511628211ull;
     printf("out hash %016llx\n", (unsigned long long)hsh);
+    // EMU_NOALLOC_SEQ=T2: the layer at T and then at T2 (the first T2 tokens)
+    // through the workspace forward and through the no-allocation forward on
+    // the shared static scratch, which keeps the previous call's contents:
+    // the outputs must agree bit for bit (every counter re-armed per call)
+    if (const char *sq = getenv("EMU_NOALLOC_SEQ")) {
+        const int64_t T2 = atoi(sq);
+        long bad = 0, zero = 0;
+        for (int64_t TT : {(int64_t)T, T2}) {
+            xs_moe_params q = p;
+            q.T = TT;
+            xs_moe_tensors tt = t;
+            tt.logits = nullptr; tt.topk_idx = nullptr; tt.topk_w = nullptr; tt.counts = nullptr;
+            tt.offsets = nullptr; tt.perm = nullptr; tt.inv = nullptr;
+            uint8_t *oa = (uint8_t *)emu_alloc((size_t)TT * H * el, "seq out a");
+            uint8_t *ob = (uint8_t *)emu_alloc((size_t)TT * H * el, "seq out b");
+            const size_t wsq = xs_moe_workspace_size(&q);
+            void *wq = emu_alloc(wsq, "seq workspace");
+            tt.out = oa;
+            bad += xs_moe_forward(&q, &tt, wq, wsq, nullptr) != 0;
+            tt.out = ob;
+            if (xs_moe_forward_noalloc(&q, &tt, nullptr)) {
+                printf("noalloc sequence: %s\n", xs_last_error());
+                ++bad;
+            }
+            bad += memcmp(oa, ob, (size_t)TT * H * el) != 0;
+            bool allz = true;
+            for (size_t i = 0; i < (size_t)TT * H * el; ++i) allz &= oa[i] == 0;
+            zero += allz;
+        }
+        printf("noalloc sequence mismatches %ld\n", bad + zero);
+    }
     printf("max-abs-rel %.4g\nerrors %ld\n", dmax / (amax > 0 ? amax : 1), (long)g_errors);
     return 0;
 }

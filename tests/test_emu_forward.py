@@ -126,6 +126,8 @@ def check_forward(rc, out, env, args, routed=None, tile_rows=None):
         # bf16: 2 codes.  f32: two orders of a sum of H positive squares
         # differ by at most about 2H ulps of the sum, and inv and y add a few
         assert int(re.search(r"norm max code diff (\d+)", out).group(1)) <= (2 * args[1] + 8 if args[9] else 2), out
+    if env.get("EMU_NOALLOC_SEQ"):
+        assert int(re.search(r"noalloc sequence mismatches (\d+)", out).group(1)) == 0, out
     pairs, tokens = map(int, re.search(r"exact pass logits (\d+) tokens (\d+)", out).groups())
     if env.get("XS_ROUTER_MARGIN"):
         assert (pairs, tokens) == (args[0] * args[3], args[0]), out

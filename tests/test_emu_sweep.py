@@ -9,6 +9,8 @@ kernel symbols of the built library):
 - the persistent stream-K MXFP4 GEMMs at 32- and 64-row tiles;
 - the approximate MFMA router's prefill (tile) kernel;
 - K longer than every LDS ring, so each GEMM family's in-loop refills run;
+- the no-allocation forward twice in a row, the second call smaller, on the
+  shared scratch (stream-K, fused combine, exact pass, MXFP4);
 - the routing kernels at each width (128, 256, 512 and 1024 experts), the
   one-launch decode routing and the prefill routing with its exact pass.
 
@@ -42,6 +44,17 @@ CASES = [
     ("tiled_deep_k_bm128", TILED, (256, 1024, 512, 8, 4, 223, 0, 0, 1, 0, 0, 0, 0, 0), 0, 128),
     ("mxfp4_stream_deep_k", {"XS_MOE_STREAM": "1"}, (64, 2048, 1024, 8, 4, 224, 1, 1, 1, 0, 0, 0, 0, 0), 1, 32),
     ("mfma_router_prefill_deep_k", {}, (300, 1024, 128, 8, 2, 225, 0, 0, 0, 0, 0, 0, 0, 0), None, None),
+    # the no-allocation forward at T and then at a smaller T on the shared
+    # scratch (which keeps the first call's contents) against the workspace
+    # forward: stream-K counters and partial tiles, the fused combine's
+    # counters, the certified router's list counters, MXFP4
+    ("noalloc_seq_stream", {"EMU_NOALLOC_SEQ": "40", "XS_MOE_GEMM": "tiled", "XS_MOE_STREAM": "1",
+                            "XS_STREAM_GROUPED": "0"}, (256, 512, 512, 64, 4, 230, 0, 1, 1, 0, 1.1, 0, 0, 0), 1, None),
+    ("noalloc_seq_fused_combine", {"EMU_NOALLOC_SEQ": "300", "XS_MOE_GEMM": "wide", "XS_FUSE_COMBINE": "1"},
+     (700, 256, 256, 16, 4, 231, 0, 1, 1, 0, 1.1, 0, 0, 0), 2, None),
+    ("noalloc_seq_exact_pass", {"EMU_NOALLOC_SEQ": "20", "XS_ROUTER_MARGIN": "1e30"},
+     (200, 512, 256, 32, 6, 232, 0, 1, 1, 0, 1.1, 0, 0, 0), None, None),
+    ("noalloc_seq_mxfp4", {"EMU_NOALLOC_SEQ": "48"}, (160, 512, 512, 16, 6, 233, 1, 1, 1, 0, 1.1, 0, 0, 0), None, None),
     # routing widths (64 experts per lane group): the one-launch decode routing
     # at 128, 256 and 512 experts; the prefill routing launches, with every
     # token through the exact pass (margin) so the second routing runs too
