@@ -17,6 +17,7 @@
 #include "hip_emu.hpp"
 #include <cmath>
 #include <random>
+#include <thread>
 
 #include "moe_oracle.h"
 #include "xs_moe.h"
@@ -75,16 +76,29 @@ int main(int argc, char **argv)
         w2 = (uint8_t *)emu_alloc((size_t)E * H * I, "w2");
         s2 = emu_alloc(4 * (size_t)E * (H / 128) * (I / 128), "s2");
     }
-    for (int e = 0; e < E; ++e) {
-        for (auto &v : w13f) v = 0.02f * nd(rng);
-        for (auto &v : w2f) v = 0.02f * nd(rng);
-        if (fp4) {
-            xo_quant_weight_mxfp4(w13f.data(), 2 * I, H, w13 + (size_t)e * 2 * I * H / 2, (uint8_t *)s13 + (size_t)e * 2 * I * H / 32);
-            xo_quant_weight_mxfp4(w2f.data(), H, I, w2 + (size_t)e * H * I / 2, (uint8_t *)s2 + (size_t)e * H * I / 32);
-        } else {
-            xo_quant_weight_fp8_block(w13f.data(), 2 * I, H, w13 + (size_t)e * 2 * I * H, (float *)s13 + (size_t)e * (2 * I / 128) * (H / 128));
-            xo_quant_weight_fp8_block(w2f.data(), H, I, w2 + (size_t)e * H * I, (float *)s2 + (size_t)e * (H / 128) * (I / 128));
-        }
+    // each expert from its own generator (seed, e), over 8 host threads: the
+    // same data however the experts are split (full-size layers take minutes
+    // on one thread)
+    {
+        std::vector<std::thread> gen;
+        for (int q = 0; q < 8; ++q)
+            gen.emplace_back([&, q] {
+                std::vector<float> a((size_t)2 * I * H), b((size_t)H * I);
+                std::normal_distribution<float> g(0.f, 1.f);
+                for (int e = q; e < E; e += 8) {
+                    std::mt19937 r((uint32_t)seed * 2654435761u + (uint32_t)e);
+                    for (auto &v : a) v = 0.02f * g(r);
+                    for (auto &v : b) v = 0.02f * g(r);
+                    if (fp4) {
+                        xo_quant_weight_mxfp4(a.data(), 2 * I, H, w13 + (size_t)e * 2 * I * H / 2, (uint8_t *)s13 + (size_t)e * 2 * I * H / 32);
+                        xo_quant_weight_mxfp4(b.data(), H, I, w2 + (size_t)e * H * I / 2, (uint8_t *)s2 + (size_t)e * H * I / 32);
+                    } else {
+                        xo_quant_weight_fp8_block(a.data(), 2 * I, H, w13 + (size_t)e * 2 * I * H, (float *)s13 + (size_t)e * (2 * I / 128) * (H / 128));
+                        xo_quant_weight_fp8_block(b.data(), H, I, w2 + (size_t)e * H * I, (float *)s2 + (size_t)e * (H / 128) * (I / 128));
+                    }
+                }
+            });
+        for (auto &t : gen) t.join();
     }
     uint8_t *sw13 = nullptr, *sw2 = nullptr;
     float *ss13 = nullptr, *ss2 = nullptr;

@@ -19,9 +19,10 @@ cover each GEMM family of the default dispatch: one-block-per-tile, the
 persistent stream-K kernels, the tall tiles with the separate and the fused
 combine, MXFP4 routed experts, the pre-norm with a residual, the
 no-allocation entry point, f32 inputs, E = 1024 with top-16, group-limited
-routing with scaling and no renormalisation, NaN / Inf tokens, and the
-weight-direct GEMMs behind XS_WEIGHT_DIRECT=1 (packed by the library's own
-packing kernels, with XS_EMU_FULL=1)."""
+routing with scaling and no renormalisation, NaN / Inf tokens, and, with
+XS_EMU_FULL=1, the weight-direct GEMMs behind XS_WEIGHT_DIRECT=1 (packed by
+the library's own packing kernels) and the layer at the V4-Flash shape
+(decode at 1, 16, 64 and 256 tokens, MXFP4 at 64)."""
 import os
 import re
 import subprocess
@@ -78,6 +79,17 @@ FULL_CASES = [
     ("wd_prefill", {"XS_WEIGHT_DIRECT": "1"}, (300, 1024, 512, 4, 2, 22, 0, 1, 1, 0, 1.1, 0, 0, 0, 1), 3),
     ("wd_mxfp4", {"XS_WEIGHT_DIRECT": "1"}, (160, 1024, 512, 16, 6, 23, 1, 1, 1, 0, 0, 0, 0, 0, 1), 5),
     ("wd_mxfp4_packed_only", {"XS_WEIGHT_DIRECT": "1"}, (100, 1024, 512, 16, 6, 25, 1, 1, 1, 0, 0, 0, 0, 0, 2), 5),
+]
+# the layer at the V4-Flash shape (H 4096, I 2048, 256 experts, top-6 and the
+# shared expert): decode batches of configs[3] on their real kernels and K
+# lengths, and MXFP4 routed experts (configs[4]'s layer) at 64 tokens; one to
+# four minutes of CPU each
+FULL_CASES += [
+    ("v4flash_decode_t1", {}, (1, 4096, 2048, 256, 6, 42, 0, 1, 1, 0, 0, 0, 0, 0), 1),
+    ("v4flash_decode_t16", {}, (16, 4096, 2048, 256, 6, 41, 0, 1, 1, 0, 0, 0, 0, 0), 1),
+    ("v4flash_decode_t64", {}, (64, 4096, 2048, 256, 6, 43, 0, 1, 1, 0, 0, 0, 0, 0), 1),
+    ("v4flash_decode_t256", {}, (256, 4096, 2048, 256, 6, 44, 0, 1, 1, 0, 1.1, 0, 0, 0), 1),
+    ("v4flash_mxfp4_t64", {}, (64, 4096, 2048, 256, 6, 45, 1, 1, 1, 0, 0, 0, 0, 0), 1),
 ]
 if os.environ.get("XS_EMU_FULL") == "1":
     CASES += FULL_CASES
