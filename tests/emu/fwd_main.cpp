@@ -163,6 +163,13 @@ int main(int argc, char **argv)
         }
         if (frag == 2) t.w13 = t.w2 = t.shared_w13 = t.shared_w2 = nullptr;
     }
+    if (T == 0) {
+        // an empty batch: both forwards succeed without a workspace and launch
+        // nothing (xs_moe_plan refuses T = 0: there is nothing to plan)
+        int r1 = xs_moe_forward(&p, &t, nullptr, 0, nullptr), r2 = xs_moe_forward_noalloc(&p, &t, nullptr);
+        printf("empty batch forward %d noalloc %d\nerrors %ld\n", r1, r2, (long)g_errors);
+        return 0;
+    }
     xs_moe_plan_t pl;
     if (xs_moe_plan(&p, &t, &pl)) { printf("plan failed: %s\n", xs_last_error()); return 1; }
     printf("plan tile_rows %d routed %d shared %d fused %d\n", pl.tile_rows, pl.routed_gemm, pl.shared_gemm, pl.fused_combine);
