@@ -236,7 +236,7 @@ int main(int argc, char **argv)
     } else {
         memcpy(xin.data(), x, xin.size());
     }
-    xo_moe_cfg cfg = {T, H, I, E, k, ng, tg, renorm, scaling, xf32 ? 0 : 1, fp4, shared, 1};
+    xo_moe_cfg cfg = {T, H, I, E, k, ng, tg, renorm, scaling, xf32 ? 0 : 1, fp4, shared, 8};   // 8 OpenMP threads
     xo_moe_inputs in = {xin.data(), wr, bias, lg, w13, s13, w2, s2, sw13, ss13, sw2, ss2};
     std::vector<int32_t> ridx((size_t)T * k), rc_((size_t)E), ro((size_t)E + 1), rp((size_t)T * k), ri((size_t)T * k);
     std::vector<float> rw((size_t)T * k), rout((size_t)T * H);

@@ -91,8 +91,17 @@ FULL_CASES += [
     ("v4flash_decode_t256", {}, (256, 4096, 2048, 256, 6, 44, 0, 1, 1, 0, 1.1, 0, 0, 0), 1),
     ("v4flash_mxfp4_t64", {}, (64, 4096, 2048, 256, 6, 45, 1, 1, 1, 0, 0, 0, 0, 0), 1),
 ]
+# prefill at the V4-Flash shape on the tall tiles (1400 tokens, Zipf(1.1)
+# routing as configs[2]) and configs[4] itself (MXFP4, 2048 tokens): about 10
+# and 20 minutes of CPU, with XS_EMU_HUGE=1
+HUGE_CASES = [
+    ("v4flash_prefill_t1400", {}, (1400, 4096, 2048, 256, 6, 46, 0, 1, 1, 0, 1.1, 0, 0, 0), 2),
+    ("v4flash_mxfp4_t2048", {}, (2048, 4096, 2048, 256, 6, 47, 1, 1, 1, 0, 1.1, 0, 0, 0), 1),
+]
 if os.environ.get("XS_EMU_FULL") == "1":
     CASES += FULL_CASES
+if os.environ.get("XS_EMU_HUGE") == "1":
+    CASES += HUGE_CASES
 
 
 def run_forward(exe, env, args):
@@ -155,6 +164,15 @@ def run_all(exe, cases, workers=4):
     with ThreadPoolExecutor(workers) as ex:
         futs = {c[0]: ex.submit(run_forward, exe, c[1], c[2]) for c in cases}
         return {n: f.result() for n, f in futs.items()}
+
+
+def test_empty_batch_emulated(fwd_emu, tmp_path):
+    """T = 0: xs_moe_forward and xs_moe_forward_noalloc return XS_OK with no
+    workspace and launch nothing (the emulator's launch log stays empty)."""
+    log = tmp_path / "launches.txt"
+    rc, out = run_forward(fwd_emu, {"EMU_KERNEL_LOG": str(log)}, (0, 256, 128, 8, 2, 5, 0, 1, 1, 0, 0, 0, 0, 0))
+    assert rc == 0 and "empty batch forward 0 noalloc 0" in out and re.search(r"^errors 0$", out, re.M), out
+    assert not log.exists() or log.read_text() == "", log.read_text()
 
 
 @pytest.fixture(scope="module")
