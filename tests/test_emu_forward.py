@@ -92,11 +92,13 @@ FULL_CASES += [
     ("v4flash_mxfp4_t64", {}, (64, 4096, 2048, 256, 6, 45, 1, 1, 1, 0, 0, 0, 0, 0), 1),
 ]
 # prefill at the V4-Flash shape on the tall tiles (1400 tokens, Zipf(1.1)
-# routing as configs[2]) and configs[4] itself (MXFP4, 2048 tokens): about 10
-# and 20 minutes of CPU, with XS_EMU_HUGE=1
+# routing as configs[2]), configs[4] itself (MXFP4, 2048 tokens) and
+# configs[2] itself (8192 tokens): about 10, 20 and 35 minutes of CPU, with
+# XS_EMU_HUGE=1
 HUGE_CASES = [
     ("v4flash_prefill_t1400", {}, (1400, 4096, 2048, 256, 6, 46, 0, 1, 1, 0, 1.1, 0, 0, 0), 2),
     ("v4flash_mxfp4_t2048", {}, (2048, 4096, 2048, 256, 6, 47, 1, 1, 1, 0, 1.1, 0, 0, 0), 1),
+    ("v4flash_prefill_t8192", {}, (8192, 4096, 2048, 256, 6, 48, 0, 1, 1, 0, 1.1, 0, 0, 0), 2),
 ]
 if os.environ.get("XS_EMU_FULL") == "1":
     CASES += FULL_CASES
