@@ -90,6 +90,9 @@ FULL_CASES += [
     ("v4flash_decode_t64", {}, (64, 4096, 2048, 256, 6, 43, 0, 1, 1, 0, 0, 0, 0, 0), 1),
     ("v4flash_decode_t256", {}, (256, 4096, 2048, 256, 6, 44, 0, 1, 1, 0, 1.1, 0, 0, 0), 1),
     ("v4flash_mxfp4_t64", {}, (64, 4096, 2048, 256, 6, 45, 1, 1, 1, 0, 0, 0, 0, 0), 1),
+    # the weight-direct GEMMs (opt-in) on packed-only layers at this shape
+    ("v4flash_wd_decode_t16", {"XS_WEIGHT_DIRECT": "1"}, (16, 4096, 2048, 256, 6, 51, 0, 1, 1, 0, 0, 0, 0, 0, 2), 4),
+    ("v4flash_wd_mxfp4_t64", {"XS_WEIGHT_DIRECT": "1"}, (64, 4096, 2048, 256, 6, 52, 1, 1, 1, 0, 0, 0, 0, 0, 2), 5),
 ]
 # prefill at the V4-Flash shape on the tall tiles (1400 tokens, Zipf(1.1)
 # routing as configs[2]), configs[4] itself (MXFP4, 2048 tokens) and
@@ -99,6 +102,8 @@ HUGE_CASES = [
     ("v4flash_prefill_t1400", {}, (1400, 4096, 2048, 256, 6, 46, 0, 1, 1, 0, 1.1, 0, 0, 0), 2),
     ("v4flash_mxfp4_t2048", {}, (2048, 4096, 2048, 256, 6, 47, 1, 1, 1, 0, 1.1, 0, 0, 0), 1),
     ("v4flash_prefill_t8192", {}, (8192, 4096, 2048, 256, 6, 48, 0, 1, 1, 0, 1.1, 0, 0, 0), 2),
+    ("v4flash_wd_prefill_t1400", {"XS_WEIGHT_DIRECT": "1"}, (1400, 4096, 2048, 256, 6, 53, 0, 1, 1, 0, 1.1, 0, 0, 0, 1),
+     3),
 ]
 if os.environ.get("XS_EMU_FULL") == "1":
     CASES += FULL_CASES
