@@ -1,9 +1,9 @@
 """Randomised host emulation (opt-in: XS_EMU_FUZZ=N runs N cases of each
 kind, XS_EMU_FUZZ_SEED picks the campaign).  Each case draws a shape, router,
 routing options (group-limited, scaling, renormalisation), dtype, expert
-format, pre-norm, residual, entry point, dispatch switches, NaN / Inf tokens
-and (a quarter of the cases) fragment-packed weights on the weight-direct
-GEMMs, runs the whole
+format, pre-norm, residual, entry point, dispatch switches, NaN / Inf tokens,
+the no-allocation forward twice in a row, and (a quarter of the cases)
+fragment-packed weights on the weight-direct GEMMs.  It runs the whole
 forward through the library's C ABI on the emulator (tests/emu/fwd_main.cpp)
 or the certified router alone (tests/emu/router_main.cpp, with one of the
 six MFMA summation models), and applies the same checks as the fixed cases:
@@ -69,6 +69,8 @@ def _forward_case(exe, i):
         env.pop("EMU_ROUTE", None)
     if T * k * H * I > 300 * 8 * 1024 * 512:
         T = 64
+    if T > 1 and r.random() < 0.15:   # the no-allocation forward twice, the second call smaller
+        env["EMU_NOALLOC_SEQ"] = str(r.randint(1, T - 1))
     args = [T, H, I, E, k, r.randint(1, 10**6), int(fp4), shared, router, int(xf32), r.choice([0, 0, 1.1]),
             int(norm), int(resid), int(r.random() < 0.15), frag]
     if shared and r.random() < 0.2:
@@ -96,6 +98,10 @@ def _forward_case(exe, i):
     m = re.search(r"max-abs-rel (\S+)", out)
     if not m or float(m.group(1)) > 2e-2:
         bad.append("output")
+    if "EMU_NOALLOC_SEQ" in env:
+        m = re.search(r"noalloc sequence mismatches (\d+)", out)
+        if not m or int(m.group(1)):
+            bad.append("noalloc sequence")
     if norm:
         m = re.search(r"norm max code diff (\d+)", out)
         if not m or int(m.group(1)) > (2 * H + 8 if xf32 else 2):
