@@ -109,6 +109,10 @@ if os.environ.get("XS_EMU_FULL") == "1":
     CASES += FULL_CASES
 if os.environ.get("XS_EMU_HUGE") == "1":
     CASES += HUGE_CASES
+if os.environ.get("XS_EMU_FULL") == "1" or os.environ.get("XS_EMU_HUGE") == "1":
+    # every case runs in the first test's setup (forward_runs): beyond the
+    # default per-test limit with the full-size cases
+    pytestmark = pytest.mark.timeout(4 * 3600)
 
 
 def run_forward(exe, env, args):

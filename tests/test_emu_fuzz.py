@@ -23,7 +23,9 @@ from test_emu_router import router_emu  # noqa: F401  (fixture)
 
 N = int(os.environ.get("XS_EMU_FUZZ", "0"))
 SEED = int(os.environ.get("XS_EMU_FUZZ_SEED", "1"))
-pytestmark = pytest.mark.skipif(N <= 0, reason="randomised emulation: set XS_EMU_FUZZ=N")
+# a campaign runs in one test: about 10 s of CPU per forward case
+pytestmark = [pytest.mark.skipif(N <= 0, reason="randomised emulation: set XS_EMU_FUZZ=N"),
+              pytest.mark.timeout(max(1200, 30 * N))]
 
 
 def _groups(r, E, k):
